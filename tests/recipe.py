@@ -1,0 +1,77 @@
+"""Portable, seeded input recipes for parity tests and golden fixtures.
+
+Every input is drawn from a SplitMix64 stream (Steele, Lea & Flood, "Fast splittable pseudorandom number
+generators", OOPSLA 2014) written in numpy uint64 arithmetic, so the same seed gives the same bytes on any
+machine and any numpy/torch version. The distributions mirror the reference's test generators
+(`jatai_cuda/teste_ops.py:18-31`: `bloco` and `cru`), re-stated with this stream instead of torch's RNG.
+"""
+import hashlib
+
+import numpy as np
+
+E_ZERO = -127
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def splitmix64(seed, n):
+    """n consecutive SplitMix64 outputs (uint64) for a given seed."""
+    idx = np.arange(1, n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + idx * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return z
+
+
+def substream(seed, tag):
+    """Derive an independent seed from (seed, tag) via SHA-256 (tag: str)."""
+    h = hashlib.sha256(f"{seed}:{tag}".encode()).digest()
+    return int.from_bytes(h[:8], "little")
+
+
+def uniform_int(seed, shape, lo, hi):
+    """Integers uniform in [lo, hi] (inclusive), int64."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    x = splitmix64(seed, n) >> np.uint64(11)
+    span = np.uint64(hi - lo + 1)
+    return (x % span).astype(np.int64).reshape(shape) + lo
+
+
+def uniform01(seed, shape):
+    n = int(np.prod(shape)) if len(shape) else 1
+    x = splitmix64(seed, n) >> np.uint64(11)
+    return (x.astype(np.float64) / float(1 << 53)).reshape(shape)
+
+
+def bloco(seed, R, C, blk, espalha=4, zera=0.0, e0=-10, mmax=127):
+    """Block tensor (m int8 [R,C], E int8 [R,C/blk]): mantissas uniform in [-mmax, mmax], exponents e0 +
+    uniform[-espalha, espalha], and each block zeroed (m = 0, E = -127) with probability `zera`.
+    Same distribution as `bloco()` in jatai_cuda/teste_ops.py:18-25."""
+    m = uniform_int(substream(seed, "m"), (R, C), -mmax, mmax).astype(np.int8)
+    E = (e0 + uniform_int(substream(seed, "E"), (R, C // blk), -espalha, espalha)).astype(np.int8)
+    if zera:
+        z = uniform01(substream(seed, "z"), (R, C // blk)) < zera
+        m = m.reshape(R, C // blk, blk)
+        m[z] = 0
+        m = m.reshape(R, C)
+        E[z] = E_ZERO
+    return np.ascontiguousarray(m), np.ascontiguousarray(E)
+
+
+def cru(seed, R, C, bits=24, e0=-30):
+    """Raw tensor (acc int32 [R,C], e int16 [R,C]): acc uniform in [-2^bits, 2^bits - 1], e = e0 + uniform[-3, 3].
+    Same distribution as `cru()` in jatai_cuda/teste_ops.py:28-31."""
+    acc = uniform_int(substream(seed, "acc"), (R, C), -(1 << bits), (1 << bits) - 1).astype(np.int32)
+    e = (e0 + uniform_int(substream(seed, "e"), (R, C), -3, 3)).astype(np.int16)
+    return np.ascontiguousarray(acc), np.ascontiguousarray(e)
+
+
+def tokens(seed, n, V):
+    return uniform_int(seed, (n,), 0, V - 1).astype(np.int32)
+
+
+def sha(a):
+    """SHA-256 of an array's C-contiguous little-endian bytes (dtype fixed by the caller)."""
+    a = np.ascontiguousarray(a)
+    return hashlib.sha256(a.tobytes()).hexdigest()

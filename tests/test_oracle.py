@@ -1,0 +1,173 @@
+"""Pins the CPU oracle (oracle/jatai_oracle.cpp) before anything is compared against it.
+
+Checks, per function:
+  * reference golden vectors written from the spec `OpsRef` (tests/golden/*.json, see make_golden.py):
+    every op case at BLK 128 and 32, config 1, primitive tables, two full training steps;
+  * closed forms that a plausible mistake would break: bitlen = int.bit_length, rnd = exact round-half-even
+    (Fraction), isqrt = floor sqrt for n >= 1, the GEMM's equal-exponent case = integer matmul + quant, split
+    invariance of the raw GEMM, the R16 round trip.
+"""
+import json
+import math
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import cases as CS
+import recipe as R
+from oracle.ops_oracle import OpsOraculo, g_rms
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _gold(nome):
+    return json.load(open(os.path.join(GOLD, nome)))
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+class BE:
+    def __init__(self, blk):
+        self.ops = OpsOraculo(blk)
+
+    def dev(self, a):
+        return torch.from_numpy(np.ascontiguousarray(a))
+
+    def limite(self, flag):
+        old, self.ops.limite = self.ops.limite, flag
+        return old
+
+
+# ---------------------------------------------------------------- primitives
+def test_primitives_vs_golden():
+    g = _gold("primitives.json")
+    d = np.arange(0, 7001, dtype=np.int64)
+    assert R.sha(OpsOraculo.prim("exp_int", d)) == g["exp_int"]["sha"]
+    n = np.concatenate([np.arange(0, 70000), R.uniform_int(7, (200000,), 0, (1 << 30) - 1)]).astype(np.int64)
+    assert R.sha(OpsOraculo.prim("isqrt", n)) == g["isqrt"]["sha"]
+    x = R.uniform_int(8, (100000,), -(1 << 29), (1 << 29) - 1)
+    s = R.uniform_int(9, (100000,), -8, 40)
+    assert R.sha(OpsOraculo.prim("rnd", x, s)) == g["rnd"]["sha"]
+    assert R.sha(OpsOraculo.prim("bitlen", x)) == g["bitlen"]["sha"]
+
+
+def test_primitives_closed_forms():
+    x = R.uniform_int(11, (3000,), -(1 << 40), 1 << 40)
+    s = R.uniform_int(12, (3000,), -10, 50)
+    x[:50] = 0
+    bl = OpsOraculo.prim("bitlen", x)
+    assert all(int(b) == abs(int(v)).bit_length() for v, b in zip(x, bl))
+    x2 = x.copy()
+    x2[(s < 0)] = x2[(s < 0)] >> 12                      # left shifts stay in int64
+    rn = OpsOraculo.prim("rnd", x2, s)
+    for v, sh, r in zip(x2, s, rn):
+        v, sh = int(v), int(sh)
+        if sh <= 0:
+            assert int(r) == v << -sh
+            continue
+        q = Fraction(v, 1 << sh)
+        f = math.floor(q)
+        exp = f + 1 if q - f > Fraction(1, 2) else f if q - f < Fraction(1, 2) else (f if f % 2 == 0 else f + 1)
+        assert int(r) == exp, (v, sh, int(r), exp)
+    n = np.concatenate([np.arange(1, 5000), R.uniform_int(13, (5000,), 1, (1 << 30) - 1)]).astype(np.int64)
+    iq = OpsOraculo.prim("isqrt", n)
+    assert all(int(q) == math.isqrt(int(v)) for v, q in zip(n, iq))
+    # exp_int(0) is 1.0 in Q15 within the polynomial's error; monotone non-increasing over its domain
+    ex = OpsOraculo.prim("exp_int", np.arange(0, 7001))
+    assert abs(int(ex[0]) - 32768) <= 8 and np.all(np.diff(ex) <= 0) and int(ex[-1]) == 0
+    ref = np.exp(-np.arange(0, 6001) / 256.0) * 32768
+    assert np.max(np.abs(ex[:6001] - ref)) < 8
+
+
+def test_g_rms():
+    # ops.py:28-30 at BLK 128 (reference shapes) and the values the BLK=32 extension uses
+    assert g_rms(256, 128) == (6, 6)
+    assert g_rms(512, 32) == (4, 5)
+
+
+# ---------------------------------------------------------------- op cases vs the reference spec
+@pytest.mark.parametrize("blk", [128, 32])
+def test_ops_vs_golden(blk):
+    gold = _gold(f"ops_blk{blk}.json")
+    be = BE(blk)
+    casos = CS.casos()
+    assert [c["nome"] for c in gold] == [n for n, _ in casos]
+    falhas = []
+    for i, ((nome, fn), gc) in enumerate(zip(casos, gold)):
+        rec = CS.Gravador(be.ops, host)
+        g = CS.Gen(R.substream(1000 + i, nome), blk, be.dev)
+        fn(rec, g, be)
+        if [list(x) for x in rec.log] != [list(x) for x in gc["chamadas"]]:
+            falhas.append(nome)
+    assert not falhas, f"oracle differs from the spec at BLK={blk}: {falhas}"
+
+
+def test_config1_vs_golden():
+    gold = _gold("config1.json")
+    for blk in (32, 128):
+        ops = OpsOraculo(blk)
+        A = tuple(torch.from_numpy(x) for x in R.bloco(R.substream(0, "A"), 512, 512, blk, espalha=4, e0=-4))
+        B = tuple(torch.from_numpy(x) for x in R.bloco(R.substream(0, "B"), 512, 512, blk, espalha=4, e0=-4))
+        assert [R.sha(host(t)) for t in ops.gemm(A, B)] == gold[str(blk)]["bloco"]
+        assert [R.sha(host(t)) for t in ops.gemm(A, B, cru=True)] == gold[str(blk)]["cru"]
+
+
+# ---------------------------------------------------------------- GEMM closed form and invariants
+@pytest.mark.parametrize("blk", [32, 128])
+def test_gemm_equal_exponents_is_integer_matmul(blk):
+    """With every exponent of A's rows and B's rows equal, all alignment shifts are 0 and the raw output is
+    16 * (A.B^T) exactly with exponent RA + RB - 4 (the textbook integer matmul)."""
+    M, N, K = 64, 96, 4 * blk
+    a = R.uniform_int(21, (M, K), -127, 127).astype(np.int8)
+    b = R.uniform_int(22, (N, K), -127, 127).astype(np.int8)
+    ea = np.full((M, K // blk), -9, np.int8)
+    eb = np.full((N, K // blk), -5, np.int8)
+    ops = OpsOraculo(blk)
+    acc, e = ops.gemm((torch.from_numpy(a), torch.from_numpy(ea)), (torch.from_numpy(b), torch.from_numpy(eb)), cru=True)
+    ref = 16 * (a.astype(np.int64) @ b.astype(np.int64).T)
+    assert np.array_equal(host(acc).astype(np.int64), ref)
+    assert np.all(host(e) == -9 - 5 - 4)
+
+
+def test_gemm_raw_split_invariance():
+    """The raw output over K equals the sum of raw outputs over K halves when RA/RB are held fixed: the spec's
+    per-block rounding makes the sum over K-blocks associative (the split-K argument)."""
+    blk, M, N, K = 32, 32, 48, 256
+    A = R.bloco(31, M, K, blk, espalha=6)
+    B = R.bloco(32, N, K, blk, espalha=6)
+    ops = OpsOraculo(blk)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    full = host(ops.gemm((t(A[0]), t(A[1])), (t(B[0]), t(B[1])), cru=True)[0]).astype(np.int64)
+    # pin each half's row maxima to the full-K maxima by appending one all-zero block carrying that maximum
+    parts = 0
+    for h in range(2):
+        sl = slice(h * K // 2, (h + 1) * K // 2)
+        bs = slice(h * K // 2 // blk, (h + 1) * K // 2 // blk)
+        am = np.concatenate([A[0][:, sl], np.zeros((M, blk), np.int8)], 1)
+        ae = np.concatenate([A[1][:, bs], A[1].max(1, keepdims=True)], 1)
+        bm = np.concatenate([B[0][:, sl], np.zeros((N, blk), np.int8)], 1)
+        be_ = np.concatenate([B[1][:, bs], B[1].max(1, keepdims=True)], 1)
+        parts = parts + host(ops.gemm((t(am), t(ae)), (t(bm), t(be_)), cru=True)[0]).astype(np.int64)
+    assert np.array_equal(full, parts)
+
+
+def test_r16_round_trip_and_sum():
+    """para8(para16(x)) == x exactly, and soma16 is closer to the exact float64 sum than soma
+    (the reference's own check, jatai_cuda/teste_res16.py:27-46)."""
+    blk = 128
+    ops = OpsOraculo(blk)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    x = tuple(t(v) for v in R.bloco(41, 256, 512, blk, espalha=7, e0=-3))
+    back = ops.para8(ops.para16(x))
+    deq = lambda m, E: host(m).astype(np.float64) * np.exp2(np.repeat(host(E).astype(np.float64), blk, 1))
+    assert np.array_equal(deq(*back), deq(*x))
+    y = tuple(t(v) for v in R.bloco(42, 256, 512, blk, espalha=7, e0=-15))
+    exato = deq(*x) + deq(*y)
+    e16 = np.linalg.norm(deq(*ops.soma16(ops.para16(x), y)) - exato)
+    e8 = np.linalg.norm(deq(*ops.soma(x, y)) - exato)
+    assert e16 < e8 / 8          # 15-bit vs 7-bit mantissas; measured ratio ~16 at a 2^-12 addend
