@@ -1,0 +1,78 @@
+/* libjatai.so -- C ABI of the Jatai INT8 training hot path on MI355X (gfx950).
+ *
+ * Drop-in for the reference library's C interface (jatai_cuda/jatai_cuda.cu:1061-1201), bound from Python by
+ * ctypes exactly as the reference binds libjatai.so (jatai_cuda/ops.py:297-310). Conventions, as in the reference:
+ *   - the caller allocates every output; the library never allocates device memory;
+ *   - pointers are raw device addresses; an absent operand is NULL;
+ *   - block tensors are (int8 mantissas [R, C], int8 exponents [R, C/BLK]); raw tensors (int32 acc [R, C],
+ *     int16 exponents [R, C]); R16 tensors (int16 mantissas [R, C], int8 exponents [R, C/BLK]);
+ *   - element counts are long long; every launch takes a trailing launch id `kid`, recorded by device sentinels;
+ *   - the return value is a hipError_t code (0 = success); launches are asynchronous on the stream set by
+ *     jt_stream (NULL = default stream);
+ *   - module state (stream, block size, knobs) is global: not thread-safe, one host thread drives the library.
+ * BLK (32 or 128) is chosen with jt_bloco; the reference fixes BLK = 128 (jatai_cuda.cu:16).
+ */
+#ifndef JATAI_H
+#define JATAI_H
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device error record and stream (jatai_cuda.cu:1062-1073, 1088) */
+int jt_erro_le(long long* out);        /* out[6] = {n, code, kid, idx, value, aux}; returns n, or -hipError */
+int jt_erro_limpa(void);               /* clears the record */
+int jt_sincroniza(void);               /* hipDeviceSynchronize */
+void jt_stream(void* stream);          /* every later launch goes to this hipStream_t (graph capture) */
+
+/* ---- tuning knobs (jatai_cuda.cu:1087-1091) */
+void jt_gemm_split(int alvo_wg);       /* split-K target workgroup count for raw GEMM outputs */
+void jt_gemm_bm(int bm);               /* accepted; the MFMA GEMM has a single tile shape */
+void jt_atencao_linhas(int n);         /* accepted; attention runs one query row per thread */
+int jt_res_estocastico(int ligado);    /* 0 ok when off; stochastic residual rounding returns hipErrorNotSupported */
+
+/* ---- block size: no reference counterpart (the reference fixes 128) */
+int jt_bloco(int blk);                 /* 32 or 128; hipErrorInvalidValue otherwise */
+int jt_bloco_atual(void);
+
+/* ---- GEMM C = A . B^T, A [M,K], B [N,K] blocked along K (jatai_cuda.cu:1093-1127)
+ * modo 0: block C (Cm, CE) | 1: raw C (C32, Ce), split-K over K-blocks | 2: Cm = soma(X, A.B^T)
+ * 3: Cm = h = A.B^T and Om2 = relu2(h) | 4: Cm = relu2_back(A.B^T, X)
+ * Requires M % 32 == 0, N % 128 == 0, K % BLK == 0, K <= 4096 (the reference: M % 64, N % 128, K % 128). */
+int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
+              const void* Xm, const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid);
+int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
+            int M, int N, int K, int modo, int kid);
+
+/* ---- element-wise, nblocos = elements / BLK (jatai_cuda.cu:1128-1154, 1074-1086) */
+int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid);
+int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);
+int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nblocos, int kid);
+int jt_relu2_back(const void* gm, const void* gE, const void* hm, const void* hE, void* om, void* oE, long long nblocos, int kid);
+int jt_momento(const void* gacc, const void* ge, void* Mm, void* ME, long long nblocos, int kid);                 /* in place */
+int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* RE, int k_lr, int ef, long long nblocos,
+            int kid);                                                                                          /* in place */
+int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblocos, int kid);
+int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nblocos, int kid);
+int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);
+
+/* ---- re-blocking, gathers (jatai_cuda.cu:1155-1166). transpoe: R % 128 == 0, C % 64 == 0. */
+int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid);
+int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid);
+int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid);
+
+/* ---- rows, D and V in {128, 256, 512, 1024} (jatai_cuda.cu:1167-1176, 1195-1200) */
+int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid);
+int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om,
+                void* oE, int M, int D, int log2D, int G, int GB, int kid);
+int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V,
+                  int log2M, int kid);
+
+/* ---- causal ALiBi attention, T % 64 == 0, T <= 256 (jatai_cuda.cu:1177-1194) */
+int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid);
+int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge,
+                    int Bt, int T, int H, int D, int GA, int limite, int kid);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

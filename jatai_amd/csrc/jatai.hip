@@ -1,0 +1,273 @@
+// libjatai.so for MI355X (gfx950): the C ABI of the Jatai INT8 training hot path.
+//
+// Entry points keep the reference's names, argument order, pointer/size conventions and return codes
+// (jatai_cuda/jatai_cuda.cu:1061-1201; declared in include/jatai.h): the caller allocates every output, pointers
+// are raw device addresses (NULL for an absent operand), element counts are long long, every launch carries a
+// trailing launch id `kid`, and the return value is the runtime's error code (0 = success). All launches go to
+// the stream set with jt_stream (torch's current, possibly capturing, stream). Like the reference, the module
+// state (stream, block size, tuning knobs) is global and not thread-safe.
+//
+// One translation unit: the kernels and the device error record `g_erro` live in the same code object.
+#include "jt_comum.h"
+#include "jt_elem.hip"
+#include "jt_linhas.hip"
+#include "jt_gemm.hip"
+#include "jt_atencao.hip"
+
+__device__ Erro g_erro;
+__device__ __noinline__ void reporta(int codigo, int kid, long long idx, long long valor, long long aux) {
+    if (atomicAdd(&g_erro.n, 1) == 0) {
+        g_erro.codigo = codigo;
+        g_erro.kid = kid;
+        g_erro.idx = idx;
+        g_erro.valor = valor;
+        g_erro.aux = aux;
+        __threadfence();
+    }
+}
+
+static hipStream_t g_stream = 0;
+static int g_blk = 128;                 // block size of every tensor: 32 or 128
+static int g_alvo_wg = 1024;            // split-K target number of workgroups (raw GEMM output)
+static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
+
+static int fim() { return (int)hipGetLastError(); }
+static unsigned grade_elem(long long nblocos) { return (unsigned)((nblocos * g_blk + 2047) / 2048); }
+static int ilog2(long long n) { int l = 0; while ((2LL << l) <= n) l++; return l; }
+
+#define POR_BLK(CHAMADA) (g_blk == 32 ? (CHAMADA(32)) : (CHAMADA(128)))
+
+extern "C" {
+
+// ---------------------------------------------------------------------------------------------- state
+int jt_erro_le(long long* out) {
+    Erro e;
+    hipError_t c = hipMemcpyFromSymbol(&e, HIP_SYMBOL(g_erro), sizeof(Erro), 0, hipMemcpyDeviceToHost);
+    if (c != hipSuccess) return -(int)c;
+    out[0] = e.n; out[1] = e.codigo; out[2] = e.kid; out[3] = e.idx; out[4] = e.valor; out[5] = e.aux;
+    return e.n;
+}
+int jt_erro_limpa() {
+    Erro e = {};
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_erro), &e, sizeof(Erro), 0, hipMemcpyHostToDevice);
+}
+int jt_sincroniza() { return (int)hipDeviceSynchronize(); }
+void jt_stream(void* st) { g_stream = (hipStream_t)st; }
+void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 1; }
+void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one tile shape; kept for the interface
+void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
+int jt_res_estocastico(int ligado) { return ligado ? (int)hipErrorNotSupported : 0; }
+// No reference counterpart: the reference fixes BLK = 128 (jatai_cuda.cu:16).
+int jt_bloco(int blk) {
+    if (blk != 32 && blk != 128) return (int)hipErrorInvalidValue;
+    g_blk = blk;
+    return 0;
+}
+int jt_bloco_atual() { return g_blk; }
+
+// ---------------------------------------------------------------------------------------------- GEMM
+int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
+              const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
+    using namespace gemm;
+    if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
+    const int nb = K / g_blk;
+    int partes = 1;
+    const long long tiles = (long long)(M / BM) * (N / BN);
+    if (modo == 1)
+        while (partes * 2 <= nb && nb % (partes * 2) == 0 && tiles * partes * 2 <= g_alvo_wg) partes *= 2;
+    if (partes > 1) {
+        const long long n = (long long)M * N;
+        k_zera32<<<(unsigned)((n / 4 + 255) / 256 + 1), 256, 0, g_stream>>>((int*)C32, n);
+    }
+    const dim3 grade(N / BN, M / BM, partes);
+    const size_t lds = gemm_lds(nb);
+    const int kpart = nb / partes;
+#define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
+             (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kpart, kid
+#define L(BL, MD) k_gemm<BL, MD><<<grade, NT, lds, g_stream>>>(ARGS)
+#define LB(MD) (g_blk == 32 ? L(32, MD) : L(128, MD))
+    switch (modo) {
+        case 0: LB(0); break;
+        case 1: LB(1); break;
+        case 2: LB(2); break;
+        case 3: LB(3); break;
+        case 4: LB(4); break;
+    }
+#undef LB
+#undef L
+#undef ARGS
+    return fim();
+}
+int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, int M, int N, int K,
+            int modo, int kid) {
+    return jt_gemm_f(A, EA, B, EB, Cm, CE, C32, Ce, nullptr, nullptr, nullptr, nullptr, M, N, K, modo, kid);
+}
+
+// ---------------------------------------------------------------------------------------------- element-wise
+int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_quant<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (int8_t*)m, (int8_t*)E, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_soma<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
+                                                                      (int8_t*)zm, (int8_t*)zE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_relu2<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)hm, (const int8_t*)hE, (int8_t*)am, (int8_t*)aE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_relu2_back(const void* gm, const void* gE, const void* hm, const void* hE, void* om, void* oE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_relu2_back<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)hm, \
+                                                                            (const int8_t*)hE, (int8_t*)om, (int8_t*)oE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_momento(const void* gacc, const void* ge, void* Mm, void* ME, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_momento<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int*)gacc, (const int16_t*)ge, (int8_t*)Mm, (int8_t*)ME, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* RE, int k_lr, int ef, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_peso<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((int8_t*)Wm, (int8_t*)WE, (const int8_t*)Mm, (const int8_t*)ME, (int8_t*)Rm, \
+                                                                      (int8_t*)RE, k_lr, ef, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_para16<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (int16_t*)zm, (int8_t*)zE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_para8<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int16_t*)xm, (const int8_t*)xE, (int8_t*)ym, (int8_t*)yE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid) {
+    if (nblocos <= 0) return 0;
+#define C(BL) (k_soma16<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int16_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
+                                                                        (int16_t*)zm, (int8_t*)zE, nblocos, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid) {
+    if (R <= 0 || C <= 0 || R % 128 || C % 64 || C % g_blk) return (int)hipErrorInvalidValue;
+#define L(BL) (k_transpoe<BL><<<dim3(C / 64, R / 128), 256, 0, g_stream>>>((const int8_t*)X, (const int8_t*)EX, (int8_t*)Y, (int8_t*)EY, R, C, kid), 0)
+    POR_BLK(L);
+#undef L
+    return fim();
+}
+int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid) {
+    if (M <= 0 || D % g_blk || D % 16) return (int)hipErrorInvalidValue;
+    const unsigned g = (unsigned)(((long long)M * (D / 16) + 255) / 256);
+#define L(BL) (k_embed<BL><<<g, 256, 0, g_stream>>>((const int8_t*)Wm, (const int8_t*)WE, (const int*)tok, (int8_t*)Xm, (int8_t*)XE, M, D, V, kid), 0)
+    POR_BLK(L);
+#undef L
+    return fim();
+}
+int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
+    if (M <= 0 || V % g_blk || V % 16) return (int)hipErrorInvalidValue;
+    const unsigned g = (unsigned)(((long long)M * (V / 16) + 255) / 256);
+#define L(BL) (k_um_quente<BL><<<g, 256, 0, g_stream>>>((const int*)tok, (int8_t*)U, (int8_t*)UE, M, V, kid), 0)
+    POR_BLK(L);
+#undef L
+    return fim();
+}
+
+// ---------------------------------------------------------------------------------------------- rows
+// one row per LPR lanes with VPR values each: D (or V) in {128, 256, 512, 1024}
+#define POR_LINHA(LEN, K3)                                                   \
+    switch (LEN) {                                                           \
+        case 128: K3(4, 32); break;                                          \
+        case 256: K3(4, 64); break;                                          \
+        case 512: K3(8, 64); break;                                          \
+        case 1024: K3(16, 64); break;                                        \
+        default: return (int)hipErrorInvalidValue;                           \
+    }
+int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid) {
+    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                               \
+        if (g_blk == 32) k_rms<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE, \
+                                                                     (int*)cr, (int*)cemax, M, log2D, G, kid);                       \
+        else k_rms<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE,             \
+                                                           (int*)cr, (int*)cemax, M, log2D, G, kid); }
+    POR_LINHA(D, K3)
+#undef K3
+    return fim();
+}
+int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om, void* oE, int M,
+                int D, int log2D, int G, int GB, int kid) {
+    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                       \
+        if (g_blk == 32) k_rms_back<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,             \
+            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid);                          \
+        else k_rms_back<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,                        \
+            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid); }
+    POR_LINHA(D, K3)
+#undef K3
+    return fim();
+}
+int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V, int log2M,
+                  int kid) {
+    if (M <= 0 || V % g_blk) return (int)hipErrorInvalidValue;
+#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                    \
+        if (g_blk == 32) k_softmax_ce<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (const int*)alvo,           \
+            (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid);                                                           \
+        else k_softmax_ce<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (const int*)alvo,                     \
+            (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid); }
+    POR_LINHA(V, K3)
+#undef K3
+    return fim();
+}
+
+// ---------------------------------------------------------------------------------------------- attention
+int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    const int hd = D / H;
+    if (hd != 4) return (int)hipErrorNotSupported;
+    if (T <= 128)
+        k_atencao4<128><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+    else
+        k_atencao4<256><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+    return fim();
+}
+int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
+                    int D, int GA, int limite, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    const int hd = D / H;
+    if (hd != 4) return (int)hipErrorNotSupported;
+    const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);
+#define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
+    if (T <= 128) {
+        if (limite) k_atencao4_back<128, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
+        else k_atencao4_back<128, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+    } else {
+        if (limite) k_atencao4_back<256, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
+        else k_atencao4_back<256, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+    }
+#undef ARGS
+    return fim();
+}
+
+}  // extern "C"

@@ -1,0 +1,223 @@
+// Jatai INT8 training kernels for MI355X (gfx950): shared formats, primitives and the device error record.
+//
+// Formats (same storage contract as the reference, jatai_cuda/jatai_cuda.cu:3-6 and ops.py:9):
+//   block tensor  m int8 [R, C] + E int8 [R, C / BLK]; value m * 2^E; an all-zero block has E = -127.
+//   raw tensor    acc int32 [R, C] + e int16 [R, C] (one exponent per element).
+//   R16 tensor    m int16 [R, C] + E int8 [R, C / BLK] (16-bit residual stream).
+// BLK is a template parameter of every kernel (32 or 128); the reference fixes 128 (ops.py:17).
+//
+// Every intermediate is an int32 kept below 2^30; the kernels check the bound where a proof does not cover it
+// and record the first violation in `g_erro` (the reference's sentinel contract, jatai_cuda.cu:22-36,
+// decoded by the host registry). Rounding is always half-to-even.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#define E_ZERO (-127)
+#define LIM (1 << 30)
+#define SEM_TOPO (-100000)
+#define U_MIN (-2147483647)
+
+enum { E_ACUM = 1, E_EXP = 2, E_SAT = 3, E_DIV = 4, E_SHL = 5, E_ARG = 6 };
+
+struct Erro {
+    int n, codigo, kid, pad;
+    long long idx, valor, aux;
+};
+extern __device__ Erro g_erro;
+
+// Cold path, kept out of line so it does not inflate hot loops. First event wins.
+__device__ __noinline__ void reporta(int codigo, int kid, long long idx, long long valor, long long aux);
+
+// ---------------------------------------------------------------------------------------------- primitives
+__device__ __forceinline__ int bitlen(int x) { return x == 0 ? 0 : 32 - __clz(x < 0 ? -x : x); }
+
+// x * 2^-s rounded half to even (ops.py:42-51). s <= 0 is a left shift, checked against 2^30.
+__device__ __forceinline__ int rnd(int x, int s, int kid, long long idx) {
+    if (s <= 0) {
+        if (s == 0 || x == 0) return x;
+        s = -s;
+        if (s > 30 || bitlen(x) + s > 30) { reporta(E_SHL, kid, idx, x, -s); return 0; }
+        return x << s;
+    }
+    if (s > 30) return 0;                        // |x| < 2^30 < 2^(s-1): rounds to 0
+    return (x + ((1 << (s - 1)) - 1) + ((x >> s) & 1)) >> s;
+}
+
+// rnd for a known s >= 0 with |x| < 2^30 (s >= 31 gives 0 through the same formula once s is clamped to 31)
+__device__ __forceinline__ int rnd_d(int x, int s) {
+    s = min(s, 31);
+    if (s == 0) return x;
+    return (x + ((1 << (s - 1)) - 1) + ((x >> s) & 1)) >> s;
+}
+
+// x * 2^-s for either sign of s where a left shift provably keeps every bit (no check)
+__device__ __forceinline__ int desloca(int x, int s) { return s >= 0 ? rnd_d(x, s) : x << min(-s, 31); }
+
+// exp(-d/256) in Q15 for d >= 0: shift plus a cubic (ops.py:75-81)
+__device__ __forceinline__ int exp_int(int d) {
+    int t = min(d, 6000) * 23637;
+    int n = t >> 22, f = (t & ((1 << 22) - 1)) >> 7;
+    int p = -1295;
+    p = ((p * f) >> 15) + 7556;
+    p = ((p * f) >> 15) - 22645;
+    p = ((p * f) >> 15) + 32765;
+    return n > 30 ? 0 : p >> n;
+}
+// exp(-(mx - u)/256) with the difference clamped before subtracting (mx - u may exceed 2^31)
+__device__ __forceinline__ int exp_dif(int mx, int u) { return exp_int(u <= mx - 6000 ? 6000 : mx - u); }
+
+__device__ __forceinline__ int isqrt_i(int n) {     // ops.py:84-89
+    n = max(n, 0);
+    int x = 1 << ((bitlen(n) + 1) / 2);
+    for (int i = 0; i < 10; i++) x = min(x, (x + n / max(x, 1)) >> 1);
+    return max(x, 1);
+}
+
+// ---------------------------------------------------------------------------------------------- lane groups
+// A block of BLK values is held by LPB consecutive lanes (a power of two <= 64), VPL values each.
+template <int LPB>
+__device__ __forceinline__ int g_max(int v) {
+#pragma unroll
+    for (int o = 1; o < LPB; o <<= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+template <int LPB>
+__device__ __forceinline__ int g_sum(int v) {
+#pragma unroll
+    for (int o = 1; o < LPB; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <int LPB>
+__device__ __forceinline__ int g_or(int v) {
+#pragma unroll
+    for (int o = 1; o < LPB; o <<= 1) v |= __shfl_xor(v, o);
+    return v;
+}
+
+// Quantize one block (LPB lanes x VPL values, per-element exponent e) into mantissas of MBITS bits plus one
+// exponent (ops.py:58-72; 16-bit variant jatai_cuda.cu:451-483): topo = max(e + bitlen(v)) over nonzeros,
+// E = topo - MBITS, q = rnd(v, E - e), E += 1 if any |q| > LIMQ, all-zero or E < -126 -> zero block.
+// Returns E (E_ZERO for a zero block). idx0 is the flat index of this lane's first value (for sentinels).
+template <int VPL, int LPB, typename MT, int MBITS, int LIMQ>
+__device__ __forceinline__ int quant_grupo(const int (&v)[VPL], const int (&e)[VPL], MT (&m)[VPL], int kid, long long idx0) {
+    int topo = SEM_TOPO;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e[i]);
+        if (v[i] != 0) topo = max(topo, e[i] + bitlen(v[i]));
+    }
+    topo = g_max<LPB>(topo);
+    if (topo == SEM_TOPO) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++) m[i] = 0;
+        return E_ZERO;
+    }
+    int E = topo - MBITS, q[VPL], est = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { q[i] = rnd(v[i], E - e[i], kid, idx0 + i); est |= q[i] > LIMQ || q[i] < -LIMQ; }
+    if (g_or<LPB>(est)) {
+        E += 1;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) q[i] = rnd(v[i], E - e[i], kid, idx0 + i);
+    }
+    if (E < -126) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++) m[i] = 0;
+        return E_ZERO;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        if (q[i] > LIMQ || q[i] < -LIMQ) reporta(E_SAT, kid, idx0 + i, q[i], E);
+        m[i] = (MT)max(-LIMQ, min(LIMQ, q[i]));
+    }
+    if (E > 126) reporta(E_EXP, kid, idx0, E, topo);
+    return E;
+}
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], int8_t (&m)[VPL], int kid, long long idx0) {
+    return quant_grupo<VPL, LPB, int8_t, 7, 127>(v, e, m, kid, idx0);
+}
+
+// Quantize a block whose values all share exponent e, where the caller knows every left shift is exact
+// (values built from int8 mantissas): same rules as quant_grupo, without per-element checks (the fused
+// GEMM epilogues use this, as jatai_cuda.cu:161-188 does).
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
+    int bl = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) bl = max(bl, bitlen(v[i]));
+    bl = g_max<LPB>(bl);
+    int E = e + bl - 7, q[VPL], est = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { q[i] = desloca(v[i], bl - 7); est |= q[i] > 127 || q[i] < -127; }
+    if (g_or<LPB>(est)) {
+        E += 1;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) q[i] = desloca(v[i], bl - 6);
+    }
+    const bool zero = bl == 0 || E < -126;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = zero ? 0 : (int8_t)q[i];
+    return zero ? E_ZERO : E;
+}
+
+// ---------------------------------------------------------------------------------------------- vector I/O
+template <int N>
+__device__ __forceinline__ void le_i8(const int8_t* p, int (&v)[N]) {
+    static_assert(N == 4 || N == 8 || N == 16, "");
+    if constexpr (N == 4) {
+        const int w = *reinterpret_cast<const int*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = (int)(int8_t)(w >> (8 * i));
+    } else if constexpr (N == 8) {
+        const int2 w = *reinterpret_cast<const int2*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) { v[i] = (int)(int8_t)(w.x >> (8 * i)); v[4 + i] = (int)(int8_t)(w.y >> (8 * i)); }
+    } else {
+        const int4 w = *reinterpret_cast<const int4*>(p);
+        const int ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[4 * j + i] = (int)(int8_t)(ws[j] >> (8 * i));
+    }
+}
+template <int N>
+__device__ __forceinline__ void grava_i8(int8_t* p, const int8_t (&m)[N]) {
+    int ws[(N + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < N / 4; j++)
+        ws[j] = (int)(uint8_t)m[4 * j] | ((int)(uint8_t)m[4 * j + 1] << 8) | ((int)(uint8_t)m[4 * j + 2] << 16) |
+                ((int)(uint8_t)m[4 * j + 3] << 24);
+    if constexpr (N == 4) *reinterpret_cast<int*>(p) = ws[0];
+    else if constexpr (N == 8) *reinterpret_cast<int2*>(p) = make_int2(ws[0], ws[1]);
+    else *reinterpret_cast<int4*>(p) = make_int4(ws[0], ws[1], ws[2], ws[3]);
+}
+template <int N>
+__device__ __forceinline__ void le_i32(const int* p, int (&v)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; j += 4) {
+        const int4 w = *reinterpret_cast<const int4*>(p + j);
+        v[j] = w.x; v[j + 1] = w.y; v[j + 2] = w.z; v[j + 3] = w.w;
+    }
+}
+template <int N>
+__device__ __forceinline__ void le_i16(const int16_t* p, int (&v)[N]) {
+    static_assert(N % 4 == 0, "");
+#pragma unroll
+    for (int j = 0; j < N; j += 4) {
+        const int2 w = *reinterpret_cast<const int2*>(p + j);
+        v[j] = (int)(int16_t)(w.x & 0xffff); v[j + 1] = w.x >> 16;
+        v[j + 2] = (int)(int16_t)(w.y & 0xffff); v[j + 3] = w.y >> 16;
+    }
+}
+template <int N>
+__device__ __forceinline__ void grava_i16(int16_t* p, const int16_t (&m)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; j += 4) {
+        const int a = (int)(uint16_t)m[j] | ((int)(uint16_t)m[j + 1] << 16);
+        const int b = (int)(uint16_t)m[j + 2] | ((int)(uint16_t)m[j + 3] << 16);
+        *reinterpret_cast<int2*>(p + j) = make_int2(a, b);
+    }
+}

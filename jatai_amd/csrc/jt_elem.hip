@@ -1,0 +1,239 @@
+// Element-wise and per-block kernels: quant, soma, relu2, relu2_back, momento, peso, para16, para8, soma16,
+// embed, um_quente, and the int32 fill used before split-K accumulation.
+//
+// Layout: 256 threads per workgroup, 8 consecutive values per lane, so a block of BLK values is LPB = BLK/8
+// consecutive lanes (4 at BLK=32, 16 at BLK=128) and one workgroup covers 2048 values. Each lane moves 8 B
+// (int8), 16 B (int16) or 32 B (int32) per operand with vector loads: these kernels stream HBM.
+#include "jt_comum.h"
+
+#define VPL 8
+#define ELEM_PROLOGO                                                   \
+    constexpr int LPB = BLK / VPL;                                     \
+    const long long o = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * VPL; \
+    const long long w = o / BLK;                                       \
+    if (w >= nblocos) return;
+
+// raw (acc int32, e int16) -> block (ops.py:125-126)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_quant(const int* __restrict__ acc, const int16_t* __restrict__ e, int8_t* __restrict__ m,
+                                               int8_t* __restrict__ E, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int v[VPL], ee[VPL];
+    le_i32(acc + o, v);
+    le_i16(e + o, ee);
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(m + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) E[w] = (int8_t)Eo;
+}
+
+// z = x + y: ec = max(xE, yE) - 21 (ops.py:128-132)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_soma(const int8_t* __restrict__ xm, const int8_t* __restrict__ xE, const int8_t* __restrict__ ym,
+                                              const int8_t* __restrict__ yE, int8_t* __restrict__ zm, int8_t* __restrict__ zE,
+                                              long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int a[VPL], b[VPL], v[VPL], ee[VPL];
+    le_i8(xm + o, a);
+    le_i8(ym + o, b);
+    const int ex = xE[w], ey = yE[w], ec = max(ex, ey) - 21;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { v[i] = rnd(a[i], ec - ex, kid, o + i) + rnd(b[i], ec - ey, kid, o + i); ee[i] = ec; }
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(zm + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) zE[w] = (int8_t)Eo;
+}
+
+// a = max(h, 0)^2 with exponent 2E (ops.py:134-137)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_relu2(const int8_t* __restrict__ hm, const int8_t* __restrict__ hE, int8_t* __restrict__ am,
+                                               int8_t* __restrict__ aE, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int h[VPL], v[VPL], ee[VPL];
+    le_i8(hm + o, h);
+    const int e2 = 2 * hE[w];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { const int r = max(h[i], 0); v[i] = r * r; ee[i] = e2; }
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(am + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) aE[w] = (int8_t)Eo;
+}
+
+// gh = g * 2 max(h, 0) with exponent gE + hE (ops.py:139-141)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_relu2_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ hm,
+                                                    const int8_t* __restrict__ hE, int8_t* __restrict__ om, int8_t* __restrict__ oE,
+                                                    long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int g[VPL], h[VPL], v[VPL], ee[VPL];
+    le_i8(gm + o, g);
+    le_i8(hm + o, h);
+    const int es = gE[w] + hE[w];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { v[i] = g[i] * max(h[i], 0) * 2; ee[i] = es; }
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(om + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) oE[w] = (int8_t)Eo;
+}
+
+// momentum, in place: m <- 7/8 m + g with g raw (ops.py:273-278)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, const int16_t* __restrict__ ge, int8_t* __restrict__ Mm,
+                                                 int8_t* __restrict__ ME, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int mm[VPL], g[VPL], eg[VPL], v[VPL], ee[VPL];
+    le_i8(Mm + o, mm);
+    le_i32(gacc + o, g);
+    le_i16(ge + o, eg);
+    const int em = ME[w] - 3;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
+        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
+        v[i] = rnd(mm[i] * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
+        ee[i] = ec;
+    }
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(Mm + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) ME[w] = (int8_t)Eo;
+}
+
+// weight update, in place: W <- W - 2^-k m (+ error-feedback residual R) (ops.py:280-290)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_peso(int8_t* __restrict__ Wm, int8_t* __restrict__ WE, const int8_t* __restrict__ Mm,
+                                              const int8_t* __restrict__ ME, int8_t* __restrict__ Rm, int8_t* __restrict__ RE, int k_lr,
+                                              int ef, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int wv[VPL], mv[VPL], rv[VPL], alvo[VPL], ee[VPL];
+    le_i8(Wm + o, wv);
+    le_i8(Mm + o, mv);
+    if (ef) le_i8(Rm + o, rv);
+    else
+#pragma unroll
+        for (int i = 0; i < VPL; i++) rv[i] = 0;
+    const int ew = WE[w], em = ME[w] - k_lr, er = ef ? (int)RE[w] : E_ZERO;
+    const int ec = max(max(ew + 7, em + 7), er + 7) - 27;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        alvo[i] = rnd(wv[i], ec - ew, kid, o + i) - rnd(mv[i], ec - em, kid, o + i) + (ef ? rnd(rv[i], ec - er, kid, o + i) : 0);
+        ee[i] = ec;
+    }
+    int8_t q[VPL];
+    const int Ew = quant8<VPL, LPB>(alvo, ee, q, kid, o);
+    grava_i8(Wm + o, q);
+    const bool lider = (threadIdx.x & (LPB - 1)) == 0;
+    if (lider) WE[w] = (int8_t)Ew;
+    if (!ef) return;
+    int dif[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) dif[i] = alvo[i] - (q[i] == 0 ? 0 : rnd(q[i], ec - Ew, kid, o + i));
+    int8_t r[VPL];
+    const int Er = quant8<VPL, LPB>(dif, ee, r, kid, o);
+    grava_i8(Rm + o, r);
+    if (lider) RE[w] = (int8_t)Er;
+}
+
+// ---------------------------------------------------------------------------------------------- R16 residual stream
+// INT8 -> R16, exact: m << 7, E - 7; zero blocks keep E = -127 (jatai_cuda.cu:491-500)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_para16(const int8_t* __restrict__ xm, const int8_t* __restrict__ xE, int16_t* __restrict__ zm,
+                                                int8_t* __restrict__ zE, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int a[VPL];
+    le_i8(xm + o, a);
+    int16_t z[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) z[i] = (int16_t)(a[i] << 7);
+    grava_i16(zm + o, z);
+    if ((threadIdx.x & (LPB - 1)) == 0) zE[w] = xE[w] == E_ZERO ? (int8_t)E_ZERO : (int8_t)(xE[w] - 7);
+}
+
+// R16 -> INT8 with the INT8 quant rules (jatai_cuda.cu:501-513)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_para8(const int16_t* __restrict__ xm, const int8_t* __restrict__ xE, int8_t* __restrict__ ym,
+                                               int8_t* __restrict__ yE, long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int v[VPL], ee[VPL];
+    le_i16(xm + o, v);
+    const int ex = xE[w];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) ee[i] = ex;
+    int8_t q[VPL];
+    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(ym + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) yE[w] = (int8_t)Eo;
+}
+
+// z (R16) = x (R16) + y (INT8): ec = max(ex + 15, ey + 7) - 28; zero blocks contribute 0 (jatai_cuda.cu:514-531)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_soma16(const int16_t* __restrict__ xm, const int8_t* __restrict__ xE, const int8_t* __restrict__ ym,
+                                                const int8_t* __restrict__ yE, int16_t* __restrict__ zm, int8_t* __restrict__ zE,
+                                                long long nblocos, int kid) {
+    ELEM_PROLOGO
+    int a[VPL], b[VPL], v[VPL], ee[VPL];
+    le_i16(xm + o, a);
+    le_i8(ym + o, b);
+    const int ex = xE[w], ey = yE[w], ec = max(ex + 15, ey + 7) - 28;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        v[i] = (ex == E_ZERO ? 0 : rnd(a[i], ec - ex, kid, o + i)) + (ey == E_ZERO ? 0 : rnd(b[i], ec - ey, kid, o + i));
+        ee[i] = ec;
+    }
+    int16_t q[VPL];
+    const int Eo = quant_grupo<VPL, LPB, int16_t, 15, 32767>(v, ee, q, kid, o);
+    grava_i16(zm + o, q);
+    if ((threadIdx.x & (LPB - 1)) == 0) zE[w] = (int8_t)Eo;
+}
+
+// ---------------------------------------------------------------------------------------------- embedding
+// X[t] = W[tok[t]] (ops.py:143-145). One lane per 16 bytes of a row; a token outside the vocabulary is
+// reported (E_ARG, index = start of output row t) and its row is written as a zero block row.
+template <int BLK>
+__global__ void __launch_bounds__(256) k_embed(const int8_t* __restrict__ Wm, const int8_t* __restrict__ WE, const int* __restrict__ tok,
+                                               int8_t* __restrict__ Xm, int8_t* __restrict__ XE, int M, int D, int V, int kid) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;      // 16-byte chunk index
+    const int chunks = D / 16;
+    if (i >= (long long)M * chunks) return;
+    const int t = (int)(i / chunks), c = (int)(i % chunks);
+    const int v = tok[t];
+    const bool ok = v >= 0 && v < V;
+    if (!ok && c == 0) reporta(E_ARG, kid, (long long)t * D, v, V);
+    const int4 z = ok ? *reinterpret_cast<const int4*>(Wm + (size_t)v * D + c * 16) : make_int4(0, 0, 0, 0);
+    *reinterpret_cast<int4*>(Xm + (size_t)t * D + c * 16) = z;
+    const int nb = D / BLK;
+    // exponent bytes: chunk c covers bytes [16c, 16c + 16) of the row; its blocks start there
+    for (int b = c * 16 / BLK; b < nb && b * BLK < (c + 1) * 16; b++)
+        if (b * BLK >= c * 16) XE[(size_t)t * nb + b] = ok ? WE[(size_t)v * nb + b] : (int8_t)E_ZERO;
+}
+
+// one-hot rows: U[t, tok[t]] = 1, exponent 0 (not -127) for every block (ops.py:147-151)
+template <int BLK>
+__global__ void __launch_bounds__(256) k_um_quente(const int* __restrict__ tok, int8_t* __restrict__ U, int8_t* __restrict__ UE, int M,
+                                                   int V, int kid) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int chunks = V / 16;
+    if (i >= (long long)M * chunks) return;
+    const int t = (int)(i / chunks), c = (int)(i % chunks);
+    const int v = tok[t];
+    const bool ok = v >= 0 && v < V;
+    if (!ok && c == 0) reporta(E_ARG, kid, (long long)t * V, v, V);
+    int8_t q[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) q[j] = (ok && c * 16 + j == v) ? 1 : 0;
+    grava_i8(U + (size_t)t * V + c * 16, q);
+    const int nb = V / BLK;
+    for (int b = c * 16 / BLK; b < nb && b * BLK < (c + 1) * 16; b++)
+        if (b * BLK >= c * 16) UE[(size_t)t * nb + b] = 0;
+}
+
+// int32 fill (split-K accumulators are zeroed with a kernel, so graph replays need no memset node)
+__global__ void __launch_bounds__(256) k_zera32(int* __restrict__ p, long long n) {
+    const long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= n) *reinterpret_cast<int4*>(p + i) = make_int4(0, 0, 0, 0);
+    else
+        for (long long j = i; j < n; j++) p[j] = 0;
+}

@@ -1,0 +1,159 @@
+// Row kernels: rms, rms_back, softmax_ce (one row per LPR consecutive lanes, VPR values per lane,
+// LPR * VPR = row length), and transpoe (128 x 64 byte tiles through LDS).
+#include "jt_comum.h"
+
+// ---------------------------------------------------------------------------------------------- RMSNorm
+// Y = quant(x * 2^k / r, e_b - k - emax + G/2), with ss = sum_b rnd(sum(m^2) << G, 2 (emax - e_b)),
+// r = isqrt(ss >> log2 D), k = bitlen(r) + 10. Caches (r, emax) per row (ops.py:153-165).
+template <int VPR, int LPR, int BLK>
+__global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, const int8_t* __restrict__ XE, int8_t* __restrict__ Ym,
+                                             int8_t* __restrict__ YE, int* __restrict__ cr, int* __restrict__ cemax, int M, int log2D,
+                                             int G, int kid) {
+    constexpr int D = VPR * LPR, nb = D / BLK, LPB = BLK / VPR;
+    const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    if (row >= M) return;
+    const long long o = (long long)row * D + lr * VPR;
+    int x[VPR];
+    le_i8(Xm + o, x);
+    const int b = lr / LPB, eb = XE[(long long)row * nb + b];
+    const int emax = g_max<LPR>(eb);
+    int sq = 0;
+#pragma unroll
+    for (int i = 0; i < VPR; i++) sq += x[i] * x[i];
+    sq = g_sum<LPB>(sq);
+    const bool lider = (lr & (LPB - 1)) == 0;
+    const int ss = g_sum<LPR>(lider ? rnd(sq << G, 2 * (emax - eb), kid, (long long)row * D) : 0);
+    if (ss >= LIM && lr == 0) reporta(E_ACUM, kid, (long long)row * D, ss, -1);
+    const int r = isqrt_i(ss >> log2D), k = bitlen(r) + 10, inv = (1 << k) / r;
+    int v[VPR], ee[VPR];
+#pragma unroll
+    for (int i = 0; i < VPR; i++) { v[i] = x[i] * inv; ee[i] = eb - k - emax + G / 2; }
+    int8_t q[VPR];
+    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    grava_i8(Ym + o, q);
+    if (lider) YE[(long long)row * nb + b] = (int8_t)Eo;
+    if (lr == 0) { cr[row] = r; cemax[row] = emax; }
+}
+
+// RMSNorm backward: dx = (g - y * mean(g y)) / rms in the spec's integer steps (ops.py:167-184)
+template <int VPR, int LPR, int BLK>
+__global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ ym,
+                                                  const int8_t* __restrict__ yE, const int* __restrict__ cr, const int* __restrict__ cemax,
+                                                  int8_t* __restrict__ om, int8_t* __restrict__ oE, int M, int log2D, int G, int GB, int kid) {
+    constexpr int D = VPR * LPR, nb = D / BLK, LPB = BLK / VPR;
+    const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    if (row >= M) return;
+    const long long o = (long long)row * D + lr * VPR;
+    int g[VPR], y[VPR];
+    le_i8(gm + o, g);
+    le_i8(ym + o, y);
+    const int b = lr / LPB, eg = gE[(long long)row * nb + b], ey = yE[(long long)row * nb + b];
+    const int smax = g_max<LPR>(eg + ey);
+    int S = 0;
+#pragma unroll
+    for (int i = 0; i < VPR; i++) S += rnd((g[i] * y[i]) << GB, smax - (eg + ey), kid, (long long)row * D);
+    S = g_sum<LPR>(S);
+    if ((S >= LIM || S <= -LIM) && lr == 0) reporta(E_ACUM, kid, (long long)row * D, S, -2);
+    int eS = smax - GB - log2D;
+    const int sh = max(bitlen(S) - 15, 0);
+    S = rnd(S, sh, kid, (long long)row * D);
+    eS += sh;
+    const int r = cr[row], k = bitlen(r) + 10, inv = (1 << k) / r, emax = cemax[row];
+    const int ec = max(eg + 7, ey + eS + 22) - 28;
+    int v[VPR], ee[VPR];
+#pragma unroll
+    for (int i = 0; i < VPR; i++) {
+        int dentro = rnd(g[i], ec - eg, kid, o + i) - rnd(y[i] * S, ec - (ey + eS), kid, o + i);
+        const int sh2 = max(bitlen(dentro) - 18, 0);
+        dentro = rnd(dentro, sh2, kid, o + i);
+        v[i] = dentro * inv;
+        ee[i] = ec + sh2 - k - (emax - G / 2);
+    }
+    int8_t q[VPR];
+    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    grava_i8(om + o, q);
+    if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Eo;
+}
+
+// ---------------------------------------------------------------------------------------------- softmax + CE
+// raw logits -> g = (P - 1[target]) in block format with exponent -12 - log2 M; d_alvo = umax - u_target and
+// soma = sum of ex per row, from which the host derives the float64 loss (ops.py:260-271; modelo.py:93).
+template <int VPR, int LPR, int BLK>
+__global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc, const int16_t* __restrict__ e, const int* __restrict__ alvo,
+                                                    int8_t* __restrict__ gm, int8_t* __restrict__ gE, int* __restrict__ d_alvo,
+                                                    int* __restrict__ soma_o, int M, int log2M, int kid) {
+    constexpr int V = VPR * LPR, nb = V / BLK, LPB = BLK / VPR;
+    const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    if (row >= M) return;
+    const int t = alvo[row];
+    if (t < 0 || t >= V) { if (lr == 0) reporta(E_ARG, kid, (long long)row * V, t, V); return; }
+    const long long o = (long long)row * V + lr * VPR;
+    int a[VPR], ea[VPR], u[VPR];
+    le_i32(acc + o, a);
+    le_i16(e + o, ea);
+    int umax = U_MIN;
+#pragma unroll
+    for (int i = 0; i < VPR; i++) { u[i] = rnd(a[i], -(ea[i] + 8), kid, o + i); umax = max(umax, u[i]); }
+    umax = g_max<LPR>(umax);
+    int ex[VPR], s = 0;
+#pragma unroll
+    for (int i = 0; i < VPR; i++) { ex[i] = exp_dif(umax, u[i]) >> 3; s += ex[i]; }
+    s = g_sum<LPR>(s);
+    if (s <= 0) { if (lr == 0) reporta(E_DIV, kid, (long long)row * V, s, umax); s = 1; }
+    const int inv = (1 << 28) / s;
+    int v[VPR], ee[VPR];
+#pragma unroll
+    for (int i = 0; i < VPR; i++) {
+        const int col = lr * VPR + i;
+        v[i] = ((ex[i] * inv + (1 << 15)) >> 16) - (col == t ? 4096 : 0);
+        ee[i] = -12 - log2M;
+        if (col == t) d_alvo[row] = umax - u[i];
+    }
+    int8_t q[VPR];
+    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    grava_i8(gm + o, q);
+    if ((lr & (LPB - 1)) == 0) gE[(long long)row * nb + lr / LPB] = (int8_t)Eo;
+    if (lr == 0) soma_o[row] = s;
+}
+
+// ---------------------------------------------------------------------------------------------- transpoe
+// X [R, C] blocked along C -> Y [C, R] blocked along R: Y = quant(m^T, expand(E)^T) (ops.py:121-123).
+// Tile 128 rows x 64 cols. Lane (cg, rc) owns 4 columns (one 32-bit LDS word) x 8 rows: it reads 8 words,
+// unpacks 32 values and runs 4 block quantizations side by side; the LPB = BLK/8 lanes of a column block are
+// consecutive lanes. Rows of the LDS tile are 17 words long so the word reads spread over the banks.
+template <int BLK>
+__global__ void __launch_bounds__(256) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
+                                                  int8_t* __restrict__ EY, int R, int C, int kid) {
+    constexpr int LPB = BLK / 8;
+    __shared__ int tile[128][17];
+    __shared__ int8_t er[128][2];
+    const int r0 = blockIdx.y * 128, c0 = blockIdx.x * 64, tid = threadIdx.x, nbx = C / BLK;
+    {
+        const int row = tid >> 1, half = tid & 1;
+        const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
+        const int4 v0 = src[0], v1 = src[1];
+        int* d = &tile[row][half * 8];
+        d[0] = v0.x; d[1] = v0.y; d[2] = v0.z; d[3] = v0.w; d[4] = v1.x; d[5] = v1.y; d[6] = v1.z; d[7] = v1.w;
+        // exponent of columns [c0 + 32 half, c0 + 32 half + 32)
+        er[row][half] = EX[(size_t)(r0 + row) * nbx + (c0 + half * 32) / BLK];
+    }
+    __syncthreads();
+    const int cg = tid >> 4, rc = tid & 15;            // columns c0 + 4 cg .. +3, rows r0 + 8 rc .. +7
+    int m[4][8], e[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int row = rc * 8 + k, word = tile[row][cg];
+        e[k] = er[row][cg >> 3];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) m[cc][k] = (word << (24 - 8 * cc)) >> 24;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+        const int col = c0 + 4 * cg + cc;
+        const long long o = (long long)col * R + r0 + rc * 8;
+        int8_t q[8];
+        const int E = quant8<8, LPB>(m[cc], e, q, kid, o);
+        grava_i8(Y + o, q);
+        if ((rc & (LPB - 1)) == 0) EY[(size_t)col * (R / BLK) + (r0 + rc * 8) / BLK] = (int8_t)E;
+    }
+}

@@ -1,0 +1,184 @@
+"""The integer training step: the same composition of ops as the reference's `Modelo.passo`
+(jatai_cuda/modelo.py:29-140) -- pre-norm decoder, RMSNorm without gain, causal ALiBi attention, ReLU^2 MLP,
+byte vocabulary, Q/K/V in one matrix, SGD with momentum 7/8, lr = 2^-k and error feedback -- run on any backend
+with the reference operator surface (OpsHip on the GPU; a CPU oracle in the tests and the CPU baseline).
+
+`PassoGravado` captures one whole training step (forward, backward, optimizer: ~522 launches at L=12) as one
+hipGraph through torch.cuda.graph (reference: modelo.py:143-180). Weights, momentum and residuals are updated in
+place by the kernels, every temporary lives in the graph's pool at a fixed address, and the loss is computed on
+the host side of the replay from the captured per-row integers (d_alvo, soma), so no library reduction is
+recorded inside the graph.
+"""
+import math
+import os
+
+import torch
+
+from . import ops as O
+
+R16 = os.environ.get("JATAI_RES16") == "1"     # 16-bit residual stream (modelo.py:26)
+
+
+def inicial(g, linhas, fan_in, dev, emb=False):
+    """Weight init: m = round(N(0,1) * 32) clamped to +-127, E = -round(log2(32 sqrt(fan_in))) (embedding: -5),
+    drawn from the CPU generator g (modelo.py:16-19; Python's round on a float)."""
+    e = -5 if emb else -int(round(math.log2(32 * math.sqrt(fan_in))))
+    m = torch.round(torch.randn(linhas, fan_in, generator=g) * 32).clamp(-127, 127).to(torch.int8)
+    return m.to(dev).contiguous(), torch.full((linhas, fan_in // O.BLK), e, dtype=torch.int8, device=dev)
+
+
+def zeros_como(t):
+    return torch.zeros_like(t[0]), torch.full_like(t[1], O.E_ZERO)
+
+
+def perda_de(d_alvo, soma):
+    """Cross-entropy in nats from the integer softmax outputs: mean(d/256 + ln(s/4096)) in float64 (modelo.py:93)."""
+    return (d_alvo.double() / 256 + torch.log(soma.double() / 4096)).mean()
+
+
+class Modelo:
+    def __init__(self, V, D, H, FF, L, semente, dev, ops, reg, r16=None):
+        self.V, self.D, self.H, self.FF, self.L, self.dev, self.ops, self.reg = V, D, H, FF, L, dev, ops, reg
+        self.r16 = R16 if r16 is None else r16
+        g = torch.Generator().manual_seed(semente)
+        p = {"emb": inicial(g, V, D, dev, emb=True)}
+        for l in range(L):
+            q, k, v = inicial(g, D, D, dev), inicial(g, D, D, dev), inicial(g, D, D, dev)
+            p[f"Wqkv{l}"] = (torch.cat([q[0], k[0], v[0]]).contiguous(), torch.cat([q[1], k[1], v[1]]).contiguous())
+            p[f"Wo{l}"] = inicial(g, D, D, dev)
+            p[f"Wup{l}"] = inicial(g, FF, D, dev)
+            p[f"Wd{l}"] = inicial(g, D, FF, dev)
+        p["out"] = inicial(g, V, D, dev)
+        self.p = p
+        self.mom = {n: zeros_como(t) for n, t in p.items()}
+        self.res = {n: zeros_como(t) for n, t in p.items()}
+        self.error_feedback = True
+        self.estatisticas = False
+        self.perda_inteira = False      # True: passo returns (d_alvo, soma) instead of the float64 loss
+
+    def _st(self, nome, t, zeros_normais=False):
+        if self.estatisticas:
+            self.reg.estatistica(nome, t, zeros_normais)
+
+    def passo(self, tok, alvo, k_lr=None):
+        """Forward (+ backward and update when k_lr is given). Returns the loss as a tensor on the device."""
+        ops, reg, p, r16 = self.ops, self.reg, self.p, self.r16
+        Bt, T = tok.shape
+        tok, alvo = tok.reshape(-1).to(torch.int32).contiguous(), alvo.reshape(-1).to(torch.int32).contiguous()
+        with reg.trecho("forward"):
+            with reg.trecho("embedding"):
+                x = ops.embed(p["emb"], tok)
+                if r16:
+                    x16 = ops.para16(x)
+            caches = []
+            for l in range(self.L):
+                with reg.trecho(f"camada {l}"):
+                    with reg.trecho("atencao"):
+                        n1, c1 = ops.rms(ops.para8(x16) if r16 else x)
+                        qkv = ops.gemm(n1, p[f"Wqkv{l}"])
+                        oc, P = ops.atencao(qkv, Bt, T, self.H)
+                        om = ops.quant(oc)
+                        if r16:
+                            x16 = ops.soma16(x16, ops.gemm(om, p[f"Wo{l}"]))
+                            x = ops.para8(x16) if self.estatisticas else None
+                        else:
+                            x = ops.gemm_soma(om, p[f"Wo{l}"], x)
+                        self._st(f"c{l}.qkv", qkv); self._st(f"c{l}.atencao_saida", om); self._st(f"c{l}.residuo1", x)
+                    with reg.trecho("mlp"):
+                        n2, c2 = ops.rms(ops.para8(x16) if r16 else x)
+                        h, a = ops.gemm_relu2(n2, p[f"Wup{l}"])
+                        if r16:
+                            x16 = ops.soma16(x16, ops.gemm(a, p[f"Wd{l}"]))
+                            x = ops.para8(x16) if self.estatisticas else None
+                        else:
+                            x = ops.gemm_soma(a, p[f"Wd{l}"], x)
+                        self._st(f"c{l}.relu2", a, zeros_normais=True); self._st(f"c{l}.residuo2", x)
+                caches.append((n1, c1, qkv, P, om, n2, c2, h, a))
+            with reg.trecho("saida"):
+                nf, cf = ops.rms(ops.para8(x16) if r16 else x)
+                logits = ops.gemm(nf, p["out"], cru=True)
+                g, d_alvo, soma = ops.softmax_ce(logits, alvo)
+        perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma)
+        if k_lr is None:
+            return perda
+        T_ = ops.transpoe
+        grads = {}
+        with reg.trecho("backward"):
+            with reg.trecho("saida"):
+                grads["out"] = ops.gemm(T_(g), T_(nf), cru=True)
+                gx = ops.gemm(g, T_(p["out"]))
+                gx = ops.rms_back(gx, nf, cf)
+                self._st("grad_saida", gx)
+                if r16:
+                    gx16 = ops.para16(gx)
+            for l in reversed(range(self.L)):
+                n1, c1, qkv, P, om, n2, c2, h, a = caches[l]
+                with reg.trecho(f"camada {l}"):
+                    with reg.trecho("mlp"):
+                        grads[f"Wd{l}"] = ops.gemm(T_(gx), T_(a), cru=True)
+                        gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
+                        grads[f"Wup{l}"] = ops.gemm(T_(gh), T_(n2), cru=True)
+                        gn = ops.gemm(gh, T_(p[f"Wup{l}"]))
+                        if r16:
+                            gx16 = ops.soma16(gx16, ops.rms_back(gn, n2, c2))
+                            gx = ops.para8(gx16)
+                        else:
+                            gx = ops.soma(gx, ops.rms_back(gn, n2, c2))
+                        self._st(f"c{l}.grad_mlp", gh, zeros_normais=True)
+                    with reg.trecho("atencao"):
+                        grads[f"Wo{l}"] = ops.gemm(T_(gx), T_(om), cru=True)
+                        go = ops.gemm(gx, T_(p[f"Wo{l}"]))
+                        gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
+                        grads[f"Wqkv{l}"] = ops.gemm(T_(gq), T_(n1), cru=True)
+                        gn = ops.gemm(gq, T_(p[f"Wqkv{l}"]))
+                        if r16:
+                            gx16 = ops.soma16(gx16, ops.rms_back(gn, n1, c1))
+                            gx = ops.para8(gx16)
+                        else:
+                            gx = ops.soma(gx, ops.rms_back(gn, n1, c1))
+                        self._st(f"c{l}.grad_qkv", gq); self._st(f"c{l}.grad_residuo", gx)
+            with reg.trecho("embedding"):
+                um = ops.um_quente(tok, self.V)
+                grads["emb"] = ops.gemm(T_(um), T_(gx), cru=True)
+        with reg.trecho("otimizador"):
+            for n, gr in grads.items():
+                with reg.trecho(n):
+                    self.mom[n] = ops.momento(gr, self.mom[n])
+                    self.p[n], self.res[n] = ops.peso(self.p[n], self.mom[n], self.res[n], k_lr, self.error_feedback)
+        return perda
+
+
+class PassoGravado:
+    """One training step captured as a hipGraph and replayed (modelo.py:143-180).
+
+    Capture runs nothing (weights do not change while recording). Inputs go to fixed buffers with copy_ before
+    each replay. The launch list of the capture (kid -> op, scope, inputs) is kept, so a device sentinel raised
+    in a replay names the same op and scope as in eager mode. Format checks run once, at capture.
+    """
+
+    def __init__(self, modelo, Bt, T, k_lr):
+        self.m, self.reg, self.k_lr = modelo, modelo.reg, k_lr
+        lib = modelo.ops.lib
+        self.tok = torch.zeros(Bt, T, dtype=torch.long, device=modelo.dev)
+        self.alvo = torch.zeros(Bt, T, dtype=torch.long, device=modelo.dev)
+        self.grafo = torch.cuda.CUDAGraph()
+        est, vig, pi = modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira
+        modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = False, False, True
+        torch.cuda.synchronize()
+        self.reg.lancamentos = []
+        try:
+            with torch.cuda.graph(self.grafo):
+                lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+                self.d_alvo, self.soma = modelo.passo(self.tok, self.alvo, k_lr=k_lr)
+        finally:
+            lib.jt_stream(None)
+            modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = est, vig, pi
+        self.lancamentos = list(self.reg.lancamentos)
+        self.reg.info(f"passo gravado num hipGraph: {len(self.lancamentos)} lancamentos", lancamentos=len(self.lancamentos))
+
+    def __call__(self, tok, alvo):
+        self.tok.copy_(tok)
+        self.alvo.copy_(alvo)
+        self.reg.lancamentos = self.lancamentos
+        self.grafo.replay()
+        return perda_de(self.d_alvo, self.soma)

@@ -1,0 +1,287 @@
+"""Operator surface of the Jatai INT8 training hot path on MI355X.
+
+`OpsHip` has the methods, arguments, return structure, shape guards and error behaviour of the reference's
+`OpsCuda` (jatai_cuda/ops.py:294-515): model code written against `OpsCuda` (modelo.py, treino_cuda.py,
+teste_ops.py) runs unchanged with `OpsHip`. Each method checks formats on the host, allocates its outputs
+with torch on the caller's device, and launches one hand-written gfx950 kernel through the C ABI of
+`libjatai.so` (include/jatai.h) via ctypes.
+
+Module globals read by callers, as in the reference: BLK (block size, 32 or 128; the reference fixes 128,
+ops.py:17), E_ZERO, GA, ATENCAO_LIMITE (attention-backward bound variant, ops.py:23), g_rms.
+
+There is no CPU fallback: if libjatai.so is missing or fails to load, constructing OpsHip raises.
+"""
+import ctypes
+import math
+import os
+
+import torch
+
+BLK = 128
+E_ZERO = -127
+GA = 4
+ATENCAO_LIMITE = False
+AQUI = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(AQUI, "libjatai.so")
+
+FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_back", "jt_momento", "jt_peso", "jt_transpoe",
+           "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
+           "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
+           "jt_bloco_atual")
+VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas")
+
+
+def g_rms(D):
+    """(G of the RMSNorm, G of its backward) for width D at the current BLK (ops.py:28-30)."""
+    nb = D // BLK
+    return 2 * ((8 - int(math.log2(nb))) // 2), 14 - int(math.log2(D))
+
+
+def carrega_lib(caminho=LIB):
+    """Load libjatai.so after torch, so the library binds to the HIP runtime torch already loaded (both carry
+    the soname libamdhip64.so.7): streams from torch.cuda are then valid handles for jt_stream."""
+    if not os.path.exists(caminho):
+        raise RuntimeError(f"libjatai.so not built ({caminho}); run `python -m jatai_amd.build` or __graft_entry__.build()")
+    lib = ctypes.CDLL(caminho)
+    for f in FUNCOES:
+        getattr(lib, f).restype = ctypes.c_int
+    for f in VOIDS:
+        getattr(lib, f).restype = None
+    lib.jt_stream.argtypes = [ctypes.c_void_p]
+    lib.jt_erro_le.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+class OpsHip:
+    nome = "hip"
+    lib_global = None
+
+    def __init__(self, reg):
+        self.reg = reg
+        self.lib = carrega_lib()
+        reg.lib = self.lib
+        if self.lib.jt_erro_limpa() != 0:
+            raise RuntimeError("libjatai: could not clear the device error record (no usable GPU?)")
+        if os.environ.get("JATAI_RES_EST") == "1":      # stochastic residual rounding (ops.py:308-309)
+            rc = self.lib.jt_res_estocastico(1)
+            if rc != 0:
+                raise RuntimeError("JATAI_RES_EST=1: stochastic residual rounding is not implemented in libjatai for MI355X")
+        self._blk = None
+        OpsHip.lib_global = self.lib
+
+    @staticmethod
+    def _a(x):
+        if torch.is_tensor(x):
+            return ctypes.c_void_p(x.data_ptr()) if x.numel() else ctypes.c_void_p(0)
+        if x is None:
+            return ctypes.c_void_p(0)
+        return ctypes.c_longlong(x) if isinstance(x, int) and abs(x) > 2**31 - 1 else ctypes.c_int(x)
+
+    def _lanca(self, op, fn, args, entradas, forma, longos=()):
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        kid = self.reg.registra(op, entradas, forma)
+        conv = [ctypes.c_longlong(a) if i in longos else self._a(a) for i, a in enumerate(args)]
+        r = getattr(self.lib, fn)(*conv, ctypes.c_int(kid))
+        self.reg.depois(kid, r)
+
+    def _novo_bloco(self, R, C, dev):
+        return torch.empty(R, C, dtype=torch.int8, device=dev), torch.empty(R, C // BLK, dtype=torch.int8, device=dev)
+
+    # ---------------------------------------------------------------- GEMM family (ops.py:329-372)
+    def _formas_gemm(self, op, a, b):
+        M, K = a.shape
+        N = b.shape[0]
+        self.reg.exige(b.shape[1] == K, f"{op}: K diferente, A {tuple(a.shape)} x B {tuple(b.shape)}")
+        self.reg.exige(M % 32 == 0 and N % 128 == 0 and K % BLK == 0 and 0 < K <= 4096,
+                       f"{op}: M multiplo de 32, N de 128, K de {BLK} e K <= 4096 (M={M}, N={N}, K={K})")
+        return M, N, K
+
+    def gemm(self, A, B, cru=False):
+        reg = self.reg
+        reg.confere_bloco("A", A); reg.confere_bloco("B", B)
+        (a, ea), (b, eb) = A, B
+        M, N, K = self._formas_gemm("gemm", a, b)
+        if cru:
+            C = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(M, N, dtype=torch.int16, device=a.device))
+            self._lanca("gemm_cru", "jt_gemm", (a, ea, b, eb, None, None, C[0], C[1], M, N, K, 1), dict(A=a, EA=ea, B=b, EB=eb), (M, N))
+        else:
+            C = self._novo_bloco(M, N, a.device)
+            self._lanca("gemm", "jt_gemm", (a, ea, b, eb, C[0], C[1], None, None, M, N, K, 0), dict(A=a, EA=ea, B=b, EB=eb), (M, N))
+        return C
+
+    def _gemm_fundida(self, op, modo, A, B, X=None, saida2=False):
+        reg = self.reg
+        reg.confere_bloco("A", A); reg.confere_bloco("B", B)
+        (a, ea), (b, eb) = A, B
+        M, N, K = self._formas_gemm(op, a, b)
+        ent = dict(A=a, EA=ea, B=b, EB=eb)
+        if X is not None:
+            reg.confere_bloco("X", X)
+            reg.exige(tuple(X[0].shape) == (M, N), f"{op}: X com forma {tuple(X[0].shape)}, esperado {(M, N)}")
+            ent.update(X=X[0], XE=X[1])
+        C = self._novo_bloco(M, N, a.device)
+        C2 = self._novo_bloco(M, N, a.device) if saida2 else (None, None)
+        self._lanca(op, "jt_gemm_f", (a, ea, b, eb, C[0], C[1], None, None, X[0] if X is not None else None,
+                                      X[1] if X is not None else None, C2[0], C2[1], M, N, K, modo), ent, (M, N))
+        return (C, C2) if saida2 else C
+
+    def gemm_soma(self, A, B, X):
+        return self._gemm_fundida("gemm_soma", 2, A, B, X=X)
+
+    def gemm_relu2(self, A, B):
+        return self._gemm_fundida("gemm_relu2", 3, A, B, saida2=True)
+
+    def gemm_relu2_back(self, A, B, Hh):
+        return self._gemm_fundida("gemm_relu2_back", 4, A, B, X=Hh)
+
+    # ---------------------------------------------------------------- re-blocking and element-wise (ops.py:374-432)
+    def transpoe(self, X):
+        self.reg.confere_bloco("X", X)
+        m, E = X
+        R, C = m.shape
+        self.reg.exige(R % 128 == 0 and C % 64 == 0, f"transpoe: linhas {R} nao multiplo de 128 ou colunas {C} nao multiplo de 64")
+        Y = self._novo_bloco(C, R, m.device)
+        self._lanca("transpoe", "jt_transpoe", (m, E, Y[0], Y[1], R, C), dict(X=m, EX=E), (C, R))
+        return Y
+
+    def quant(self, Cc):
+        self.reg.confere_cru("C", Cc)
+        acc, e = Cc
+        R, C = acc.shape
+        self.reg.exige(C % BLK == 0, f"quant: colunas {C} nao multiplo de {BLK}")
+        Y = self._novo_bloco(R, C, acc.device)
+        self._lanca("quant", "jt_quant", (acc, e, Y[0], Y[1], R * C // BLK), dict(acc=acc, e=e), (R, C), longos=(4,))
+        return Y
+
+    def _elem(self, op, fn, ins, nomes):
+        for n, t in zip(nomes, ins):
+            self.reg.confere_bloco(n, t)
+        m0 = ins[0][0]
+        for n, t in zip(nomes[1:], ins[1:]):
+            self.reg.exige(t[0].shape == m0.shape, f"{op}: '{n}' com forma {tuple(t[0].shape)}, esperado {tuple(m0.shape)}")
+        Y = self._novo_bloco(*m0.shape, m0.device)
+        args = [x for t in ins for x in t] + [Y[0], Y[1], m0.numel() // BLK]
+        ent = {f"{n}{s}": x for n, t in zip(nomes, ins) for s, x in zip(("", "E"), t)}
+        self._lanca(op, fn, args, ent, tuple(m0.shape), longos=(len(args) - 1,))
+        return Y
+
+    def soma(self, X, Y):
+        return self._elem("soma", "jt_soma", (X, Y), ("x", "y"))
+
+    # ---- 16-bit residual stream: (int16 mantissa, int8 exponent per block) (ops.py:406-426)
+    def _r16(self, op, fn, args, ent, forma, saida16):
+        m0 = args[0]
+        R, C = forma
+        Y = (torch.empty(R, C, dtype=torch.int16 if saida16 else torch.int8, device=m0.device),
+             torch.empty(R, C // BLK, dtype=torch.int8, device=m0.device))
+        a = list(args) + [Y[0], Y[1], R * C // BLK]
+        self._lanca(op, fn, a, ent, forma, longos=(len(a) - 1,))
+        return Y
+
+    def para16(self, X):
+        self.reg.confere_bloco("x", X)
+        return self._r16("para16", "jt_para16", X, dict(x=X[0], xE=X[1]), tuple(X[0].shape), True)
+
+    def para8(self, X16):
+        self.reg.confere_r16("x16", X16)
+        return self._r16("para8", "jt_para8", X16, dict(x16=X16[0], xE=X16[1]), tuple(X16[0].shape), False)
+
+    def soma16(self, X16, Y):
+        self.reg.confere_r16("x16", X16)
+        self.reg.confere_bloco("y", Y)
+        self.reg.exige(tuple(Y[0].shape) == tuple(X16[0].shape), f"soma16: formas {tuple(X16[0].shape)} e {tuple(Y[0].shape)}")
+        return self._r16("soma16", "jt_soma16", (*X16, *Y), dict(x16=X16[0], y=Y[0]), tuple(X16[0].shape), True)
+
+    def relu2(self, Hh):
+        return self._elem("relu2", "jt_relu2", (Hh,), ("h",))
+
+    def relu2_back(self, Gg, Hh):
+        return self._elem("relu2_back", "jt_relu2_back", (Gg, Hh), ("g", "h"))
+
+    def embed(self, W, tok):
+        self.reg.confere_bloco("W", W)
+        m, E = W
+        V, D = m.shape
+        M = tok.numel()
+        X = self._novo_bloco(M, D, m.device)
+        self._lanca("embed", "jt_embed", (m, E, tok, X[0], X[1], M, D, V), dict(W=m, tok=tok), (M, D))
+        return X
+
+    def um_quente(self, tok, V):
+        M = tok.numel()
+        U = self._novo_bloco(M, V, tok.device)
+        self._lanca("um_quente", "jt_um_quente", (tok, U[0], U[1], M, V), dict(tok=tok), (M, V))
+        return U
+
+    # ---------------------------------------------------------------- rows (ops.py:449-502)
+    def rms(self, X):
+        self.reg.confere_bloco("x", X)
+        m, E = X
+        M, D = m.shape
+        self.reg.exige(D in (128, 256, 512, 1024), f"rms: D={D} fora de {{128, 256, 512, 1024}}")
+        G, _ = g_rms(D)
+        Y = self._novo_bloco(M, D, m.device)
+        r = torch.empty(M, dtype=torch.int32, device=m.device)
+        emax = torch.empty(M, dtype=torch.int32, device=m.device)
+        self._lanca("rms", "jt_rms", (m, E, Y[0], Y[1], r, emax, M, D, int(math.log2(D)), G), dict(x=m, xE=E), (M, D))
+        return Y, (r, emax)
+
+    def rms_back(self, Gg, Y, cache):
+        self.reg.confere_bloco("g", Gg); self.reg.confere_bloco("y", Y)
+        (g, gE), (y, yE) = Gg, Y
+        M, D = g.shape
+        G, GB = g_rms(D)
+        O = self._novo_bloco(M, D, g.device)
+        self._lanca("rms_back", "jt_rms_back", (g, gE, y, yE, cache[0], cache[1], O[0], O[1], M, D, int(math.log2(D)), G, GB),
+                    dict(g=g, gE=gE, y=y, yE=yE, r=cache[0], emax=cache[1]), (M, D))
+        return O
+
+    def atencao(self, QKV, Bt, T, H):
+        self.reg.confere_bloco("qkv", QKV)
+        m, E = QKV
+        D = m.shape[1] // 3
+        self.reg.exige(T <= 256 and T % 64 == 0 and D % H == 0 and D // H == 4 and m.shape[0] == Bt * T,
+                       f"atencao: T={T} (<=256, multiplo de 64), D={D}, H={H} (largura de cabeca 4)")
+        oacc = torch.empty(Bt * T, D, dtype=torch.int32, device=m.device)
+        oe = torch.empty(Bt * T, D, dtype=torch.int16, device=m.device)
+        P = torch.empty(Bt * H, T, T, dtype=torch.uint8, device=m.device)
+        self._lanca("atencao", "jt_atencao", (m, E, oacc, oe, P, Bt, T, H, D, GA), dict(qkv=m, qkvE=E), (Bt * T, D))
+        return (oacc, oe), P
+
+    def atencao_back(self, GO, QKV, P, Bt, T, H):
+        self.reg.confere_bloco("go", GO); self.reg.confere_bloco("qkv", QKV)
+        (gm, gE), (m, E) = GO, QKV
+        D = gm.shape[1]
+        acc = torch.empty(Bt * T, 3 * D, dtype=torch.int32, device=m.device)
+        e = torch.empty(Bt * T, 3 * D, dtype=torch.int16, device=m.device)
+        self._lanca("atencao_back", "jt_atencao_back", (gm, gE, m, E, P, acc, e, Bt, T, H, D, GA, int(ATENCAO_LIMITE)),
+                    dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D))
+        return acc, e
+
+    def softmax_ce(self, L, alvo):
+        self.reg.confere_cru("logits", L)
+        acc, e = L
+        M, V = acc.shape
+        self.reg.exige(V in (128, 256, 512, 1024) and V % BLK == 0, f"softmax_ce: V={V}")
+        g = self._novo_bloco(M, V, acc.device)
+        d = torch.empty(M, dtype=torch.int32, device=acc.device)
+        s = torch.empty(M, dtype=torch.int32, device=acc.device)
+        self._lanca("softmax_ce", "jt_softmax_ce", (acc, e, alvo, g[0], g[1], d, s, M, V, int(math.log2(M))),
+                    dict(acc=acc, e=e, alvo=alvo), (M, V))
+        return g, d, s
+
+    # ---------------------------------------------------------------- optimizer, in place (ops.py:504-515)
+    def momento(self, Gc, Mom):
+        self.reg.confere_cru("grad", Gc); self.reg.confere_bloco("momento", Mom)
+        n = Mom[0].numel() // BLK
+        self._lanca("momento", "jt_momento", (Gc[0], Gc[1], Mom[0], Mom[1], n), dict(g=Gc[0], ge=Gc[1]), tuple(Mom[0].shape), longos=(4,))
+        return Mom
+
+    def peso(self, W, Mom, R, k, ef):
+        for n, t in (("W", W), ("momento", Mom), ("residuo", R)):
+            self.reg.confere_bloco(n, t)
+        n = W[0].numel() // BLK
+        self._lanca("peso", "jt_peso", (W[0], W[1], Mom[0], Mom[1], R[0], R[1], k, int(ef), n), dict(), tuple(W[0].shape), longos=(8,))
+        return W, R

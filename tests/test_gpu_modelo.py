@@ -1,0 +1,101 @@
+"""Model-level parity of the HIP path.
+
+* two full training steps (522 ops each: forward, backward, optimizer) at the reference model shape
+  (V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=8, BLK=128): every op output equals the spec's
+  (trace written from OpsRef + Modelo.passo, the reference's `conferir 2` protocol, treino_cuda.py:48-60);
+* the hipGraph-captured step replays to the same bits as eager steps, for every replay, with eager work and
+  synchronization between replays; and the per-step (d_alvo, soma) of the golden loss trace;
+* a token outside the vocabulary inside a replayed graph raises ErroJatai naming op embed, scope
+  "forward / embedding", row 401, value 300 (the reference's teste_erro_grafo.py:13-30).
+"""
+import numpy as np
+import pytest
+import torch
+
+import recipe as R
+import traco as TR
+from backends import LOGS, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops(vigiar=False):
+    from jatai_amd import ops as O
+    from jatai_amd.registro import Registro
+    O.BLK = 128
+    reg = Registro(LOGS, "modelo", vigiar=vigiar, eco=False)
+    return O.OpsHip(reg), reg
+
+
+def test_dois_passos_vs_spec():
+    ops, reg = _ops()
+    reg.novo_passo(0)
+    _, init, passos = TR.roda(ops, reg, "cuda", 2, host)
+    reg.fim_passo()
+    TR.confere(init, passos)
+
+
+def _estado(m):
+    return [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
+
+
+def test_grafo_igual_ao_eager_e_ao_spec():
+    from jatai_amd.modelo import Modelo, PassoGravado
+    g = TR.gold()
+    f = g["forma"]
+    n = min(len(g["passos"]), 6)
+    ops, reg = _ops()
+    dev = "cuda"
+    mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, ops, reg)
+    eager, grafado = mk(), mk()
+    for m in (eager, grafado):
+        m.perda_inteira = True
+    hist_e, hist_g = [], []
+    reg.novo_passo(0)
+    for p in range(n):
+        tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], dev)
+        d, s = eager.passo(tok, alvo, k_lr=f["k_lr"])
+        hist_e.append((R.sha(host(d)), R.sha(host(s))))
+    reg.fim_passo()
+    tok, alvo = TR.lote(0, f["Bt"], f["T"], f["V"], dev)
+    d, s = grafado.passo(tok, alvo, k_lr=f["k_lr"])
+    hist_g.append((R.sha(host(d)), R.sha(host(s))))
+    grafado.perda_inteira = False
+    pg = PassoGravado(grafado, f["Bt"], f["T"], f["k_lr"])
+    perdas = []
+    for p in range(1, n):
+        reg.novo_passo(p)
+        tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], dev)
+        perdas.append(float(pg(tok, alvo)))
+        torch.cuda.synchronize()
+        hist_g.append((R.sha(host(pg.d_alvo)), R.sha(host(pg.soma))))
+        reg.fim_passo()
+        _ = torch.ones(1024, device=dev).sum().item()        # eager work between replays
+    assert hist_g == hist_e, "graph replays differ from eager steps"
+    assert _estado(grafado) == _estado(eager), "weights / momentum / residuals differ after graph replays"
+    for p in range(n):
+        assert [hist_e[p][0], hist_e[p][1]] == [g["passos"][p]["d_alvo"], g["passos"][p]["soma"]], f"step {p} vs spec"
+    for p, x in enumerate(perdas, start=1):
+        assert abs(x - g["passos"][p]["perda"]) <= 1e-12 * abs(g["passos"][p]["perda"])
+
+
+def test_erro_no_grafo():
+    from jatai_amd.modelo import Modelo, PassoGravado
+    from jatai_amd.registro import ErroJatai
+    g = TR.gold()
+    f = g["forma"]
+    ops, reg = _ops()
+    m = Modelo(f["V"], f["D"], f["H"], f["FF"], 2, 0, "cuda", ops, reg)
+    tok, alvo = TR.lote(0, 8, 128, 256, "cuda")
+    reg.novo_passo(0); m.passo(tok, alvo, k_lr=4); reg.fim_passo()
+    pg = PassoGravado(m, 8, 128, 4)
+    reg.novo_passo(1); pg(tok, alvo); reg.fim_passo()
+    ruim = tok.clone()
+    ruim[3, 17] = 300
+    reg.novo_passo(2)
+    with pytest.raises(ErroJatai) as e:
+        pg(ruim, alvo)
+        reg.fim_passo()
+    msg = str(e.value)
+    assert "forward / embedding" in msg and "linha 401, coluna 0" in msg and "valor    : 300" in msg, msg
+    assert "operacao : embed" in msg
