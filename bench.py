@@ -1,0 +1,206 @@
+"""Throughput of the INT8 integer training step on one MI355X, with the roofline of its dominant kernel and the CPU
+oracle timed on the same host as the baseline.
+
+A step is one hipGraph replay of the whole training step (forward, backward, momentum + error-feedback update of
+every weight) over one synthetic batch of uniform random token ids, following the reference's tokens/s protocol
+(jatai_cuda/treino_cuda.py:119-151): copy the batch into the graph's input buffers, clear the device error record,
+replay, read the error record. Batches are resident in HBM before the timed region.
+
+Workloads (--config):
+  r   reference-native shape: 12 layers, D=256, 64 heads x 4, FF=1024, T=128, Bt=16 (2048 tokens), BLK=128 --
+      the configuration of the reference's published 34,248 tokens/s (GTX 1650, README.md:87)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config r] [--no-cpu]
+Prints one JSON line.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "INT8 train tokens/s (12L, 2048 tok); block-32 GEMM TOPS & % i8 MFMA peak"
+PEAK_I8 = 5.0e15          # MI355X dense int8 MFMA, ops/s
+PEAK_HBM = 8.0e12         # bytes/s
+
+CONFIGS = {
+    "r": dict(V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=16, BLK=128, r16=False,
+              nome="reference-native 12L D256 H64x4 FF1024 T128 Bt16 BLK128", publicado=34248.0),
+}
+
+
+def args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="r", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def gemm_formas(c):
+    """(name, M, N, K, raw) of every GEMM of one step (modelo.py:51-134), one entry per distinct shape, with counts."""
+    M, D, FF, V, L = c["Bt"] * c["T"], c["D"], c["FF"], c["V"], c["L"]
+    f = {}
+
+    def add(n, m, nn, k, cru, cont):
+        f[n] = (m, nn, k, cru, f.get(n, (0, 0, 0, 0, 0))[4] + cont)
+    add("fwd qkv", M, 3 * D, D, False, L)
+    add("fwd out-proj+soma", M, D, D, False, L)
+    add("fwd ffn-up+relu2", M, FF, D, False, L)
+    add("fwd ffn-down+soma", M, D, FF, False, L)
+    add("logits", M, V, D, True, 1)
+    add("dX out", M, D, V, False, 1)
+    add("dX ffn-down", M, FF, D, False, L)
+    add("dX ffn-up", M, D, FF, False, L)
+    add("dX out-proj", M, D, D, False, L)
+    add("dX qkv", M, D, 3 * D, False, L)
+    add("dW qkv", 3 * D, D, M, True, L)
+    add("dW out-proj", D, D, M, True, L)
+    add("dW ffn-up", FF, D, M, True, L)
+    add("dW ffn-down", D, FF, M, True, L)
+    add("dW out", V, D, M, True, 1)
+    add("dW emb", V, D, M, True, 1)
+    return f
+
+
+def mede_gemms(O, ops, c, rep=20):
+    """Average launch duration of each GEMM shape with HIP events on the launch stream (the default stream,
+    which torch.cuda.Event records on), inputs resident in HBM, and 2MNK / duration."""
+    import numpy as np
+    import torch
+    blk = c["BLK"]
+    out = {}
+    g = torch.Generator().manual_seed(3)
+
+    def bloco(R, C, e0):
+        m = torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda()
+        E = (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda()
+        return m, E
+    for nome, (M, N, K, cru, cont) in gemm_formas(c).items():
+        A, B = bloco(M, K, -8), bloco(N, K, -12)
+        for _ in range(3):
+            ops.gemm(A, B, cru=cru)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(rep):
+            ops.gemm(A, B, cru=cru)
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / rep
+        out[nome] = dict(M=M, N=N, K=K, cru=cru, por_passo=cont, ms=ms, tops=2 * M * N * K / (ms * 1e-3) / 1e12)
+    return out
+
+
+def cpu_baseline(c, segundos):
+    """The CPU oracle (int64 C++ restatement of the spec, OpenMP) running the same model's training step on a
+    bounded sample: batches of 2 sequences until `segundos` of wall time, tokens/s = tokens / wall."""
+    import torch
+    from jatai_amd import ops as O
+    from jatai_amd.modelo import Modelo
+    from oracle.ops_oracle import OpsOraculo
+
+    class Nada:
+        def trecho(self, n):
+            import contextlib
+            return contextlib.nullcontext()
+    O.BLK = c["BLK"]
+    m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, "cpu", OpsOraculo(c["BLK"]), Nada(), r16=c["r16"])
+    g = torch.Generator().manual_seed(11)
+    bt = 2
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        x = torch.randint(0, c["V"], (bt, c["T"] + 1), generator=g)
+        m.passo(x[:, :-1], x[:, 1:], k_lr=4)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= segundos:
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=n * bt * c["T"] / dt, unit="tokens/s", cores=threads, kind="port",
+                sample=f"{n} training steps of the same {c['L']}-layer model at Bt={bt} x T={c['T']} on the int64 CPU oracle "
+                       f"(oracle/jatai_oracle.cpp, OpenMP {threads} threads), {dt:.1f} s")
+
+
+def main():
+    a = args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the multi-GPU path is a design "
+              f"(DESIGN.md), not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from jatai_amd import ops as O
+    from jatai_amd.modelo import Modelo, PassoGravado
+    from jatai_amd.registro import Registro
+
+    c = CONFIGS[a.config]
+    O.BLK = c["BLK"]
+    reg = Registro("/tmp/jatai_bench", "bench", eco=False)
+    ops = O.OpsHip(reg)
+    dev = "cuda"
+    m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, dev, ops, reg, r16=c["r16"])
+    g = torch.Generator().manual_seed(1)
+    nlotes = 6
+    lotes = []
+    for _ in range(nlotes):
+        x = torch.randint(0, c["V"], (c["Bt"], c["T"] + 1), generator=g).to(dev)
+        lotes.append((x[:, :-1].contiguous(), x[:, 1:].contiguous()))
+    reg.novo_passo(0)
+    m.passo(*lotes[0], k_lr=4)
+    reg.fim_passo()
+    pg = PassoGravado(m, c["Bt"], c["T"], 4)
+    nlanc = len(pg.lancamentos)
+
+    def passo(i):
+        reg.novo_passo(i)
+        perda = pg(*lotes[i % nlotes])
+        reg.fim_passo()
+        return perda
+    for i in range(a.warmup):
+        passo(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        perda = passo(i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    perda = float(perda)
+    tokens = c["Bt"] * c["T"]
+    tps = tokens * a.steps / dt
+
+    gem = mede_gemms(O, ops, c)
+    tot_gemm_ms = sum(v["ms"] * v["por_passo"] for v in gem.values())
+    dom_nome, dom = max(gem.items(), key=lambda kv: kv[1]["ms"] * kv[1]["por_passo"])
+    achieved = 2 * dom["M"] * dom["N"] * dom["K"] / (dom["ms"] * 1e-3)
+    roof = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_I8 / 1e12, "unit": "TOP/s",
+            "frac": achieved / PEAK_I8, "traffic": None, "kernel": f"k_gemm {dom_nome} M={dom['M']} N={dom['N']} K={dom['K']}",
+            "avg_ms": dom["ms"]}
+    res = {"metric": METRIC, "value": tps, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": dt / a.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": tps / c["publicado"] if c.get("publicado") else None, "dtype": "int8",
+           "data": "synthetic: uniform random token ids, random-init weights (modelo.py init, seed 0)",
+           "config": {"workload": c["nome"], "layers": c["L"], "d_model": c["D"], "heads": c["H"], "ffn": c["FF"],
+                      "vocab": c["V"], "seq_len": c["T"], "batch": c["Bt"], "tokens_per_step": tokens, "block": c["BLK"],
+                      "graph_launches": nlanc, "parallelism": "single GPU"},
+           "loss_last_step": perda,
+           "roofline": roof,
+           "gemm_shapes": {k: {"M": v["M"], "N": v["N"], "K": v["K"], "ms": round(v["ms"], 5), "TOPS": round(v["tops"], 2),
+                               "pct_i8_peak": round(100 * v["tops"] * 1e12 / PEAK_I8, 2), "per_step": v["por_passo"]}
+                           for k, v in gem.items()},
+           "gemm_ms_per_step_eager_sum": tot_gemm_ms}
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(c, a.cpu_seconds)
+        res["speedup_vs_cpu_baseline"] = tps / res["cpu_baseline"]["value"]
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

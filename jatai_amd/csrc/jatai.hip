@@ -28,12 +28,34 @@ __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long lo
 
 static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
-static int g_alvo_wg = 1024;            // split-K target number of workgroups (raw GEMM output)
+static int g_alvo_wg = 512;             // GEMM K-split target: workgroups of 4 waves wanted per launch
 static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
 
 static int fim() { return (int)hipGetLastError(); }
+// Every kernel moves 8- or 16-byte vectors: operands must be 16-byte aligned (torch allocations are 256-byte
+// aligned). A misaligned pointer is rejected on the host with hipErrorInvalidValue.
+static bool alinhado(const void* p) { return ((uintptr_t)p & 15) == 0; }
+template <typename... P>
+static bool alinhados(P... p) { return (alinhado(p) && ...); }
 static unsigned grade_elem(long long nblocos) { return (unsigned)((nblocos * g_blk + 2047) / 2048); }
 static int ilog2(long long n) { int l = 0; while ((2LL << l) <= n) l++; return l; }
+
+// Dynamic LDS above 64 KiB must be allowed per kernel (gfx950 has 160 KiB per CU): raised once per kernel and
+// size, remembered by kernel address (every k_gemm instantiation has the same function type).
+template <typename K>
+static void lds_max(K* k, size_t lds) {
+    static const void* chave[64];
+    static size_t feito[64];
+    static int n = 0;
+    if (lds <= 65536) return;
+    const void* f = reinterpret_cast<const void*>(k);
+    int i = 0;
+    while (i < n && chave[i] != f) i++;
+    if (i < n && feito[i] >= lds) return;
+    hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (i == n && n < 64) { chave[n] = f; feito[n] = lds; n++; }
+    else if (i < n) feito[i] = lds;
+}
 
 #define POR_BLK(CHAMADA) (g_blk == 32 ? (CHAMADA(32)) : (CHAMADA(128)))
 
@@ -53,7 +75,7 @@ int jt_erro_limpa() {
 }
 int jt_sincroniza() { return (int)hipDeviceSynchronize(); }
 void jt_stream(void* st) { g_stream = (hipStream_t)st; }
-void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 1; }
+void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 512; }
 void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one tile shape; kept for the interface
 void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
 int jt_res_estocastico(int ligado) { return ligado ? (int)hipErrorNotSupported : 0; }
@@ -70,30 +92,31 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
               const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
     using namespace gemm;
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
+    if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk;
-    int partes = 1;
+    // K-splits inside a workgroup: up to 4, while the grid has fewer than g_alvo_wg x 4 waves and each split
+    // keeps at least two K-blocks
     const long long tiles = (long long)(M / BM) * (N / BN);
-    if (modo == 1)
-        while (partes * 2 <= nb && nb % (partes * 2) == 0 && tiles * partes * 2 <= g_alvo_wg) partes *= 2;
-    if (partes > 1) {
-        const long long n = (long long)M * N;
-        k_zera32<<<(unsigned)((n / 4 + 255) / 256 + 1), 256, 0, g_stream>>>((int*)C32, n);
-    }
-    const dim3 grade(N / BN, M / BM, partes);
-    const size_t lds = gemm_lds(nb);
-    const int kpart = nb / partes;
+    // (two K-splits at most: each holds two 21 KiB stage buffers in LDS, 160 KiB per workgroup)
+    const int ksmax = 2;
+    int ks = 1;
+    while (ks < ksmax && tiles * 4 * ks < (long long)g_alvo_wg * 4 && nb >= 4 * ks) ks *= 2;
+    const dim3 grade(N / BN, M / BM);
+    const size_t lds = gemm_lds(nb, ks);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
-             (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kpart, kid
-#define L(BL, MD) k_gemm<BL, MD><<<grade, NT, lds, g_stream>>>(ARGS)
-#define LB(MD) (g_blk == 32 ? L(32, MD) : L(128, MD))
+             (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kid
+#define L(BL, MD, S) (lds_max(k_gemm<BL, MD, S>, lds), k_gemm<BL, MD, S><<<grade, 256 * S, lds, g_stream>>>(ARGS))
+#define LS2(BL, MD) (ks == 1 ? L(BL, MD, 1) : L(BL, MD, 2))
+#define LB2(MD) (g_blk == 32 ? LS2(32, MD) : LS2(128, MD))
     switch (modo) {
-        case 0: LB(0); break;
-        case 1: LB(1); break;
-        case 2: LB(2); break;
-        case 3: LB(3); break;
-        case 4: LB(4); break;
+        case 0: LB2(0); break;
+        case 1: LB2(1); break;
+        case 2: LB2(2); break;
+        case 3: LB2(3); break;
+        case 4: LB2(4); break;
     }
-#undef LB
+#undef LB2
+#undef LS2
 #undef L
 #undef ARGS
     return fim();
@@ -106,6 +129,7 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
 // ---------------------------------------------------------------------------------------------- element-wise
 int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(acc, e, m, E)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_quant<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (int8_t*)m, (int8_t*)E, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -113,6 +137,7 @@ int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos
 }
 int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(xm, xE, ym, yE, zm, zE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_soma<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
                                                                       (int8_t*)zm, (int8_t*)zE, nblocos, kid), 0)
     POR_BLK(C);
@@ -121,6 +146,7 @@ int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void
 }
 int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(hm, hE, am, aE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_relu2<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)hm, (const int8_t*)hE, (int8_t*)am, (int8_t*)aE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -128,6 +154,7 @@ int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nbloc
 }
 int jt_relu2_back(const void* gm, const void* gE, const void* hm, const void* hE, void* om, void* oE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(gm, gE, hm, hE, om, oE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_relu2_back<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)hm, \
                                                                             (const int8_t*)hE, (int8_t*)om, (int8_t*)oE, nblocos, kid), 0)
     POR_BLK(C);
@@ -136,6 +163,7 @@ int jt_relu2_back(const void* gm, const void* gE, const void* hm, const void* hE
 }
 int jt_momento(const void* gacc, const void* ge, void* Mm, void* ME, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(gacc, ge, Mm, ME)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_momento<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int*)gacc, (const int16_t*)ge, (int8_t*)Mm, (int8_t*)ME, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -143,6 +171,7 @@ int jt_momento(const void* gacc, const void* ge, void* Mm, void* ME, long long n
 }
 int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* RE, int k_lr, int ef, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(Wm, WE, Mm, ME, Rm, RE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_peso<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((int8_t*)Wm, (int8_t*)WE, (const int8_t*)Mm, (const int8_t*)ME, (int8_t*)Rm, \
                                                                       (int8_t*)RE, k_lr, ef, nblocos, kid), 0)
     POR_BLK(C);
@@ -151,6 +180,7 @@ int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* 
 }
 int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(xm, xE, zm, zE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_para16<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (int16_t*)zm, (int8_t*)zE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -158,6 +188,7 @@ int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblo
 }
 int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(xm, xE, ym, yE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_para8<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int16_t*)xm, (const int8_t*)xE, (int8_t*)ym, (int8_t*)yE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -165,6 +196,7 @@ int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nbloc
 }
 int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
+    if (!alinhados(xm, xE, ym, yE, zm, zE)) return (int)hipErrorInvalidValue;
 #define C(BL) (k_soma16<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int16_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
                                                                         (int16_t*)zm, (int8_t*)zE, nblocos, kid), 0)
     POR_BLK(C);
@@ -173,6 +205,7 @@ int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, vo
 }
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid) {
     if (R <= 0 || C <= 0 || R % 128 || C % 64 || C % g_blk) return (int)hipErrorInvalidValue;
+    if (!alinhados(X, EX, Y, EY)) return (int)hipErrorInvalidValue;
 #define L(BL) (k_transpoe<BL><<<dim3(C / 64, R / 128), 256, 0, g_stream>>>((const int8_t*)X, (const int8_t*)EX, (int8_t*)Y, (int8_t*)EY, R, C, kid), 0)
     POR_BLK(L);
 #undef L
@@ -180,6 +213,7 @@ int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, 
 }
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid) {
     if (M <= 0 || D % g_blk || D % 16) return (int)hipErrorInvalidValue;
+    if (!alinhados(Wm, WE, tok, Xm, XE)) return (int)hipErrorInvalidValue;
     const unsigned g = (unsigned)(((long long)M * (D / 16) + 255) / 256);
 #define L(BL) (k_embed<BL><<<g, 256, 0, g_stream>>>((const int8_t*)Wm, (const int8_t*)WE, (const int*)tok, (int8_t*)Xm, (int8_t*)XE, M, D, V, kid), 0)
     POR_BLK(L);
@@ -188,6 +222,7 @@ int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE
 }
 int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
     if (M <= 0 || V % g_blk || V % 16) return (int)hipErrorInvalidValue;
+    if (!alinhados(tok, U, UE)) return (int)hipErrorInvalidValue;
     const unsigned g = (unsigned)(((long long)M * (V / 16) + 255) / 256);
 #define L(BL) (k_um_quente<BL><<<g, 256, 0, g_stream>>>((const int*)tok, (int8_t*)U, (int8_t*)UE, M, V, kid), 0)
     POR_BLK(L);
@@ -207,6 +242,7 @@ int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
     }
 int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid) {
     if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (!alinhados(Xm, XE, Ym, YE, cr, cemax)) return (int)hipErrorInvalidValue;
 #define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                               \
         if (g_blk == 32) k_rms<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE, \
                                                                      (int*)cr, (int*)cemax, M, log2D, G, kid);                       \
@@ -219,6 +255,7 @@ int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* c
 int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om, void* oE, int M,
                 int D, int log2D, int G, int GB, int kid) {
     if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE)) return (int)hipErrorInvalidValue;
 #define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                       \
         if (g_blk == 32) k_rms_back<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,             \
             (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid);                          \
@@ -231,6 +268,7 @@ int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, 
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V, int log2M,
                   int kid) {
     if (M <= 0 || V % g_blk) return (int)hipErrorInvalidValue;
+    if (!alinhados(acc, e, alvo, gm, gE, d_alvo, soma)) return (int)hipErrorInvalidValue;
 #define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                    \
         if (g_blk == 32) k_softmax_ce<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (const int*)alvo,           \
             (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid);                                                           \
@@ -244,6 +282,7 @@ int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, vo
 // ---------------------------------------------------------------------------------------------- attention
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
     if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd != 4) return (int)hipErrorNotSupported;
     if (T <= 128)
@@ -255,6 +294,7 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
     if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd != 4) return (int)hipErrorNotSupported;
     const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);

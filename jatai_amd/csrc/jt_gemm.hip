@@ -5,147 +5,227 @@
 // sa = RA_i - ea_ib, sb = RB_j - eb_jb, round half to even; base_ij = RA_i + RB_j - 4.
 //
 // The rounding runs in fp32, where it is exact: |p| < 2^21, so p, p * 2^(4 - s) (a power-of-two scale) and
-// its nearest-even integer (v_rndne_f32) are all representable, and for s >= 31 the scaled value is below 1/2
-// and rounds to 0 exactly as rnd(., s >= 31) does. Per output and K-block this is add3 (the shift), cvt,
-// ldexp, rndne, cvt, add: six VALU ops, against ~9 for the integer form. This per-block VALU epilogue, not
-// the MFMA, bounds the kernel.
+// its nearest-even integer (v_rndne_f32) are all representable, and for s >= 26 the scaled value is below 1/2
+// and rounds to 0 exactly as rnd(., s) does. The shift n = 4 - sa - sb is one add of two precomputed terms, so
+// per output and K-block the epilogue is add, cvt, ldexp, rndne, cvt, add: six VALU ops (~9 in integer form).
+// This per-block VALU epilogue, not the MFMA, bounds the kernel.
 //
-// Tiling: a workgroup of 4 waves owns a 32 x 128 output tile (one 128-column block at BLK=128, four at
-// BLK=32); each wave a 32 x 32 sub-tile of 2 x 2 MFMA 16x16 tiles, with A/B fragments read straight from
-// global memory (each lane 8 contiguous bytes of one row) and exponents staged once in LDS. After the K loop
-// the accumulators go through LDS into a row-block layout (16 consecutive columns per lane) where the block
-// quantization and the fused epilogues run:
-//   MODO 0 block output | 1 raw output (split-K over gridDim.z with atomics into a zeroed buffer)
-//   2 + residual add (soma) | 3 + ReLU^2 second output | 4 ReLU^2 backward with H
+// Tiling: a workgroup of 4 x KS waves owns a 32 x 128 output tile (one 128-column block at BLK=128, four at
+// BLK=32). K is walked in stages of 128 bytes per row (4 blocks at BLK=32, 1 at BLK=128): wave group g
+// (4 waves) takes stages s = g (mod KS) and stages each one through its own double-buffered LDS tile of
+// 160 rows (32 of A, 128 of B) with coalesced 16-byte loads, issued one stage ahead of the MFMAs; wave w of the
+// group computes the 32 x 32 sub-tile of columns 32 w as 2 x 2 MFMA 16x16x32 tiles. The KS partial sums are
+// added in LDS (integer addition, exact in any order). The summed tile is then read in a row-block layout
+// (16 consecutive columns per lane) where the block quantization and the fused epilogues run:
+//   MODO 0 block output | 1 raw output | 2 + residual add (soma) | 3 + ReLU^2 second output
+//   4 ReLU^2 backward with H
 // The fused epilogues compute exactly the separate ops on the quantized GEMM output (jatai_cuda.cu:195-200).
 #include "jt_comum.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace gemm {
-constexpr int BM = 32, BN = 128, NT = 256, PAD = 4;
+constexpr int BM = 32, BN = 128, PAD = 4;
+constexpr int SK = 128;                  // bytes of K per row and stage
+constexpr int LD = SK + 8;               // LDS row stride of a stage tile (8-byte pad spreads rows over the banks)
+constexpr int ROWS = BM + BN;            // rows of a stage tile: 32 of A then 128 of B
+constexpr int STAGE = ROWS * LD;         // bytes of one stage buffer
 }
 
-template <int BLK, int MODO>
-__global__ void __launch_bounds__(256) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
-                                              const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
-                                              int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
-                                              const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
-                                              int N, int K, int kpart, int kid) {
+template <int BLK, int MODO, int KS>
+__global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
+                                                   const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
+                                                   int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
+                                                   const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
+                                                   int N, int K, int kid) {
     using namespace gemm;
     extern __shared__ __align__(16) char smem[];
-    const int nb = K / BLK;
-    // LDS: ea as int32 [nb][BM], eb as int8 [nb][BN], RA [BM], RB [BN]; the accumulator tile reuses the front.
-    int* ea_s = reinterpret_cast<int*>(smem);
-    int8_t* eb_s = reinterpret_cast<int8_t*>(smem + (size_t)nb * BM * 4);
-    int* ra_s = reinterpret_cast<int*>(smem + (size_t)nb * BM * 4 + (size_t)nb * BN);
+    const int nb = K / BLK, ns = (K + SK - 1) / SK;
+    constexpr int BPS = SK / BLK;                                   // blocks per stage
+    constexpr int KST = BLK / 32;                                   // MFMA k-steps per block
+    // LDS: RA [BM], RB [BN] int32 (live to the end); shift terms na[b][i] = ea_ib + 4 - RA_i (int32) and
+    // nb[b][j] = eb_jb - RB_j (int8), clamped at -100 (n = na + nb <= -22 scales |p| < 2^21 below 1/2, i.e. to
+    // 0, as rnd(., s >= 26) does); then the stage buffers [KS][2][STAGE], which first hold the raw exponent
+    // bytes and at the end the KS accumulator tiles.
+    int* ra_s = reinterpret_cast<int*>(smem);
     int* rb_s = ra_s + BM;
+    int* na_s = rb_s + BN;
+    int8_t* nb_s = reinterpret_cast<int8_t*>(na_s + (size_t)nb * BM);
+    char* buf = reinterpret_cast<char*>(nb_s) + (((size_t)nb * BN + 15) & ~(size_t)15);
+    int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nb], EB rows [BN][nb]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
-    for (int i = tid; i < BM * nb; i += NT) { const int r = i / nb, b = i % nb; ea_s[b * BM + r] = EA[(size_t)(row0 + r) * nb + b]; }
-    for (int i = tid; i < BN * nb; i += NT) { const int r = i / nb, b = i % nb; eb_s[b * BN + r] = EB[(size_t)(col0 + r) * nb + b]; }
-    __syncthreads();
-    if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, ea_s[b * BM + tid]); ra_s[tid] = m; }
-    else if (tid >= 64 && tid < 64 + BN) { const int c = tid - 64; int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)eb_s[b * BN + c]); rb_s[c] = m; }
-    __syncthreads();
-
-    // lane coordinates inside the wave's 32 x 32 sub-tile
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
-    const int wc = wave * 32;                                       // wave's first column in the WG tile
-    int k0[2][2][4];                                                // 4 - RA_i - RB_j per output
+    const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
+    char* meu = buf + (size_t)g * 2 * STAGE;                        // this group's two stage buffers
+
+    // stage loads: thread tg of a group moves 16-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
+    // (row 0..31 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
+    const int vr = tg >> 3, vc = (tg & 7) * 16;
+    const int8_t* src[5];
+    src[0] = A + (size_t)(row0 + vr) * K + vc;
 #pragma unroll
-    for (int ti = 0; ti < 2; ti++)
+    for (int i = 1; i < 5; i++) src[i] = B + (size_t)(col0 + vr + 32 * (i - 1)) * K + vc;
+    int4 reg[5];
+    auto busca = [&](int st) {
+        const bool ok = st * SK + vc < K;
 #pragma unroll
-        for (int tj = 0; tj < 2; tj++)
+        for (int i = 0; i < 5; i++) reg[i] = ok ? *reinterpret_cast<const int4*>(src[i] + (size_t)st * SK) : make_int4(0, 0, 0, 0);
+    };
+    auto guarda = [&](int par) {
+        char* d = meu + par * STAGE + vr * LD + vc;
 #pragma unroll
-            for (int i = 0; i < 4; i++) k0[ti][tj][i] = 4 - ra_s[16 * ti + 4 * lg + i] - rb_s[wc + 16 * tj + lr];
-    int acc[2][2][4] = {};
-    const int8_t* pa0 = A + (size_t)(row0 + lr) * K + 8 * lg;
-    const int8_t* pa1 = pa0 + (size_t)16 * K;
-    const int8_t* pb0 = B + (size_t)(col0 + wc + lr) * K + 8 * lg;
-    const int8_t* pb1 = pb0 + (size_t)16 * K;
-    const int b_ini = blockIdx.z * kpart, b_fim = min(nb, b_ini + kpart);
-    constexpr int KS = BLK / 32;                                    // MFMA k-steps per block
-    long fa[2][KS], fb[2][KS];
-    auto carrega = [&](int b) {
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const size_t off = (size_t)b * BLK + 32 * s;
-            fa[0][s] = *reinterpret_cast<const long*>(pa0 + off);
-            fa[1][s] = *reinterpret_cast<const long*>(pa1 + off);
-            fb[0][s] = *reinterpret_cast<const long*>(pb0 + off);
-            fb[1][s] = *reinterpret_cast<const long*>(pb1 + off);
+        for (int i = 0; i < 5; i++) {
+            int2* q = reinterpret_cast<int2*>(d + 32 * i * LD);
+            q[0] = make_int2(reg[i].x, reg[i].y);
+            q[1] = make_int2(reg[i].z, reg[i].w);
         }
     };
-    if (b_ini < b_fim) carrega(b_ini);
-    for (int b = b_ini; b < b_fim; b++) {
-        v4i p[2][2];
-#pragma unroll
-        for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-            for (int tj = 0; tj < 2; tj++) {
-                p[ti][tj] = v4i{0, 0, 0, 0};
-#pragma unroll
-                for (int s = 0; s < KS; s++) p[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti][s], fb[tj][s], p[ti][tj], 0, 0, 0);
-            }
-        if (b + 1 < b_fim) carrega(b + 1);                          // next block's fragments in flight
-        const v4i ea0 = *reinterpret_cast<const v4i*>(ea_s + b * BM + 4 * lg);
-        const v4i ea1 = *reinterpret_cast<const v4i*>(ea_s + b * BM + 16 + 4 * lg);
-        const int eb0 = eb_s[b * BN + wc + lr], eb1 = eb_s[b * BN + wc + 16 + lr];
-#pragma unroll
-        for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-            for (int tj = 0; tj < 2; tj++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = k0[ti][tj][i] + (ti ? ea1[i] : ea0[i]) + (tj ? eb1 : eb0);     // 4 - sa - sb
-                    acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
-                }
-    }
+    if (g < ns) busca(g);                                           // first stage in flight during the exponent staging
 
-    // ---- output stage: accumulators to LDS, then 16 consecutive columns of one row per lane
-    __syncthreads();
-    int* acc_s = reinterpret_cast<int*>(smem);                     // [BM][BN + PAD]
-    // RA/RB must survive: copy them to registers first
-    const int orow = tid >> 3, oc = (tid & 7) * 16;
-    const int ra = ra_s[orow];
-    int base[16];
+    // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
+    const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
+    const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
+    const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
+    int xin[16], exin = 0;
+    if constexpr (MODO == 2 || MODO == 4) {
+        if (tid < 256) { le_i8(Xm + o, xin); exin = XE[oe]; }
+    }
+    // exponents of the tile's 32 rows of A and 128 rows of B: two contiguous spans (32 nb and 128 nb bytes,
+    // multiples of 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span
+    // re-read its last vector and store it to a junk slot after the span, so neither side branches
+    {
+        const int nva = 2 * nb, nvt = 10 * nb;
+        const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
+        const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
+        for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
+            int4 t[4];
 #pragma unroll
-    for (int j = 0; j < 16; j++) base[j] = ra + rb_s[oc + j] - 4;
+            for (int k = 0; k < 4; k++) {
+                const int v = min(v0 + k * 256 * KS, nvt - 1);
+                t[k] = v < nva ? ga[v] : gb[v - nva];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = min(v0 + k * 256 * KS, nvt);
+                *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
+            }
+        }
+    }
     __syncthreads();
+    if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
+    else if (tid >= 64 && tid < 64 + BN) {
+        const int c = tid - 64;
+        int m = -128;
+        for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
+        rb_s[c] = m;
+    }
+    __syncthreads();
+    for (int i = tid; i < BM * nb; i += 256 * KS) {                 // i = b * BM + r
+        const int r = i & (BM - 1), b = i >> 5;
+        na_s[i] = max((int)st_s[r * nb + b] + 4 - ra_s[r], -100);
+    }
+    for (int i = tid; i < BN * nb; i += 256 * KS) {                 // i = b * BN + c
+        const int c = i & (BN - 1), b = i >> 7;
+        nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nb + b] - rb_s[c], -100);
+    }
+    __syncthreads();                                                // staging bytes consumed: buffers are free
+    if (g < ns) guarda(0);
+    __syncthreads();
+
+    int acc[2][2][4] = {};
+    int par = 0;
+    for (int st = g; st < ns; st += KS) {
+        if (st + KS < ns) busca(st + KS);                           // next stage of this group in flight
+        const char* tile = meu + par * STAGE;
+#pragma unroll
+        for (int bl = 0; bl < BPS; bl++) {
+            const int b = st * BPS + bl;
+            if (b >= nb) break;
+            v4i p[2][2];
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++) p[ti][tj] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int k = 0; k < KST; k++) {
+                const int kb = (bl * KST + k) * 32 + 8 * lg;
+                long fa[2], fb[2];
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    fa[t] = *reinterpret_cast<const long*>(tile + (16 * t + lr) * LD + kb);
+                    fb[t] = *reinterpret_cast<const long*>(tile + (BM + wc + 16 * t + lr) * LD + kb);
+                }
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                    for (int tj = 0; tj < 2; tj++) p[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], p[ti][tj], 0, 0, 0);
+            }
+            const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
+            const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
+            const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);                     // 4 - sa - sb
+                        acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
+                    }
+        }
+        par ^= 1;
+        if (st + KS < ns) guarda(par);
+        __syncthreads();
+    }
+    // groups with fewer stages still take part in every barrier of the loop above
+    for (int st = g + ((ns - g + KS - 1) / KS) * KS; st < ((ns + KS - 1) / KS) * KS; st += KS) __syncthreads();
+
+    // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout
+    int base[16];
+    if (tid < 256) {
+        const int ra = ra_s[orow];
+#pragma unroll
+        for (int j = 0; j < 16; j++) base[j] = ra + rb_s[oc + j] - 4;
+    }
+    int* acc_s = reinterpret_cast<int*>(buf);                      // [KS][BM][BN + PAD]
+    constexpr int TILE = BM * (BN + PAD);
 #pragma unroll
     for (int ti = 0; ti < 2; ti++)
 #pragma unroll
         for (int tj = 0; tj < 2; tj++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc_s[(16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
+            for (int i = 0; i < 4; i++) acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
     __syncthreads();
-    int v[16];
-#pragma unroll
-    for (int j = 0; j < 16; j += 4) {
-        const v4i t = *reinterpret_cast<const v4i*>(acc_s + orow * (BN + PAD) + oc + j);
-        v[j] = t[0]; v[j + 1] = t[1]; v[j + 2] = t[2]; v[j + 3] = t[3];
-    }
-    const int r = row0 + orow, c = col0 + oc;
-    const size_t o = (size_t)r * N + c;
     if constexpr (MODO == 1) {
-        if (gridDim.z > 1) {
+        // raw output, coalesced: thread t writes column t % 128 of rows 16 (t / 128) .. +15 (64 consecutive ints per wave)
+        if (tid < 256) {
+            const int c = tid & 127, r0 = (tid >> 7) * 16;
+            const int rbc = rb_s[c] - 4;
+#pragma unroll 4
+            for (int rr = 0; rr < 16; rr++) {
+                const int r = r0 + rr;
+                int v = 0;
 #pragma unroll
-            for (int j = 0; j < 16; j++) atomicAdd(C32 + o + j, v[j]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; j += 4) *reinterpret_cast<int4*>(C32 + o + j) = make_int4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+                for (int q = 0; q < KS; q++) v += acc_s[q * TILE + r * (BN + PAD) + c];
+                const size_t oo = (size_t)(row0 + r) * N + col0 + c;
+                C32[oo] = v;
+                Ce[oo] = (int16_t)max(-30000, ra_s[r] + rbc);
+            }
         }
-        if (blockIdx.z == 0) {
-            int16_t eo[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++) eo[j] = (int16_t)max(-30000, base[j]);
-            grava_i16(Ce + o, eo);
-        }
+        return;
     } else {
+        if (tid >= 256) return;
+        int v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+            v4i t = *reinterpret_cast<const v4i*>(acc_s + orow * (BN + PAD) + oc + j);
+#pragma unroll
+            for (int q = 1; q < KS; q++) t += *reinterpret_cast<const v4i*>(acc_s + q * TILE + orow * (BN + PAD) + oc + j);
+            v[j] = t[0]; v[j + 1] = t[1]; v[j + 2] = t[2]; v[j + 3] = t[3];
+        }
         constexpr int LPB = BLK / 16;
         const bool lider = (tid & (LPB - 1)) == 0;
-        const size_t oe = (size_t)r * (N / BLK) + c / BLK;
         int8_t m[16];
         const int E = quant8<16, LPB>(v, base, m, kid, o);
         if constexpr (MODO == 0 || MODO == 3) {
@@ -163,11 +243,10 @@ __global__ void __launch_bounds__(256) k_gemm(const int8_t* __restrict__ A, cons
             if (lider) OE2[oe] = (int8_t)Ea;
         }
         if constexpr (MODO == 2) {                                 // z = soma(X, C): ec = max(xE, E) - 21
-            int x[16], s[16];
-            le_i8(Xm + o, x);
-            const int ex = XE[oe], ec = max(ex, E) - 21;
+            int s[16];
+            const int ec = max(exin, E) - 21;
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = desloca(x[j], ec - ex) + desloca((int)m[j], ec - E);
+            for (int j = 0; j < 16; j++) s[j] = desloca(xin[j], ec - exin) + desloca((int)m[j], ec - E);
             int8_t q[16];
             const int Ez = quant8_comum<16, LPB>(s, ec, q);
             if (Ez > 126 && lider) reporta(E_EXP, kid, (long long)o, Ez, -6);
@@ -175,13 +254,11 @@ __global__ void __launch_bounds__(256) k_gemm(const int8_t* __restrict__ A, cons
             if (lider) CE[oe] = (int8_t)Ez;
         }
         if constexpr (MODO == 4) {                                 // gh = C * 2 max(H, 0), exponent E + eh
-            int h[16], s[16];
-            le_i8(Xm + o, h);
-            const int eh = XE[oe];
+            int s[16];
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = (int)m[j] * max(h[j], 0) * 2;
+            for (int j = 0; j < 16; j++) s[j] = (int)m[j] * max(xin[j], 0) * 2;
             int8_t q[16];
-            const int Eg = quant8_comum<16, LPB>(s, E + eh, q);
+            const int Eg = quant8_comum<16, LPB>(s, E + exin, q);
             if (Eg > 126 && lider) reporta(E_EXP, kid, (long long)o, Eg, -8);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Eg;
@@ -189,10 +266,14 @@ __global__ void __launch_bounds__(256) k_gemm(const int8_t* __restrict__ A, cons
     }
 }
 
-// dynamic LDS bytes for a K of nb blocks (the accumulator tile needs BM * (BN + PAD) * 4)
-static inline size_t gemm_lds(int nb) {
+// dynamic LDS bytes for nb K-blocks and KS K-splits
+static inline size_t gemm_lds(int nb, int ks) {
     using namespace gemm;
-    const size_t ex = (size_t)nb * BM * 4 + (size_t)nb * BN + (BM + BN) * 4;
-    const size_t ac = (size_t)BM * (BN + PAD) * 4;
-    return ex > ac ? ex : ac;
+    const size_t fixo = (size_t)(BM + BN) * 4 + (size_t)nb * BM * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
+    size_t area = (size_t)ks * 2 * STAGE;
+    const size_t exp_bruto = (size_t)nb * (BM + BN) + 16;
+    const size_t acc = (size_t)ks * BM * (BN + PAD) * 4;
+    if (exp_bruto > area) area = exp_bruto;
+    if (acc > area) area = acc;
+    return fixo + area;
 }
