@@ -7,10 +7,12 @@ every weight) over one synthetic batch of uniform random token ids, following th
 replay, read the error record. Batches are resident in HBM before the timed region.
 
 Workloads (--config):
+  b4  BASELINE config 4 (default): 12 layers, D=512, 8 heads x 64, FF=2048, V=256, T=256, Bt=8 (2048 tokens),
+      BLK=32
   r   reference-native shape: 12 layers, D=256, 64 heads x 4, FF=1024, T=128, Bt=16 (2048 tokens), BLK=128 --
       the configuration of the reference's published 34,248 tokens/s (GTX 1650, README.md:87)
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config r] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config b4|r] [--no-cpu]
 Prints one JSON line.
 """
 import argparse
@@ -28,6 +30,8 @@ PEAK_I8 = 5.0e15          # MI355X dense int8 MFMA, ops/s
 PEAK_HBM = 8.0e12         # bytes/s
 
 CONFIGS = {
+    "b4": dict(V=256, D=512, H=8, FF=2048, L=12, T=256, Bt=8, BLK=32, r16=False,
+               nome="BASELINE config 4: 12L D512 H8x64 FF2048 V256 T256 Bt8 BLK32", publicado=None),
     "r": dict(V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=16, BLK=128, r16=False,
               nome="reference-native 12L D256 H64x4 FF1024 T128 Bt16 BLK128", publicado=34248.0),
 }
@@ -38,7 +42,7 @@ def args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="r", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="b4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     return ap.parse_args()

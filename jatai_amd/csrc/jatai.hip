@@ -13,6 +13,7 @@
 #include "jt_linhas.hip"
 #include "jt_gemm.hip"
 #include "jt_atencao.hip"
+#include "jt_atencao_hd.hip"
 
 __device__ Erro g_erro;
 __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long long valor, long long aux) {
@@ -281,32 +282,63 @@ int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, vo
 
 // ---------------------------------------------------------------------------------------------- attention
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
-    if (hd != 4) return (int)hipErrorNotSupported;
-    if (T <= 128)
-        k_atencao4<128><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
-    else
-        k_atencao4<256><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+    if (hd == 4) {
+        if (T > 256) return (int)hipErrorInvalidValue;
+        if (T <= 128)
+            k_atencao4<128><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+        else
+            k_atencao4<256><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+        return fim();
+    }
+    if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
+    const size_t lds = (size_t)T * hd * 4;
+    const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
+#define L(HD) (lds_max(k_atencao_hd<HD>, lds), k_atencao_hd<HD><<<g, hd::NT, lds, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, \
+              (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid))
+    if (hd == 16) L(16); else if (hd == 32) L(32); else L(64);
+#undef L
     return fim();
 }
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T > 256 || T <= 0) return (int)hipErrorInvalidValue;
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
     if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
-    if (hd != 4) return (int)hipErrorNotSupported;
     const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);
+    if (hd == 4) {
+        if (T > 256) return (int)hipErrorInvalidValue;
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
-    if (T <= 128) {
-        if (limite) k_atencao4_back<128, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
-        else k_atencao4_back<128, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
-    } else {
-        if (limite) k_atencao4_back<256, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
-        else k_atencao4_back<256, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
-    }
+        if (T <= 128) {
+            if (limite) k_atencao4_back<128, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
+            else k_atencao4_back<128, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+        } else {
+            if (limite) k_atencao4_back<256, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
+            else k_atencao4_back<256, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+        }
 #undef ARGS
+        return fim();
+    }
+    if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
+    const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
+    const size_t lds1 = (size_t)T * hd * 2, lds3 = (size_t)(2 * T + 2 * hd::QB) * hd * 2 + (size_t)T * 4;
+    const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
+    const uint8_t* P8 = (const uint8_t*)P;
+    int16_t* Ge16 = (int16_t*)Ge;
+#define FASES(HD, LM)                                                                                                      \
+    {                                                                                                                      \
+        k_atb_max1<HD, LM><<<g, hd::NT, lds1, g_stream>>>(go8, goE8, q8, qE8, Ge16, T, H, D, g_blk, GA);                   \
+        k_atb_slin<HD, LM><<<g, hd::NT, lds1, g_stream>>>(go8, goE8, q8, qE8, P8, Ge16, T, H, D, g_blk, GA, kid);          \
+        lds_max(k_atb_grad<HD, LM>, lds3);                                                                                 \
+        k_atb_grad<HD, LM><<<g, hd::NT, lds3, g_stream>>>(go8, goE8, q8, qE8, P8, (int*)Gacc, Ge16, T, H, D, g_blk, GA, dsb, kid); \
+        k_atb_exp<HD, LM><<<Bt * H, hd::NT, 0, g_stream>>>(goE8, qE8, Ge16, T, H, D, g_blk, GA, dsb);                       \
+    }
+#define LIM_(HD) { if (limite) FASES(HD, 1) else FASES(HD, 0) }
+    if (hd == 16) LIM_(16) else if (hd == 32) LIM_(32) else LIM_(64)
+#undef LIM_
+#undef FASES
     return fim();
 }
 

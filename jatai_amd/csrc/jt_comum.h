@@ -74,6 +74,8 @@ __device__ __forceinline__ int isqrt_i(int n) {     // ops.py:84-89
     return max(x, 1);
 }
 
+__host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2_c(n >> 1); }
+
 // ---------------------------------------------------------------------------------------------- lane groups
 // A block of BLK values is held by LPB consecutive lanes (a power of two <= 64), VPL values each.
 template <int LPB>

@@ -242,18 +242,28 @@ class OpsHip:
         self.reg.confere_bloco("qkv", QKV)
         m, E = QKV
         D = m.shape[1] // 3
-        self.reg.exige(T <= 256 and T % 64 == 0 and D % H == 0 and D // H == 4 and m.shape[0] == Bt * T,
-                       f"atencao: T={T} (<=256, multiplo de 64), D={D}, H={H} (largura de cabeca 4)")
+        self._formas_atencao("atencao", m, Bt, T, H, D)
         oacc = torch.empty(Bt * T, D, dtype=torch.int32, device=m.device)
         oe = torch.empty(Bt * T, D, dtype=torch.int16, device=m.device)
         P = torch.empty(Bt * H, T, T, dtype=torch.uint8, device=m.device)
         self._lanca("atencao", "jt_atencao", (m, E, oacc, oe, P, Bt, T, H, D, GA), dict(qkv=m, qkvE=E), (Bt * T, D))
         return (oacc, oe), P
 
+    def _formas_atencao(self, op, m, Bt, T, H, D):
+        """Head width hd = D/H: 4 is the spec's shape (T <= 256); 16, 32 and 64 run the generalized kernels
+        (T <= 512). T must be a multiple of 64."""
+        hd = D // H if H and D % H == 0 else 0
+        self.reg.exige(hd in (4, 16, 32, 64) and T % 64 == 0 and T <= (256 if hd == 4 else 512) and m.shape[0] == Bt * T
+                       and m.shape[1] == 3 * D,
+                       f"{op}: T={T} (multiplo de 64, <= 256 com cabeca 4, <= 512 senao), D={D}, H={H} (cabeca 4, 16, 32 ou 64)")
+
     def atencao_back(self, GO, QKV, P, Bt, T, H):
         self.reg.confere_bloco("go", GO); self.reg.confere_bloco("qkv", QKV)
         (gm, gE), (m, E) = GO, QKV
         D = gm.shape[1]
+        self._formas_atencao("atencao_back", m, Bt, T, H, D)
+        self.reg.exige(tuple(P.shape) == (Bt * H, T, T) and P.dtype == torch.uint8 and P.is_contiguous(),
+                       f"atencao_back: P com forma {tuple(P.shape)}, esperado {(Bt * H, T, T)} uint8")
         acc = torch.empty(Bt * T, 3 * D, dtype=torch.int32, device=m.device)
         e = torch.empty(Bt * T, 3 * D, dtype=torch.int16, device=m.device)
         self._lanca("atencao_back", "jt_atencao_back", (gm, gE, m, E, P, acc, e, Bt, T, H, D, GA, int(ATENCAO_LIMITE)),

@@ -1,0 +1,45 @@
+"""Attention at head width 64 (the BASELINE configs' 8 heads x 64 of D = 512, T = 256): the HIP kernels against
+the CPU oracle's generalized restatement (jatai_oracle.cpp, which reduces to the spec at head width 4, pinned by
+the golden fixtures). Bit-exact: P, the raw output (acc, e), and the backward's raw (acc, e) in both variants.
+The generalization itself has no reference counterpart: parity beyond the head-width-4 reduction is unpinned."""
+import pytest
+import torch
+
+import recipe as R
+from backends import CPU, GPU, host, primeira_diferenca
+
+pytestmark = pytest.mark.gpu
+
+
+def _cmp(a, b, nome):
+    d = primeira_diferenca(host(a), host(b))
+    assert d is None, f"{nome}: (flat index, gpu, oracle, count) = {d}"
+
+
+# exponents e0 +- espalha stay in the range where the int32 sentinels stay silent (e0 + espalha <= 2, as the
+# reference's own spread cases, teste_ops.py:86-87); GPU() reads the device error record after every op
+@pytest.mark.parametrize("blk,Bt,T,H,D,esp,e0,limite", [
+    (32, 2, 256, 8, 512, 3, -7, False),
+    (32, 2, 256, 8, 512, 10, -9, True),
+    (128, 2, 128, 8, 512, 6, -7, False),
+    (32, 1, 256, 4, 256, 12, -10, True),
+    (32, 2, 128, 16, 512, 2, -7, False),
+], ids=["cfg4", "cfg4-limite-espalhado", "blk128-T128", "H4-espalhado-limite", "hd32"])
+def test_atencao_hd_vs_oraculo(blk, Bt, T, H, D, esp, e0, limite):
+    M = Bt * T
+    seed = R.substream(555, f"{blk} {Bt} {T} {H} {D} {esp} {limite}")
+    qn = R.bloco(R.substream(seed, "qkv"), M, 3 * D, blk, espalha=esp, e0=e0, zera=0.05)
+    gn = R.bloco(R.substream(seed, "go"), M, D, blk, espalha=esp, e0=-20, zera=0.05)
+    res = []
+    for be in (GPU(blk, vigiar=True), CPU(blk)):
+        qkv = tuple(be.dev(v) for v in qn)
+        go = tuple(be.dev(v) for v in gn)
+        (oacc, oe), P = be.ops.atencao(qkv, Bt, T, H)
+        old = be.limite(limite)
+        try:
+            gacc, ge = be.ops.atencao_back(go, qkv, P, Bt, T, H)
+        finally:
+            be.limite(old)
+        res.append((oacc, oe, P, gacc, ge))
+    for nome, a, b in zip(("oacc", "oe", "P", "gacc", "ge"), *res):
+        _cmp(a, b, nome)

@@ -1,0 +1,40 @@
+"""One full training step at the BASELINE config-4 widths (D=512, 8 heads x 64, FF=2048, V=256, T=256, BLK=32),
+with 2 layers and 2 sequences: every op output of the HIP path equals the CPU oracle's (jatai_amd.modelo.Modelo
+on both backends, same init and tokens). Also checks the step is stable under hipGraph replay."""
+import pytest
+import torch
+
+import cases as CS
+import recipe as R
+from backends import LOGS, host
+
+pytestmark = pytest.mark.gpu
+
+
+def test_passo_config4_vs_oraculo():
+    from jatai_amd import ops as O
+    from jatai_amd.modelo import Modelo
+    from jatai_amd.registro import Registro
+    from oracle.ops_oracle import OpsOraculo
+    import traco as TR
+    O.BLK = 32
+    V, D, H, FF, L, Bt, T = 256, 512, 8, 2048, 2, 2, 256
+    reg = Registro(LOGS, "modelo_b", eco=False)
+    gpu = CS.Gravador(O.OpsHip(reg), host)
+    cpu = CS.Gravador(OpsOraculo(32), host)
+    mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg)
+    mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub())
+    for p in range(2):
+        x = R.tokens(R.substream(31, f"b4 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
+        tok = torch.from_numpy(x[:, :-1].copy()).long()
+        alvo = torch.from_numpy(x[:, 1:].copy()).long()
+        gpu.log, cpu.log = [], []
+        reg.novo_passo(p)
+        pg = float(mg.passo(tok.cuda(), alvo.cuda(), k_lr=4))
+        reg.fim_passo()
+        pc = float(mc.passo(tok, alvo, k_lr=4))
+        assert len(gpu.log) == len(cpu.log)
+        for k, (a, b) in enumerate(zip(gpu.log, cpu.log)):
+            assert list(a) == list(b), f"step {p}, op #{k} '{b[0]}' differs from the oracle"
+        assert abs(pg - pc) <= 1e-12 * abs(pc)
+    O.BLK = 128
