@@ -30,6 +30,9 @@ void jt_gemm_bm(int bm);               /* accepted; the MFMA GEMM has a single t
 void jt_atencao_linhas(int n);         /* accepted; attention runs one query row per thread */
 int jt_res_estocastico(int ligado);    /* 0 ok when off; stochastic residual rounding returns hipErrorNotSupported */
 
+/* ---- no reference counterpart: attention kernel family at head width 64, matrix cores (1, default) or dot2 (0) */
+void jt_atencao_mfma(int ligado);
+
 /* ---- block size: no reference counterpart (the reference fixes 128) */
 int jt_bloco(int blk);                 /* 32 or 128; hipErrorInvalidValue otherwise */
 int jt_bloco_atual(void);

@@ -31,6 +31,7 @@ static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
 static int g_alvo_wg = 512;             // GEMM K-split target: workgroups of 4 waves wanted per launch
 static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
+static int g_atencao_mfma = 1;          // head width 64: matrix-core attention (1) or the dot2 kernels (0)
 
 static int fim() { return (int)hipGetLastError(); }
 // Every kernel moves 8- or 16-byte vectors: operands must be 16-byte aligned (torch allocations are 256-byte
@@ -79,6 +80,8 @@ void jt_stream(void* st) { g_stream = (hipStream_t)st; }
 void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 512; }
 void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one tile shape; kept for the interface
 void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
+// No reference counterpart: selects the matrix-core (1, default) or dot2 (0) attention kernels at head width 64.
+void jt_atencao_mfma(int ligado) { g_atencao_mfma = ligado ? 1 : 0; }
 int jt_res_estocastico(int ligado) { return ligado ? (int)hipErrorNotSupported : 0; }
 // No reference counterpart: the reference fixes BLK = 128 (jatai_cuda.cu:16).
 int jt_bloco(int blk) {
@@ -294,8 +297,17 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
         return fim();
     }
     if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
-    const size_t lds = (size_t)T * hd * 4;
     const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
+    if (hd == 64 && g_atencao_mfma) {                // matrix-core forward (scores kept in registers: T <= 256)
+        const size_t Tk = (size_t)T, lds_mf = Tk * 64 + ((Tk * 2 + 15) & ~(size_t)15) + 64 * Tk * 2 + 4 * 16 * Tk * 2;
+        if (T <= 256) {
+            lds_max(k_atencao_mf<256>, lds_mf);
+            k_atencao_mf<256><<<g, 256, lds_mf, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P,
+                                                            T, H, D, g_blk, GA, kid);
+            return fim();
+        }
+    }
+    const size_t lds = (size_t)T * hd * 4;
 #define L(HD) (lds_max(k_atencao_hd<HD>, lds), k_atencao_hd<HD><<<g, hd::NT, lds, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, \
               (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid))
     if (hd == 16) L(16); else if (hd == 32) L(32); else L(64);
@@ -323,6 +335,30 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     }
     if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
     const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
+    if (hd == 64 && g_atencao_mfma && T <= 256) {        // matrix-core backward: 5 launches
+        const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
+        const uint8_t* P8 = (const uint8_t*)P;
+        int16_t* Ge16 = (int16_t*)Ge;
+        int* G32 = (int*)Gacc;
+        const size_t n = (size_t)T, pad = (n * 2 + 15) & ~(size_t)15;
+        const size_t l_lin = n * 64 + pad, l_gq = n * 64 + pad + 64 * n * 2 + 4 * 16 * n * 2;
+        const size_t l_gkv = n * 64 + pad + 2 * 64 * n * 2 + 4 * 16 * n * 2 + 4 * 16 * n + n * 4;
+        const size_t lds1 = (size_t)T * hd * 2;
+#define MF(LM)                                                                                                              \
+        {                                                                                                                   \
+            if (LM) k_atb_max1<64, 1><<<g, hd::NT, lds1, g_stream>>>(go8, goE8, q8, qE8, Ge16, T, H, D, g_blk, GA);         \
+            else k_atb_mf_linhas<256, 1, 0><<<g, 256, l_lin, g_stream>>>(go8, goE8, q8, qE8, P8, Ge16, T, H, D, g_blk, GA, kid); \
+            k_atb_mf_linhas<256, 2, LM><<<g, 256, l_lin, g_stream>>>(go8, goE8, q8, qE8, P8, Ge16, T, H, D, g_blk, GA, kid);  \
+            lds_max(k_atb_mf_gq<256, LM>, l_gq);                                                                            \
+            k_atb_mf_gq<256, LM><<<g, 256, l_gq, g_stream>>>(go8, goE8, q8, qE8, P8, G32, Ge16, T, H, D, g_blk, GA, dsb, kid); \
+            lds_max(k_atb_mf_gkv<256, LM>, l_gkv);                                                                          \
+            k_atb_mf_gkv<256, LM><<<g, 256, l_gkv, g_stream>>>(go8, goE8, q8, qE8, P8, G32, Ge16, T, H, D, g_blk, GA, dsb, kid); \
+            k_atb_exp<64, LM><<<Bt * H, hd::NT, 0, g_stream>>>(goE8, qE8, Ge16, T, H, D, g_blk, GA, dsb);                  \
+        }
+        if (limite) MF(1) else MF(0)
+#undef MF
+        return fim();
+    }
     const size_t lds1 = (size_t)T * hd * 2, lds3 = (size_t)(2 * T + 2 * hd::QB) * hd * 2 + (size_t)T * 4;
     const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
     const uint8_t* P8 = (const uint8_t*)P;

@@ -69,7 +69,7 @@ __device__ __forceinline__ void alinha_lane(const int8_t* m, const int8_t* E, in
     le_i8(m + (size_t)tok * ld + c, v);
 #pragma unroll
     for (int k = 0; k < DL / 2; k++) {
-        const int a0 = rnd_d(v[2 * k] << GA, s), a1 = rnd_d(v[2 * k + 1] << GA, s);
+        const int a0 = rnd_d(shl(v[2 * k], GA), s), a1 = rnd_d(shl(v[2 * k + 1], GA), s);
         w[k] = (a0 & 0xffff) | (a1 << 16);
     }
 }
@@ -429,4 +429,506 @@ __global__ void __launch_bounds__(hd::NT) k_atb_exp(const int8_t* __restrict__ g
         grava_i16(Ge + o + D, bq);
         grava_i16(Ge + o + 2 * D, cv);
     }
+}
+
+// ---------------------------------------------------------------------------------------------- forward on MFMA (HD = 64)
+// Same arithmetic as k_atencao_hd, computed with matrix cores. An aligned value a = rnd(m << GA, s) is exactly
+// m8 << L with m8 int8 and L >= 0 per (token, 32-dimension half): (m, GA - s) if s <= GA, else (rnd(m, s - GA), 0)
+// (the reference's packing, jatai_cuda.cu:789-818). So q_i . k_j = sum over the two halves c of
+// (m8q_i . m8k_j)_c << (Lq_ic + Lk_jc): one i8 MFMA 16x16x32 per half and tile, shifted and added exactly in
+// int32 (|(.)_c| < 2^19, shift <= 8). The scores of a wave's 16 query rows stay in registers (16 per key tile),
+// so max, sum and P take one pass each over them. PV runs as an f16 MFMA 16x16x32: P <= 255 and |v| <= 2032
+// are exact in f16, products exact in fp32, and every partial sum is bounded by sum_j P_ij * 2032 < 2^20 (the
+// P of a row sum to at most 256 + T/2), so the fp32 accumulation is exact and converts back to the same int.
+// Workgroup = 4 waves = 64 query rows of one (sequence, head); wave w owns rows 16 w .. 16 w + 15.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void m8_L(int m, int s, int GA, int& m8, int& L) {
+    if (s <= GA) { m8 = m; L = GA - s; }
+    else { m8 = rnd_d(m, s - GA); L = 0; }
+}
+
+template <int TMAX>
+__global__ void __launch_bounds__(256) k_atencao_mf(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, int* __restrict__ Oacc,
+                                                    int16_t* __restrict__ Oe, uint8_t* __restrict__ P, int T, int H, int D, int blk, int GA,
+                                                    int kid) {
+    constexpr int HD = 64, NTT = TMAX / 16;
+    extern __shared__ __align__(16) char sm_mf[];
+    const int nqb = T / 64, bh = blockIdx.x / nqb, qb = blockIdx.x % nqb, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, Tk = qb * 64 + 64, nbl = ld / blk;
+    int8_t* km = reinterpret_cast<int8_t*>(sm_mf);                  // [Tk][64] m8 of k
+    int8_t* kL = km + (size_t)Tk * 64;                              // [Tk][2] L of k per half
+    _Float16* vt = reinterpret_cast<_Float16*>(kL + (((size_t)Tk * 2 + 15) & ~(size_t)15));   // [64][Tk] aligned v, transposed
+    _Float16* ps = vt + (size_t)64 * Tk;                            // [4][16][Tk] P of each wave
+    __shared__ int red[4];
+    __shared__ int qL[64][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int emq = emx_cabeca<HD>(qE, ld, h * HD, blk, b0, T, red);
+    const int emk = emx_cabeca<HD>(qE, ld, D + h * HD, blk, b0, T, red);
+    const int emv = emx_cabeca<HD>(qE, ld, 2 * D + h * HD, blk, b0, T, red);
+    // k and v of tokens [0, Tk): thread (t, c4) handles dimensions 16 c4 .. 16 c4 + 15 of token t
+    for (int t = tid >> 2; t < Tk; t += 64) {
+        const int c4 = tid & 3, half = c4 >> 1;
+        const size_t base = (size_t)(b0 + t) * ld;
+        int v[16];
+        le_i8(qm + base + D + h * HD + 16 * c4, v);
+        const int sk = emk - (int)qE[(size_t)(b0 + t) * nbl + (D + h * HD + 16 * c4) / blk];
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sk, GA, a, L); m8[k] = (int8_t)a; }
+        grava_i8(km + (size_t)t * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) kL[t * 2 + half] = (int8_t)L;
+        le_i8(qm + base + 2 * D + h * HD + 16 * c4, v);
+        const int sv = emv - (int)qE[(size_t)(b0 + t) * nbl + (2 * D + h * HD + 16 * c4) / blk];
+#pragma unroll
+        for (int k = 0; k < 16; k++) vt[(size_t)(16 * c4 + k) * Tk + t] = (_Float16)rnd_d(shl(v[k], GA), sv);
+    }
+    // q fragments: A row lr = query row 16 w + lr, dimensions 32 c + 8 lg .. + 7 of half c
+    const int ia = qb * 64 + 16 * w + lr;
+    long qa[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int col = h * HD + 32 * c + 8 * lg;
+        int v[8];
+        le_i8(qm + (size_t)(b0 + ia) * ld + col, v);
+        const int s = emq - (int)qE[(size_t)(b0 + ia) * nbl + col / blk];
+        long pk = 0;
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) { int a; m8_L(v[k], s, GA, a, L); pk |= (long)(uint8_t)a << (8 * k); }
+        qa[c] = pk;
+        if (lg == 0) qL[16 * w + lr][c] = L;
+    }
+    __syncthreads();
+    const int eq = emq - GA, ek = emk - GA, ev = emv - GA;
+    const int su = -(eq + ek - 3 + 8), incl = 8 - (8 * h) / H;     // log2(64) / 2 = 3
+    const int i0 = qb * 64 + 16 * w + 4 * lg;                        // this lane's 4 score rows: i0 .. i0 + 3
+    int lq[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lq[v][0] = qL[16 * w + 4 * lg + v][0]; lq[v][1] = qL[16 * w + 4 * lg + v][1]; }
+    const int ntk = qb * 4 + w + 1;                                  // key tiles [0, 16 ntk) reach the wave's last row
+    const long long idx = (long long)(b0 + i0) * D + h * HD;
+    int uu[NTT][4], mx[4] = {U_MIN, U_MIN, U_MIN, U_MIN};
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t >= ntk) continue;                                      // guarded, not break: uu stays in registers
+        const int j = 16 * t + lr;
+        const long kb0 = *reinterpret_cast<const long*>(km + (size_t)j * 64 + 8 * lg);
+        const long kb1 = *reinterpret_cast<const long*>(km + (size_t)j * 64 + 32 + 8 * lg);
+        const int lk0 = kL[j * 2], lk1 = kL[j * 2 + 1];
+        const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[0], kb0, v4i{0, 0, 0, 0}, 0, 0, 0);
+        const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[1], kb1, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int i = i0 + v;
+            const int s = shl(p0[v], lq[v][0] + lk0) + shl(p1[v], lq[v][1] + lk1);
+            const int r = su >= 0 ? rnd_d(s, su) : rnd(s, su, kid, idx);
+            const int u = j <= i ? r - ((i - j) << incl) : U_MIN;
+            uu[t][v] = u;
+            mx[v] = max(mx[v], u);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) mx[v] = g_max<16>(mx[v]);
+    int soma[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t >= ntk) continue;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int ex = uu[t][v] == U_MIN ? 0 : exp_dif(mx[v], uu[t][v]) >> 3;
+            uu[t][v] = ex;
+            soma[v] += ex;
+        }
+    }
+    int inv[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int s = g_sum<16>(soma[v]);
+        if (s <= 0) { if (lr == 0) reporta(E_DIV, kid, idx + (long long)v * D, s, mx[v]); s = 1; }
+        inv[v] = (1 << 28) / s;
+    }
+    uint8_t* Pb = P + (size_t)bh * T * T;
+    _Float16* pw = ps + (size_t)w * 16 * Tk;
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t >= ntk) continue;
+        const int j = 16 * t + lr;
+        unsigned pk = 0;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int p = min((uu[t][v] * inv[v] + (1 << 19)) >> 20, 255);
+            pk |= (unsigned)p << (8 * v);
+            pw[(size_t)(4 * lg + v) * Tk + j] = (_Float16)p;
+        }
+        *reinterpret_cast<unsigned*>(Pb + (size_t)j * T + i0) = pk;
+    }
+    for (int t = ntk; t < T / 16; t++) *reinterpret_cast<unsigned*>(Pb + (size_t)(16 * t + lr) * T + i0) = 0u;
+    if (ntk & 1)
+#pragma unroll
+        for (int v = 0; v < 4; v++) pw[(size_t)(4 * lg + v) * Tk + 16 * ntk + lr] = (_Float16)0;
+    __syncthreads();
+    // O = P V on f16 MFMA: A = P rows lr, keys 32 ch + 8 lg ..; B = v^T dims 16 dt + lr, same keys
+    f4_t o[4] = {};
+    const int nch = (ntk + 1) / 2;
+    for (int ch = 0; ch < nch; ch++) {
+        const h8_t a = *reinterpret_cast<const h8_t*>(pw + (size_t)lr * Tk + 32 * ch + 8 * lg);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const h8_t bv = *reinterpret_cast<const h8_t*>(vt + (size_t)(16 * dt + lr) * Tk + 32 * ch + 8 * lg);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, o[dt], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const size_t x = (size_t)(b0 + i0 + v) * D + h * HD + 16 * dt + lr;
+            const int ov = (int)o[dt][v];
+            if (ov >= LIM || ov <= -LIM) reporta(E_ACUM, kid, x, ov, -3);
+            Oacc[x] = ov;
+            Oe[x] = (int16_t)(ev - 8);
+        }
+}
+
+// ---------------------------------------------------------------------------------------------- backward on MFMA (HD = 64)
+// Same arithmetic as the dot2 backward above, with matrix cores:
+//   gP (or gP^T) tiles: i8 MFMA per 32-dimension half on the m8 << L packing, shifted and added in int32;
+//   gq = dS K and gk = dS^T Q: f16 MFMA with dS (|dS| < 2^12) split as a 256 + b 16 + c, a in [-16, 15],
+//     b, c in [0, 15], so each piece times |k| <= 2032 and summed over <= 256 terms stays below 2^24: exact
+//     in fp32; the three exact sums are recombined in int32;
+//   gv = P^T dO: f16 MFMA with P split as 16 ph + pl (pieces <= 15; a column of P is not bounded by 256).
+// Launch B3r computes gq for a block's query rows, B3c gk and gv for a block's key rows (one writer per output).
+typedef short s8_t __attribute__((ext_vector_type(8)));
+
+// m8 bytes of dimensions 32 c + 8 g .. + 7 of head slice col0 for token row tok, and L of that half
+__device__ __forceinline__ long m8L_frag(const int8_t* m, const int8_t* E, int ld, int col0, int blk, int tok, int emx, int GA, int c, int g,
+                                         int& L) {
+    const int col = col0 + 32 * c + 8 * g;
+    int v[8];
+    le_i8(m + (size_t)tok * ld + col, v);
+    const int s = emx - (int)E[(size_t)tok * (ld / blk) + col / blk];
+    long pk = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) { int a; m8_L(v[k], s, GA, a, L); pk |= (long)(uint8_t)a << (8 * k); }
+    return pk;
+}
+
+// Stage rows [t0, t0 + n) of a head slice as m8 [n][64] + L [n][2] (threads 4 per row)
+__device__ __forceinline__ void estagia_m8(const int8_t* m, const int8_t* E, int ld, int col0, int blk, int b0, int t0, int n, int emx, int GA,
+                                           int8_t* dm, int8_t* dL) {
+    for (int t = threadIdx.x >> 2; t < n; t += blockDim.x >> 2) {
+        const int c4 = threadIdx.x & 3;
+        int v[16];
+        le_i8(m + (size_t)(b0 + t0 + t) * ld + col0 + 16 * c4, v);
+        const int s = emx - (int)E[(size_t)(b0 + t0 + t) * (ld / blk) + (col0 + 16 * c4) / blk];
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) { int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a; }
+        grava_i8(dm + (size_t)t * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) dL[t * 2 + (c4 >> 1)] = (int8_t)L;
+    }
+}
+
+// Stage rows [t0, t0 + n) of a head slice as aligned f16, transposed: dt[d][t] (stride n)
+__device__ __forceinline__ void estagia_f16t(const int8_t* m, const int8_t* E, int ld, int col0, int blk, int b0, int t0, int n, int emx, int GA,
+                                             _Float16* dt) {
+    for (int t = threadIdx.x >> 2; t < n; t += blockDim.x >> 2) {
+        const int c4 = threadIdx.x & 3;
+        int v[16];
+        le_i8(m + (size_t)(b0 + t0 + t) * ld + col0 + 16 * c4, v);
+        const int s = emx - (int)E[(size_t)(b0 + t0 + t) * (ld / blk) + (col0 + 16 * c4) / blk];
+#pragma unroll
+        for (int k = 0; k < 16; k++) dt[(size_t)(16 * c4 + k) * n + t] = (_Float16)rnd_d(shl(v[k], GA), s);
+    }
+}
+
+// 16 x 16 tile of X Y^T over the 64 head dimensions from m8 fragments: lane (lr, lg) gets rows 4 lg + v, column lr
+__device__ __forceinline__ void tile_xyt(long xa0, long xa1, long yb0, long yb1, const int (&lx)[4][2], int ly0, int ly1, int (&out)[4]) {
+    const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa0, yb0, v4i{0, 0, 0, 0}, 0, 0, 0);
+    const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa1, yb1, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; v++) out[v] = shl(p0[v], lx[v][0] + ly0) + shl(p1[v], lx[v][1] + ly1);
+}
+
+// f16 pieces of 8 int16 dS values: dS = a 256 + b 16 + c
+__device__ __forceinline__ void pedacos_ds(const s8_t& d, h8_t& a, h8_t& b, h8_t& c) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int x = d[k];
+        a[k] = (_Float16)(x >> 8);
+        b[k] = (_Float16)((x >> 4) & 15);
+        c[k] = (_Float16)(x & 15);
+    }
+}
+
+// B1/B2 (rows of query block qb; PASSO 1: max |gP|; PASSO 2: s_i and the dS maxima). LIMITE runs only PASSO 2.
+template <int TMAX, int PASSO, int LIMITE>
+__global__ void __launch_bounds__(256) k_atb_mf_linhas(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE,
+                                                       const int8_t* __restrict__ qm, const int8_t* __restrict__ qE,
+                                                       const uint8_t* __restrict__ P, int16_t* __restrict__ Ge, int T, int H, int D, int blk,
+                                                       int GA, int kid) {
+    constexpr int HD = 64, NTT = TMAX / 16;
+    extern __shared__ __align__(16) char sm_mf[];
+    const int nqb = T / 64, bh = blockIdx.x / nqb, qb = blockIdx.x % nqb, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, Tk = qb * 64 + 64;
+    int8_t* vm = reinterpret_cast<int8_t*>(sm_mf);                  // [Tk][64]
+    int8_t* vL = vm + (size_t)Tk * 64;                              // [Tk][2]
+    __shared__ int red[4];
+    __shared__ int gL[64][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int emg = emx_cabeca<HD>(goE, D, h * HD, blk, b0, T, red);
+    const int emv = emx_cabeca<HD>(qE, ld, 2 * D + h * HD, blk, b0, T, red);
+    estagia_m8(qm, qE, ld, 2 * D + h * HD, blk, b0, 0, Tk, emv, GA, vm, vL);
+    const int ia = qb * 64 + 16 * w + lr;
+    long ga[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        int L;
+        ga[c] = m8L_frag(gom, goE, D, h * HD, blk, b0 + ia, emg, GA, c, lg, L);
+        if (lg == 0) gL[16 * w + lr][c] = L;
+    }
+    int sh = 0;
+    if (PASSO == 2) sh = sh_gp<LIMITE>(Ge, b0, D, h, HD, nqb);
+    __syncthreads();
+    int lx[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lx[v][0] = gL[16 * w + 4 * lg + v][0]; lx[v][1] = gL[16 * w + 4 * lg + v][1]; }
+    const int i0 = qb * 64 + 16 * w + 4 * lg, ntk = qb * 4 + w + 1;
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+    int g[NTT][4];
+    int mg = 0, s[4] = {0, 0, 0, 0}, pm = 0, gm = 0;
+    unsigned pr[NTT];
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t >= ntk) continue;
+        const int j = 16 * t + lr;
+        int o[4];
+        tile_xyt(ga[0], ga[1], *reinterpret_cast<const long*>(vm + (size_t)j * 64 + 8 * lg),
+                 *reinterpret_cast<const long*>(vm + (size_t)j * 64 + 32 + 8 * lg), lx, vL[j * 2], vL[j * 2 + 1], o);
+        if (PASSO == 1) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) if (j <= i0 + v) mg = max(mg, abs(o[v]));
+        } else {
+            pr[t] = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);      // P_ij of rows i0 .. i0 + 3 (0 above the diagonal)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int x = j <= i0 + v ? rnd_d(o[v], sh) : 0;
+                const int p = (pr[t] >> (8 * v)) & 255;
+                g[t][v] = x;
+                s[v] += p * x;
+                if (LIMITE) { pm = max(pm, p); gm = max(gm, abs(x)); }
+            }
+        }
+    }
+    int* slq = slot_hd(Ge, b0, qb, D, h, HD);
+    if (PASSO == 1) {
+        mg = wg_max(mg, red);
+        if (tid == 0) slq[1] = mg;
+        return;
+    }
+    int sl[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int tot = g_sum<16>(s[v]);
+        if ((tot >= LIM || tot <= -LIM) && lr == 0) reporta(E_ACUM, kid, (long long)(b0 + i0 + v) * ld + h * HD, tot, -4);
+        sl[v] = rnd_d(tot, 8);
+        if (lr == 0) slot_hd(Ge, b0, i0 + v, D, h, HD)[0] = sl[v];
+    }
+    if (LIMITE) {
+        pm = wg_max(pm, red);
+        gm = wg_max(gm, red);
+        const int smx = wg_max(max(max(abs(sl[0]), abs(sl[1])), max(abs(sl[2]), abs(sl[3]))), red);
+        if (tid == 0) { slq[3] = pm; slq[4] = gm; slq[5] = smx; }
+    } else {
+        int md = 0;
+#pragma unroll
+        for (int t = 0; t < NTT; t++) {
+            if (t >= ntk) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) md = max(md, abs((int)((pr[t] >> (8 * v)) & 255) * (g[t][v] - sl[v])));
+        }
+        md = wg_max(md, red);
+        if (tid == 0) slq[3] = md;
+    }
+}
+
+// B3r: gq_i = sum_{j <= i} dS_ij k_j for the query rows of block qb
+template <int TMAX, int LIMITE>
+__global__ void __launch_bounds__(256) k_atb_mf_gq(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
+                                                   const int8_t* __restrict__ qE, const uint8_t* __restrict__ P, int* __restrict__ Gacc,
+                                                   int16_t* __restrict__ Ge, int T, int H, int D, int blk, int GA, int dsb, int kid) {
+    constexpr int HD = 64, NTT = TMAX / 16;
+    extern __shared__ __align__(16) char sm_mf[];
+    const int nqb = T / 64, bh = blockIdx.x / nqb, qb = blockIdx.x % nqb, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, Tk = qb * 64 + 64;
+    int8_t* vm = reinterpret_cast<int8_t*>(sm_mf);                  // [Tk][64]
+    int8_t* vL = vm + (size_t)Tk * 64;                              // [Tk][2]
+    _Float16* kt = reinterpret_cast<_Float16*>(vL + (((size_t)Tk * 2 + 15) & ~(size_t)15));   // [64][Tk]
+    short* dsw = reinterpret_cast<short*>(kt + (size_t)64 * Tk);    // [4][16][Tk]
+    __shared__ int red[4];
+    __shared__ int gL[64][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const CabecaHd cb = cabeca_hd<HD>(goE, qE, D, h, blk, b0, T, GA, red);
+    estagia_m8(qm, qE, ld, 2 * D + h * HD, blk, b0, 0, Tk, cb.ev + GA, GA, vm, vL);
+    estagia_f16t(qm, qE, ld, D + h * HD, blk, b0, 0, Tk, cb.ek + GA, GA, kt);
+    const int ia = qb * 64 + 16 * w + lr;
+    long ga[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        int L;
+        ga[c] = m8L_frag(gom, goE, D, h * HD, blk, b0 + ia, cb.ego + GA, GA, c, lg, L);
+        if (lg == 0) gL[16 * w + lr][c] = L;
+    }
+    const int sh = sh_gp<LIMITE>(Ge, b0, D, h, HD, nqb), sh2 = sh_ds<LIMITE>(Ge, b0, D, h, HD, nqb, dsb);
+    const int i0 = qb * 64 + 16 * w + 4 * lg, ntk = qb * 4 + w + 1;
+    int sl[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) sl[v] = slot_hd(Ge, b0, i0 + v, D, h, HD)[0];
+    __syncthreads();
+    int lx[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lx[v][0] = gL[16 * w + 4 * lg + v][0]; lx[v][1] = gL[16 * w + 4 * lg + v][1]; }
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+    short* dw = dsw + (size_t)w * 16 * Tk;
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t >= ntk) continue;
+        const int j = 16 * t + lr;
+        int o[4];
+        tile_xyt(ga[0], ga[1], *reinterpret_cast<const long*>(vm + (size_t)j * 64 + 8 * lg),
+                 *reinterpret_cast<const long*>(vm + (size_t)j * 64 + 32 + 8 * lg), lx, vL[j * 2], vL[j * 2 + 1], o);
+        const unsigned pr = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int p = (pr >> (8 * v)) & 255;
+            const int ds = j <= i0 + v ? rnd_d(p * (rnd_d(o[v], sh) - sl[v]), sh2) : 0;
+            dw[(size_t)(4 * lg + v) * Tk + j] = (short)ds;
+        }
+    }
+    if (ntk & 1)
+#pragma unroll
+        for (int v = 0; v < 4; v++) dw[(size_t)(4 * lg + v) * Tk + 16 * ntk + lr] = 0;
+    __syncthreads();
+    f4_t acc[4][3] = {};
+    const int nch = (ntk + 1) / 2;
+    for (int ch = 0; ch < nch; ch++) {
+        h8_t pa, pb, pc;
+        pedacos_ds(*reinterpret_cast<const s8_t*>(dw + (size_t)lr * Tk + 32 * ch + 8 * lg), pa, pb, pc);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const h8_t kv = *reinterpret_cast<const h8_t*>(kt + (size_t)(16 * dt + lr) * Tk + 32 * ch + 8 * lg);
+            acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, kv, acc[dt][0], 0, 0, 0);
+            acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, kv, acc[dt][1], 0, 0, 0);
+            acc[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, kv, acc[dt][2], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const long long gq = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
+            const size_t o = (size_t)(b0 + i0 + v) * ld + h * HD + 16 * dt + lr;
+            if (gq >= LIM || gq <= -LIM) reporta(E_ACUM, kid, o, gq, -5);
+            Gacc[o] = (int)gq;
+        }
+}
+
+// B3c: gk_j = sum_{i >= j} dS_ij q_i and gv_j = sum_{i >= j} P_ij dO_i for the key rows of block kb
+template <int TMAX, int LIMITE>
+__global__ void __launch_bounds__(256) k_atb_mf_gkv(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
+                                                    const int8_t* __restrict__ qE, const uint8_t* __restrict__ P, int* __restrict__ Gacc,
+                                                    int16_t* __restrict__ Ge, int T, int H, int D, int blk, int GA, int dsb, int kid) {
+    constexpr int HD = 64, NTT = TMAX / 16;
+    extern __shared__ __align__(16) char sm_mf[];
+    const int nqb = T / 64, bh = blockIdx.x / nqb, kb = blockIdx.x % nqb, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, q0 = kb * 64, nq = T - q0;     // queries [q0, T)
+    int8_t* gm8 = reinterpret_cast<int8_t*>(sm_mf);                 // dO m8 [nq][64]
+    int8_t* gL8 = gm8 + (size_t)nq * 64;                            // [nq][2]
+    _Float16* qt = reinterpret_cast<_Float16*>(gL8 + (((size_t)nq * 2 + 15) & ~(size_t)15));  // [64][nq]
+    _Float16* gt = qt + (size_t)64 * nq;                            // dO aligned [64][nq]
+    short* dsw = reinterpret_cast<short*>(gt + (size_t)64 * nq);    // [4][16][nq] dS^T
+    uint8_t* pw = reinterpret_cast<uint8_t*>(dsw + (size_t)4 * 16 * nq);   // [4][16][nq] P^T
+    int* slv = reinterpret_cast<int*>(pw + (size_t)4 * 16 * nq);    // [nq]
+    __shared__ int red[4];
+    __shared__ int vLs[64][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const CabecaHd cb = cabeca_hd<HD>(goE, qE, D, h, blk, b0, T, GA, red);
+    estagia_m8(gom, goE, D, h * HD, blk, b0, q0, nq, cb.ego + GA, GA, gm8, gL8);
+    estagia_f16t(qm, qE, ld, h * HD, blk, b0, q0, nq, cb.eq + GA, GA, qt);
+    estagia_f16t(gom, goE, D, h * HD, blk, b0, q0, nq, cb.ego + GA, GA, gt);
+    for (int t = tid; t < nq; t += 256) slv[t] = slot_hd(Ge, b0, q0 + t, D, h, HD)[0];
+    // v fragments of this wave's 16 keys j0 + lr as the A operand (rows = keys)
+    const int j0 = q0 + 16 * w, ja = j0 + lr;
+    long va[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        int L;
+        va[c] = m8L_frag(qm, qE, ld, 2 * D + h * HD, blk, b0 + ja, cb.ev + GA, GA, c, lg, L);
+        if (lg == 0) vLs[16 * w + lr][c] = L;
+    }
+    const int sh = sh_gp<LIMITE>(Ge, b0, D, h, HD, nqb), sh2 = sh_ds<LIMITE>(Ge, b0, D, h, HD, nqb, dsb);
+    __syncthreads();
+    int lx[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lx[v][0] = vLs[16 * w + 4 * lg + v][0]; lx[v][1] = vLs[16 * w + 4 * lg + v][1]; }
+    const int jr = j0 + 4 * lg;                                      // this lane's 4 keys: jr .. jr + 3
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+    short* dw = dsw + (size_t)w * 16 * nq;
+    uint8_t* pww = pw + (size_t)w * 16 * nq;
+    const int t0 = w, nt = nq / 16;                                  // query tiles [t0, nt) (relative to q0) reach keys >= j0
+    for (int t = 0; t < t0; t++)                                     // tiles before the diagonal: zero
+#pragma unroll
+        for (int v = 0; v < 4; v++) { dw[(size_t)(4 * lg + v) * nq + 16 * t + lr] = 0; pww[(size_t)(4 * lg + v) * nq + 16 * t + lr] = 0; }
+#pragma unroll
+    for (int t = 0; t < NTT; t++) {
+        if (t < t0 || t >= nt) continue;
+        const int il = 16 * t + lr, i = q0 + il;                     // this lane's query (column)
+        int o[4];
+        tile_xyt(va[0], va[1], *reinterpret_cast<const long*>(gm8 + (size_t)il * 64 + 8 * lg),
+                 *reinterpret_cast<const long*>(gm8 + (size_t)il * 64 + 32 + 8 * lg), lx, gL8[il * 2], gL8[il * 2 + 1], o);
+        const int sl = slv[il];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int j = jr + v;
+            const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
+            const int ds = i >= j ? rnd_d(p * (rnd_d(o[v], sh) - sl), sh2) : 0;
+            dw[(size_t)(4 * lg + v) * nq + il] = (short)ds;
+            pww[(size_t)(4 * lg + v) * nq + il] = (uint8_t)p;
+        }
+    }
+    __syncthreads();
+    f4_t ak[4][3] = {}, av[4][2] = {};
+    for (int ch = (16 * t0) / 32; ch < nq / 32; ch++) {
+        h8_t pa, pb, pc, ph, pl;
+        pedacos_ds(*reinterpret_cast<const s8_t*>(dw + (size_t)lr * nq + 32 * ch + 8 * lg), pa, pb, pc);
+        const uint8_t* pp = pww + (size_t)lr * nq + 32 * ch + 8 * lg;
+#pragma unroll
+        for (int k = 0; k < 8; k++) { ph[k] = (_Float16)(pp[k] >> 4); pl[k] = (_Float16)(pp[k] & 15); }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const h8_t qv = *reinterpret_cast<const h8_t*>(qt + (size_t)(16 * dt + lr) * nq + 32 * ch + 8 * lg);
+            const h8_t gv = *reinterpret_cast<const h8_t*>(gt + (size_t)(16 * dt + lr) * nq + 32 * ch + 8 * lg);
+            ak[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, qv, ak[dt][0], 0, 0, 0);
+            ak[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, qv, ak[dt][1], 0, 0, 0);
+            ak[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, qv, ak[dt][2], 0, 0, 0);
+            av[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, gv, av[dt][0], 0, 0, 0);
+            av[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, gv, av[dt][1], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const long long gk = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
+            const long long gvv = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+            const size_t o = (size_t)(b0 + jr + v) * ld + h * HD + 16 * dt + lr;
+            if (gk >= LIM || gk <= -LIM) reporta(E_ACUM, kid, o + D, gk, -5);
+            if (gvv >= LIM || gvv <= -LIM) reporta(E_ACUM, kid, o + 2 * D, gvv, -5);
+            Gacc[o + D] = (int)gk;
+            Gacc[o + 2 * D] = (int)gvv;
+        }
 }

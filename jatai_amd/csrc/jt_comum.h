@@ -74,6 +74,10 @@ __device__ __forceinline__ int isqrt_i(int n) {     // ops.py:84-89
     return max(x, 1);
 }
 
+// left shift of a possibly negative int as two's-complement bits (a signed left shift of a negative value is
+// undefined in C++17)
+__device__ __forceinline__ int shl(int x, int s) { return (int)((unsigned)x << s); }
+
 __host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2_c(n >> 1); }
 
 // ---------------------------------------------------------------------------------------------- lane groups

@@ -43,7 +43,7 @@ def test_grafo_igual_ao_eager_e_ao_spec():
     from jatai_amd.modelo import Modelo, PassoGravado
     g = TR.gold()
     f = g["forma"]
-    n = min(len(g["passos"]), 6)
+    n = len(g["passos"])                                 # every step of the golden loss trace
     ops, reg = _ops()
     dev = "cuda"
     mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, ops, reg)
