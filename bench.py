@@ -45,6 +45,7 @@ def args():
     ap.add_argument("--config", default="b4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--so-passo", action="store_true", help="time the step only (no GEMM sweep, no CPU baseline): for profiling")
     return ap.parse_args()
 
 
@@ -180,6 +181,10 @@ def main():
     tokens = c["Bt"] * c["T"]
     tps = tokens * a.steps / dt
 
+    if a.so_passo:
+        print(json.dumps({"metric": METRIC, "value": tps, "unit": "tokens/s", "ms_per_step": dt / a.steps * 1e3,
+                          "steps": a.steps, "warmup": a.warmup, "graph_launches": nlanc, "config": c["nome"]}), flush=True)
+        return
     gem = mede_gemms(O, ops, c)
     tot_gemm_ms = sum(v["ms"] * v["por_passo"] for v in gem.values())
     dom_nome, dom = max(gem.items(), key=lambda kv: kv[1]["ms"] * kv[1]["por_passo"])

@@ -58,6 +58,13 @@ int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblo
 int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nblocos, int kid);
 int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);
 
+/* ---- no reference counterpart: momento then peso for ntab tensors in one launch. `tabela` is a device array of
+ * ntab entries {const int* gacc; const int16_t* ge; int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE; long long inicio, nblocos;}
+ * sorted by inicio (the tensor's first block in a global numbering), ntab <= 256, nblocos = the total. Results equal jt_momento
+ * followed by jt_peso on each tensor (ops.py:273-290). */
+int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid);
+int jt_tab_otim_bytes(void);           /* sizeof of one table entry (80) */
+
 /* ---- re-blocking, gathers (jatai_cuda.cu:1155-1166). transpoe: R % 128 == 0, C % 64 == 0. */
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid);
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid);

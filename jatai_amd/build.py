@@ -2,7 +2,7 @@
 
 One translation unit (csrc/jatai.hip includes the kernel files), so the device error record is shared by every
 kernel. Packed-FP32 instruction selection is disabled (-packed-fp32-ops); the host pass warns that it does not
-know the feature, which is harmless. Usage: python -m jatai_amd.build
+know the feature, which is harmless. MFMA destinations are kept in VGPRs (-amdgpu-mfma-vgpr-form). Usage: python -m jatai_amd.build
 """
 import os
 import subprocess
@@ -13,7 +13,9 @@ CSRC = os.path.join(AQUI, "csrc")
 SAIDA = os.path.join(AQUI, "libjatai.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-mcode-object-version=5",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA results in VGPRs: the epilogues read every MFMA output, an AGPR->VGPR move each otherwise
+         "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def build(saida=SAIDA, extra=()):

@@ -101,26 +101,31 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
     // K-splits inside a workgroup: up to 4, while the grid has fewer than g_alvo_wg x 4 waves and each split
     // keeps at least two K-blocks
     const long long tiles = (long long)(M / BM) * (N / BN);
-    // (two K-splits at most: each holds two 21 KiB stage buffers in LDS, 160 KiB per workgroup)
-    const int ksmax = 2;
+    // (each K-split holds two stage buffers in LDS -- 11 KiB at BLK=32, 21 KiB at BLK=128, 160 KiB per workgroup --
+    // and the fused epilogues of modes 2-4 would spill at 1024 threads)
+    const int ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
     int ks = 1;
     while (ks < ksmax && tiles * 4 * ks < (long long)g_alvo_wg * 4 && nb >= 4 * ks) ks *= 2;
     const dim3 grade(N / BN, M / BM);
-    const size_t lds = gemm_lds(nb, ks);
+    const size_t lds = gemm_lds(nb, ks, g_blk);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
              (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kid
 #define L(BL, MD, S) (lds_max(k_gemm<BL, MD, S>, lds), k_gemm<BL, MD, S><<<grade, 256 * S, lds, g_stream>>>(ARGS))
 #define LS2(BL, MD) (ks == 1 ? L(BL, MD, 1) : L(BL, MD, 2))
+#define LS4(BL, MD) (ks == 1 ? L(BL, MD, 1) : ks == 2 ? L(BL, MD, 2) : L(BL, MD, 4))
 #define LB2(MD) (g_blk == 32 ? LS2(32, MD) : LS2(128, MD))
+#define LB4(MD) (g_blk == 32 ? LS4(32, MD) : LS2(128, MD))
     switch (modo) {
-        case 0: LB2(0); break;
-        case 1: LB2(1); break;
+        case 0: LB4(0); break;
+        case 1: LB4(1); break;
         case 2: LB2(2); break;
         case 3: LB2(3); break;
         case 4: LB2(4); break;
     }
 #undef LB2
+#undef LB4
 #undef LS2
+#undef LS4
 #undef L
 #undef ARGS
     return fim();
@@ -182,6 +187,17 @@ int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* 
 #undef C
     return fim();
 }
+// No reference counterpart: momento + peso of ntab tensors in one launch (table of TabOtim entries in device
+// memory, sorted by `inicio`, nblocos = total blocks). Same results as jt_momento then jt_peso per tensor.
+int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid) {
+    if (nblocos <= 0 || ntab <= 0 || ntab > 256) return nblocos == 0 ? 0 : (int)hipErrorInvalidValue;
+    if (!alinhados(tabela)) return (int)hipErrorInvalidValue;
+#define C(BL) (k_otimizador<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const TabOtim*)tabela, ntab, nblocos, k_lr, ef, kid), 0)
+    POR_BLK(C);
+#undef C
+    return fim();
+}
+int jt_tab_otim_bytes() { return (int)sizeof(TabOtim); }
 int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(xm, xE, zm, zE)) return (int)hipErrorInvalidValue;
@@ -208,9 +224,11 @@ int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, vo
     return fim();
 }
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid) {
-    if (R <= 0 || C <= 0 || R % 128 || C % 64 || C % g_blk) return (int)hipErrorInvalidValue;
+    const int TR = g_blk == 32 ? 64 : 128;
+    if (R <= 0 || C <= 0 || R % TR || C % 64 || C % g_blk) return (int)hipErrorInvalidValue;
     if (!alinhados(X, EX, Y, EY)) return (int)hipErrorInvalidValue;
-#define L(BL) (k_transpoe<BL><<<dim3(C / 64, R / 128), 256, 0, g_stream>>>((const int8_t*)X, (const int8_t*)EX, (int8_t*)Y, (int8_t*)EY, R, C, kid), 0)
+#define L(BL) (k_transpoe<BL, BL == 32 ? 64 : 128><<<dim3(C / 64, R / (BL == 32 ? 64 : 128)), BL == 32 ? 128 : 256, 0, g_stream>>>( \
+    (const int8_t*)X, (const int8_t*)EX, (int8_t*)Y, (int8_t*)EY, R, C, kid), 0)
     POR_BLK(L);
 #undef L
     return fim();

@@ -51,8 +51,12 @@ __device__ __forceinline__ int rnd_d(int x, int s) {
     return (x + ((1 << (s - 1)) - 1) + ((x >> s) & 1)) >> s;
 }
 
+// left shift of a possibly negative int as two's-complement bits (a signed left shift of a negative value is
+// undefined in C++17)
+__device__ __forceinline__ int shl(int x, int s) { return (int)((unsigned)x << s); }
+
 // x * 2^-s for either sign of s where a left shift provably keeps every bit (no check)
-__device__ __forceinline__ int desloca(int x, int s) { return s >= 0 ? rnd_d(x, s) : x << min(-s, 31); }
+__device__ __forceinline__ int desloca(int x, int s) { return s >= 0 ? rnd_d(x, s) : shl(x, min(-s, 31)); }
 
 // exp(-d/256) in Q15 for d >= 0: shift plus a cubic (ops.py:75-81)
 __device__ __forceinline__ int exp_int(int d) {
@@ -73,10 +77,6 @@ __device__ __forceinline__ int isqrt_i(int n) {     // ops.py:84-89
     for (int i = 0; i < 10; i++) x = min(x, (x + n / max(x, 1)) >> 1);
     return max(x, 1);
 }
-
-// left shift of a possibly negative int as two's-complement bits (a signed left shift of a negative value is
-// undefined in C++17)
-__device__ __forceinline__ int shl(int x, int s) { return (int)((unsigned)x << s); }
 
 __host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2_c(n >> 1); }
 
@@ -119,13 +119,15 @@ __device__ __forceinline__ int quant_grupo(const int (&v)[VPL], const int (&e)[V
         for (int i = 0; i < VPL; i++) m[i] = 0;
         return E_ZERO;
     }
+    // E - e >= bitlen(v) - MBITS for every nonzero v, so a left shift here keeps |q| < 2^MBITS: no bit is lost and
+    // the shift needs no check (zeros shift to zero)
     int E = topo - MBITS, q[VPL], est = 0;
 #pragma unroll
-    for (int i = 0; i < VPL; i++) { q[i] = rnd(v[i], E - e[i], kid, idx0 + i); est |= q[i] > LIMQ || q[i] < -LIMQ; }
+    for (int i = 0; i < VPL; i++) { q[i] = desloca(v[i], E - e[i]); est |= q[i] > LIMQ || q[i] < -LIMQ; }
     if (g_or<LPB>(est)) {
         E += 1;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) q[i] = rnd(v[i], E - e[i], kid, idx0 + i);
+        for (int i = 0; i < VPL; i++) q[i] = desloca(v[i], E - e[i]);
     }
     if (E < -126) {
 #pragma unroll

@@ -237,3 +237,72 @@ __global__ void __launch_bounds__(256) k_zera32(int* __restrict__ p, long long n
     else
         for (long long j = i; j < n; j++) p[j] = 0;
 }
+
+// ---------------------------------------------------------------------------------------------- fused optimizer
+// momento then peso for many tensors in one launch. Per block: Mom <- quant(rnd(7 m, ec - em) + rnd(g, ec - ge), ec)
+// (ops.py:273-278), then W, R <- peso(W, Mom, R, k, ef) (ops.py:280-290) on the new Mom held in registers: the
+// same arithmetic as k_momento followed by k_peso, with Mom read once and the second launch gone.
+// The tensor list is a device table of TabOtim entries (fixed addresses: parameters, momenta, residuals and the
+// persistent raw-gradient buffers of the model); entry t covers global blocks [inicio_t, inicio_t + nblocos_t).
+struct TabOtim {
+    const int* gacc;
+    const int16_t* ge;
+    int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE;
+    long long inicio, nblocos;
+};
+
+template <int BLK>
+__global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ tab, int ntab, long long nblocos, int k_lr, int ef, int kid) {
+    constexpr int LPB = BLK / VPL;
+    const long long og = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * VPL;
+    const long long wg = og / BLK;
+    if (wg >= nblocos) return;
+    int t = 0;                                                      // table entry holding global block wg (entries sorted)
+    for (int s = 128; s; s >>= 1)
+        if (t + s < ntab && tab[t + s].inicio <= wg) t += s;
+    const TabOtim d = tab[t];
+    const long long w = wg - d.inicio, o = w * BLK + (og % BLK);
+    int mm[VPL], g[VPL], eg[VPL], v[VPL], ee[VPL];
+    le_i8(d.Mm + o, mm);
+    le_i32(d.gacc + o, g);
+    le_i16(d.ge + o, eg);
+    const int em = d.ME[w] - 3;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
+        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
+        v[i] = rnd(mm[i] * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
+        ee[i] = ec;
+    }
+    int8_t q[VPL];
+    const int Em = quant8<VPL, LPB>(v, ee, q, kid, o);
+    grava_i8(d.Mm + o, q);
+    const bool lider = (threadIdx.x & (LPB - 1)) == 0;
+    if (lider) d.ME[w] = (int8_t)Em;
+    // peso with the new momentum
+    int wv[VPL], rv[VPL], alvo[VPL];
+    le_i8(d.Wm + o, wv);
+    if (ef) le_i8(d.Rm + o, rv);
+    else
+#pragma unroll
+        for (int i = 0; i < VPL; i++) rv[i] = 0;
+    const int ew = d.WE[w], emk = Em - k_lr, er = ef ? (int)d.RE[w] : E_ZERO;
+    const int ec = max(max(ew + 7, emk + 7), er + 7) - 27;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        alvo[i] = rnd(wv[i], ec - ew, kid, o + i) - rnd(q[i], ec - emk, kid, o + i) + (ef ? rnd(rv[i], ec - er, kid, o + i) : 0);
+        ee[i] = ec;
+    }
+    int8_t qw[VPL];
+    const int Ew = quant8<VPL, LPB>(alvo, ee, qw, kid, o);
+    grava_i8(d.Wm + o, qw);
+    if (lider) d.WE[w] = (int8_t)Ew;
+    if (!ef) return;
+    int dif[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) dif[i] = alvo[i] - (qw[i] == 0 ? 0 : rnd(qw[i], ec - Ew, kid, o + i));
+    int8_t r[VPL];
+    const int Er = quant8<VPL, LPB>(dif, ee, r, kid, o);
+    grava_i8(d.Rm + o, r);
+    if (lider) d.RE[w] = (int8_t)Er;
+}

@@ -26,10 +26,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace gemm {
 constexpr int BM = 32, BN = 128, PAD = 4;
-constexpr int SK = 128;                  // bytes of K per row and stage
-constexpr int LD = SK + 8;               // LDS row stride of a stage tile (8-byte pad spreads rows over the banks)
 constexpr int ROWS = BM + BN;            // rows of a stage tile: 32 of A then 128 of B
-constexpr int STAGE = ROWS * LD;         // bytes of one stage buffer
+// bytes of K per row and stage: 64 at BLK=32 (two blocks; smaller buffers, more resident waves), 128 at BLK=128
+template <int BLK> struct Est {
+    static constexpr int SK = BLK == 32 ? 64 : 128;
+    static constexpr int LD = SK + 8;    // LDS row stride of a stage tile (8-byte pad spreads rows over the banks)
+    static constexpr int STAGE = ROWS * LD;
+    static constexpr int VB = SK / 8;    // bytes each of the 8 lanes of a row moves per stage
+};
 }
 
 template <int BLK, int MODO, int KS>
@@ -39,6 +43,7 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
                                                    int N, int K, int kid) {
     using namespace gemm;
+    constexpr int SK = Est<BLK>::SK, LD = Est<BLK>::LD, STAGE = Est<BLK>::STAGE, VB = Est<BLK>::VB;
     extern __shared__ __align__(16) char smem[];
     const int nb = K / BLK, ns = (K + SK - 1) / SK;
     constexpr int BPS = SK / BLK;                                   // blocks per stage
@@ -57,11 +62,11 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
     const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
-    char* meu = buf + (size_t)g * 2 * STAGE;                        // this group's two stage buffers
+    char* meu = buf + (size_t)g * 3 * STAGE;                        // this group's three stage buffers
 
-    // stage loads: thread tg of a group moves 16-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
+    // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
     // (row 0..31 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
-    const int vr = tg >> 3, vc = (tg & 7) * 16;
+    const int vr = tg >> 3, vc = (tg & 7) * VB;
     const int8_t* src[5];
     src[0] = A + (size_t)(row0 + vr) * K + vc;
 #pragma unroll
@@ -70,7 +75,13 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     auto busca = [&](int st) {
         const bool ok = st * SK + vc < K;
 #pragma unroll
-        for (int i = 0; i < 5; i++) reg[i] = ok ? *reinterpret_cast<const int4*>(src[i] + (size_t)st * SK) : make_int4(0, 0, 0, 0);
+        for (int i = 0; i < 5; i++) {
+            if constexpr (VB == 16) reg[i] = ok ? *reinterpret_cast<const int4*>(src[i] + (size_t)st * SK) : make_int4(0, 0, 0, 0);
+            else {
+                const int2 t = ok ? *reinterpret_cast<const int2*>(src[i] + (size_t)st * SK) : make_int2(0, 0);
+                reg[i] = make_int4(t.x, t.y, 0, 0);
+            }
+        }
     };
     auto guarda = [&](int par) {
         char* d = meu + par * STAGE + vr * LD + vc;
@@ -78,10 +89,20 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
         for (int i = 0; i < 5; i++) {
             int2* q = reinterpret_cast<int2*>(d + 32 * i * LD);
             q[0] = make_int2(reg[i].x, reg[i].y);
-            q[1] = make_int2(reg[i].z, reg[i].w);
+            if constexpr (VB == 16) q[1] = make_int2(reg[i].z, reg[i].w);
         }
     };
+    int4 reg2[5];                                                   // second register set: loads run two stages ahead
+    auto busca2 = [&](int st) {
+        int4 t[5];
+#pragma unroll
+        for (int i = 0; i < 5; i++) t[i] = reg[i];
+        busca(st);
+#pragma unroll
+        for (int i = 0; i < 5; i++) { reg2[i] = reg[i]; reg[i] = t[i]; }
+    };
     if (g < ns) busca(g);                                           // first stage in flight during the exponent staging
+    if (g + KS < ns) busca2(g + KS);                                // and the second
 
     // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
     const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
@@ -134,10 +155,9 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     __syncthreads();
 
     int acc[2][2][4] = {};
-    int par = 0;
-    for (int st = g; st < ns; st += KS) {
-        if (st + KS < ns) busca(st + KS);                           // next stage of this group in flight
-        const char* tile = meu + par * STAGE;
+    // stage k of this group (k = 0, 1, ...) is stage g + k KS, held in buffer k % 3. In iteration k the loads of
+    // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored.
+    auto calcula = [&](const char* tile, int st) {
 #pragma unroll
         for (int bl = 0; bl < BPS; bl++) {
             const int b = st * BPS + bl;
@@ -174,12 +194,29 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
                         acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
                     }
         }
-        par ^= 1;
-        if (st + KS < ns) guarda(par);
+    };
+    const int nk = g < ns ? (ns - g + KS - 1) / KS : 0;            // stages of this group
+    for (int k = 0; k < nk; k += 2) {
+        // even k: new loads into reg, the pending stage k + 1 sits in reg2
+        if (k + 2 < nk) busca(g + (k + 2) * KS);
+        calcula(meu + (k % 3) * STAGE, g + k * KS);
+        if (k + 1 < nk) {
+#pragma unroll
+            for (int i = 0; i < 5; i++) { const int4 t = reg2[i]; reg2[i] = reg[i]; reg[i] = t; }
+            guarda((k + 1) % 3);                                    // stores reg (stage k + 1)
+#pragma unroll
+            for (int i = 0; i < 5; i++) { const int4 t = reg2[i]; reg2[i] = reg[i]; reg[i] = t; }
+        }
+        __syncthreads();
+        if (k + 1 >= nk) break;
+        // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
+        if (k + 3 < nk) busca2(g + (k + 3) * KS);
+        calcula(meu + ((k + 1) % 3) * STAGE, g + (k + 1) * KS);
+        if (k + 2 < nk) guarda((k + 2) % 3);                        // stores reg (stage k + 2)
         __syncthreads();
     }
     // groups with fewer stages still take part in every barrier of the loop above
-    for (int st = g + ((ns - g + KS - 1) / KS) * KS; st < ((ns + KS - 1) / KS) * KS; st += KS) __syncthreads();
+    for (int k = nk; k < (ns + KS - 1) / KS; k++) __syncthreads();
 
     // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout
     int base[16];
@@ -267,10 +304,10 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
 }
 
 // dynamic LDS bytes for nb K-blocks and KS K-splits
-static inline size_t gemm_lds(int nb, int ks) {
+static inline size_t gemm_lds(int nb, int ks, int blk) {
     using namespace gemm;
     const size_t fixo = (size_t)(BM + BN) * 4 + (size_t)nb * BM * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
-    size_t area = (size_t)ks * 2 * STAGE;
+    size_t area = (size_t)ks * 3 * (blk == 32 ? Est<32>::STAGE : Est<128>::STAGE);
     const size_t exp_bruto = (size_t)nb * (BM + BN) + 16;
     const size_t acc = (size_t)ks * BM * (BN + PAD) * 4;
     if (exp_bruto > area) area = exp_bruto;

@@ -118,16 +118,17 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
 
 // ---------------------------------------------------------------------------------------------- transpoe
 // X [R, C] blocked along C -> Y [C, R] blocked along R: Y = quant(m^T, expand(E)^T) (ops.py:121-123).
-// Tile 128 rows x 64 cols. Lane (cg, rc) owns 4 columns (one 32-bit LDS word) x 8 rows: it reads 8 words,
-// unpacks 32 values and runs 4 block quantizations side by side; the LPB = BLK/8 lanes of a column block are
-// consecutive lanes. Rows of the LDS tile are 17 words long so the word reads spread over the banks.
-template <int BLK>
-__global__ void __launch_bounds__(256) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
-                                                  int8_t* __restrict__ EY, int R, int C, int kid) {
-    constexpr int LPB = BLK / 8;
-    __shared__ int tile[128][17];
-    __shared__ int8_t er[128][2];
-    const int r0 = blockIdx.y * 128, c0 = blockIdx.x * 64, tid = threadIdx.x, nbx = C / BLK;
+// Tile TR rows x 64 cols (TR = 64 at BLK=32, 128 at BLK=128: a multiple of the output block), 2 TR threads.
+// Lane (cg, rc) owns 4 columns (one 32-bit LDS word) x 8 rows: it reads 8 words, unpacks 32 values and runs 4
+// block quantizations side by side; the LPB = BLK/8 lanes of a column block are consecutive lanes. Rows of the
+// LDS tile are 17 words long so the word reads spread over the banks.
+template <int BLK, int TR>
+__global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
+                                                     int8_t* __restrict__ EY, int R, int C, int kid) {
+    constexpr int LPB = BLK / 8, RC = TR / 8;
+    __shared__ int tile[TR][17];
+    __shared__ int8_t er[TR][2];
+    const int r0 = blockIdx.y * TR, c0 = blockIdx.x * 64, tid = threadIdx.x, nbx = C / BLK;
     {
         const int row = tid >> 1, half = tid & 1;
         const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
@@ -138,7 +139,7 @@ __global__ void __launch_bounds__(256) k_transpoe(const int8_t* __restrict__ X, 
         er[row][half] = EX[(size_t)(r0 + row) * nbx + (c0 + half * 32) / BLK];
     }
     __syncthreads();
-    const int cg = tid >> 4, rc = tid & 15;            // columns c0 + 4 cg .. +3, rows r0 + 8 rc .. +7
+    const int cg = tid / RC, rc = tid % RC;                         // columns c0 + 4 cg .. +3, rows r0 + 8 rc .. +7
     int m[4][8], e[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {

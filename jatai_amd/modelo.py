@@ -55,6 +55,19 @@ class Modelo:
         self.error_feedback = True
         self.estatisticas = False
         self.perda_inteira = False      # True: passo returns (d_alvo, soma) instead of the float64 loss
+        # One fused optimizer launch over all tensors when the backend has it (OpsHip): the weight gradients are
+        # written to persistent raw buffers whose addresses, with the weights', momenta's and residuals', sit in
+        # a device table built once. Same results as momento then peso per tensor.
+        self.otimizador_fundido = hasattr(ops, "otimizador")
+        self._gbuf, self._tabela = None, None
+
+    def _prepara_otimizador(self):
+        if self._gbuf is None:
+            ordem = ["out"] + [f"{w}{l}" for l in reversed(range(self.L)) for w in ("Wd", "Wup", "Wo", "Wqkv")] + ["emb"]
+            self._gbuf = {n: (torch.empty(self.p[n][0].shape, dtype=torch.int32, device=self.dev),
+                              torch.empty(self.p[n][0].shape, dtype=torch.int16, device=self.dev)) for n in ordem}
+            self._tabela = self.ops.tabela_otimizador([(self._gbuf[n], self.mom[n], self.p[n], self.res[n]) for n in ordem])
+        return self._gbuf
 
     def _st(self, nome, t, zeros_normais=False):
         if self.estatisticas:
@@ -103,9 +116,13 @@ class Modelo:
             return perda
         T_ = ops.transpoe
         grads = {}
+        gb = self._prepara_otimizador() if self.otimizador_fundido else None
+
+        def grad_w(n, A, B):        # weight gradient, raw: into the persistent buffer when the optimizer is fused
+            return ops.gemm(A, B, cru=True, saida=gb[n]) if gb else ops.gemm(A, B, cru=True)
         with reg.trecho("backward"):
             with reg.trecho("saida"):
-                grads["out"] = ops.gemm(T_(g), T_(nf), cru=True)
+                grads["out"] = grad_w("out", T_(g), T_(nf))
                 gx = ops.gemm(g, T_(p["out"]))
                 gx = ops.rms_back(gx, nf, cf)
                 self._st("grad_saida", gx)
@@ -115,9 +132,9 @@ class Modelo:
                 n1, c1, qkv, P, om, n2, c2, h, a = caches[l]
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("mlp"):
-                        grads[f"Wd{l}"] = ops.gemm(T_(gx), T_(a), cru=True)
+                        grads[f"Wd{l}"] = grad_w(f"Wd{l}", T_(gx), T_(a))
                         gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
-                        grads[f"Wup{l}"] = ops.gemm(T_(gh), T_(n2), cru=True)
+                        grads[f"Wup{l}"] = grad_w(f"Wup{l}", T_(gh), T_(n2))
                         gn = ops.gemm(gh, T_(p[f"Wup{l}"]))
                         if r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n2, c2))
@@ -126,10 +143,10 @@ class Modelo:
                             gx = ops.soma(gx, ops.rms_back(gn, n2, c2))
                         self._st(f"c{l}.grad_mlp", gh, zeros_normais=True)
                     with reg.trecho("atencao"):
-                        grads[f"Wo{l}"] = ops.gemm(T_(gx), T_(om), cru=True)
+                        grads[f"Wo{l}"] = grad_w(f"Wo{l}", T_(gx), T_(om))
                         go = ops.gemm(gx, T_(p[f"Wo{l}"]))
                         gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
-                        grads[f"Wqkv{l}"] = ops.gemm(T_(gq), T_(n1), cru=True)
+                        grads[f"Wqkv{l}"] = grad_w(f"Wqkv{l}", T_(gq), T_(n1))
                         gn = ops.gemm(gq, T_(p[f"Wqkv{l}"]))
                         if r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n1, c1))
@@ -139,8 +156,11 @@ class Modelo:
                         self._st(f"c{l}.grad_qkv", gq); self._st(f"c{l}.grad_residuo", gx)
             with reg.trecho("embedding"):
                 um = ops.um_quente(tok, self.V)
-                grads["emb"] = ops.gemm(T_(um), T_(gx), cru=True)
+                grads["emb"] = grad_w("emb", T_(um), T_(gx))
         with reg.trecho("otimizador"):
+            if self.otimizador_fundido:
+                ops.otimizador(self._tabela, k_lr, self.error_feedback)
+                return perda
             for n, gr in grads.items():
                 with reg.trecho(n):
                     self.mom[n] = ops.momento(gr, self.mom[n])
@@ -164,6 +184,8 @@ class PassoGravado:
         self.grafo = torch.cuda.CUDAGraph()
         est, vig, pi = modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira
         modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = False, False, True
+        if modelo.otimizador_fundido:
+            modelo._prepara_otimizador()          # buffers and the device table exist before capture
         torch.cuda.synchronize()
         self.reg.lancamentos = []
         try:

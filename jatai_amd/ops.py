@@ -27,7 +27,7 @@ LIB = os.path.join(AQUI, "libjatai.so")
 FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_back", "jt_momento", "jt_peso", "jt_transpoe",
            "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
-           "jt_bloco_atual")
+           "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -98,13 +98,20 @@ class OpsHip:
                        f"{op}: M multiplo de 32, N de 128, K de {BLK} e K <= 4096 (M={M}, N={N}, K={K})")
         return M, N, K
 
-    def gemm(self, A, B, cru=False):
+    def gemm(self, A, B, cru=False, saida=None):
+        """`saida`: optional preallocated raw output (int32 [M, N], int16 [M, N]) for cru=True."""
         reg = self.reg
         reg.confere_bloco("A", A); reg.confere_bloco("B", B)
         (a, ea), (b, eb) = A, B
         M, N, K = self._formas_gemm("gemm", a, b)
         if cru:
-            C = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(M, N, dtype=torch.int16, device=a.device))
+            if saida is not None:
+                reg.exige(saida[0].dtype == torch.int32 and saida[1].dtype == torch.int16 and tuple(saida[0].shape) == (M, N)
+                          and tuple(saida[1].shape) == (M, N) and saida[0].is_contiguous() and saida[1].is_contiguous(),
+                          f"gemm: saida deve ser (int32, int16) contiguos de forma {(M, N)}")
+                C = saida
+            else:
+                C = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(M, N, dtype=torch.int16, device=a.device))
             self._lanca("gemm_cru", "jt_gemm", (a, ea, b, eb, None, None, C[0], C[1], M, N, K, 1), dict(A=a, EA=ea, B=b, EB=eb), (M, N))
         else:
             C = self._novo_bloco(M, N, a.device)
@@ -288,6 +295,27 @@ class OpsHip:
         n = Mom[0].numel() // BLK
         self._lanca("momento", "jt_momento", (Gc[0], Gc[1], Mom[0], Mom[1], n), dict(g=Gc[0], ge=Gc[1]), tuple(Mom[0].shape), longos=(4,))
         return Mom
+
+    # no reference counterpart: momento + peso of every tensor in one launch
+    def tabela_otimizador(self, itens):
+        """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] with fixed addresses (updated in place)."""
+        linhas, inicio = [], 0
+        for Gc, Mom, W, R in itens:
+            self.reg.confere_cru("grad", Gc)
+            for n, t in (("momento", Mom), ("W", W), ("residuo", R)):
+                self.reg.confere_bloco(n, t)
+            nb = W[0].numel() // BLK
+            self.reg.exige(Gc[0].numel() == W[0].numel() == Mom[0].numel() == R[0].numel(), "otimizador: formas diferentes")
+            linhas.append([t.data_ptr() for t in (Gc[0], Gc[1], Mom[0], Mom[1], W[0], W[1], R[0], R[1])] + [inicio, nb])
+            inicio += nb
+        self.reg.exige(0 < len(linhas) <= 256, "otimizador: de 1 a 256 tensores")
+        self.reg.exige(self.lib.jt_tab_otim_bytes() == 80, "otimizador: tamanho de entrada da tabela inesperado")
+        tab = torch.tensor(linhas, dtype=torch.int64).to(W[0].device)
+        return tab, len(linhas), inicio
+
+    def otimizador(self, tabela, k, ef):
+        tab, ntab, nblocos = tabela
+        self._lanca("otimizador", "jt_otimizador", (tab, ntab, nblocos, k, int(ef)), dict(), (nblocos * BLK,), longos=(2,))
 
     def peso(self, W, Mom, R, k, ef):
         for n, t in (("W", W), ("momento", Mom), ("residuo", R)):

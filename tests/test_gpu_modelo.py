@@ -5,6 +5,8 @@
   (trace written from OpsRef + Modelo.passo, the reference's `conferir 2` protocol, treino_cuda.py:48-60);
 * the hipGraph-captured step replays to the same bits as eager steps, for every replay, with eager work and
   synchronization between replays; and the per-step (d_alvo, soma) of the golden loss trace;
+* the fused optimizer (momento + peso of all 50 tensors in one launch) leaves weights, momenta and residuals
+  bit-identical to momento then peso per tensor, with and without error feedback;
 * a token outside the vocabulary inside a replayed graph raises ErroJatai naming op embed, scope
   "forward / embedding", row 401, value 300 (the reference's teste_erro_grafo.py:13-30).
 """
@@ -99,3 +101,25 @@ def test_erro_no_grafo():
     msg = str(e.value)
     assert "forward / embedding" in msg and "linha 401, coluna 0" in msg and "valor    : 300" in msg, msg
     assert "operacao : embed" in msg
+
+
+@pytest.mark.parametrize("ef", [True, False])
+def test_otimizador_fundido_igual_por_tensor(ef):
+    from jatai_amd.modelo import Modelo
+    g = TR.gold()
+    f = g["forma"]
+    ops, reg = _ops()
+    mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", ops, reg)
+    fundido, separado = mk(), mk()
+    separado.otimizador_fundido = False
+    assert fundido.otimizador_fundido
+    for m in (fundido, separado):
+        m.error_feedback = ef
+    reg.novo_passo(0)
+    for p in range(3):
+        tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], "cuda")
+        a = float(fundido.passo(tok, alvo, k_lr=f["k_lr"]))
+        b = float(separado.passo(tok, alvo, k_lr=f["k_lr"]))
+        assert a == b, (p, a, b)
+    reg.fim_passo()
+    assert _estado(fundido) == _estado(separado)

@@ -40,6 +40,7 @@ def roda(ops, reg, dev, passos, host):
     f = g["forma"]
     rec = CS.Gravador(ops, host)
     m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, rec, reg)
+    m.otimizador_fundido = False        # the trace records momento and peso per tensor, as the spec runs them
     init = {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()}
     out = []
     for p in range(passos):
