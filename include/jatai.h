@@ -67,6 +67,11 @@ int jt_tab_otim_bytes(void);           /* sizeof of one table entry (80) */
 
 /* ---- re-blocking, gathers (jatai_cuda.cu:1155-1166). transpoe: R % 128 == 0, C % 64 == 0. */
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid);
+/* no reference counterpart: n transposes in launches of up to 64 tensors. `entradas` is a HOST array of n entries
+ * {const void* X; const void* EX; void* Y; void* EY; int R; int C;} (device pointers inside); entry i equals
+ * jt_transpoe(X, EX, Y, EY, R, C, kid + i). */
+int jt_transpoe_lote(const void* entradas, int n, int kid);
+int jt_entrada_t_bytes(void);          /* sizeof of one entry (40) */
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid);
 int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid);
 

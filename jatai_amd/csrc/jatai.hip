@@ -29,7 +29,7 @@ __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long lo
 
 static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
-static int g_alvo_wg = 512;             // GEMM K-split target: workgroups of 4 waves wanted per launch
+static int g_alvo_wg = 1024;            // GEMM K-split target: tiles x K-splits per launch
 static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
 static int g_atencao_mfma = 1;          // head width 64: matrix-core attention (1) or the dot2 kernels (0)
 
@@ -54,7 +54,7 @@ static void lds_max(K* k, size_t lds) {
     int i = 0;
     while (i < n && chave[i] != f) i++;
     if (i < n && feito[i] >= lds) return;
-    hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);   // a refusal surfaces at the launch
     if (i == n && n < 64) { chave[n] = f; feito[n] = lds; n++; }
     else if (i < n) feito[i] = lds;
 }
@@ -77,7 +77,7 @@ int jt_erro_limpa() {
 }
 int jt_sincroniza() { return (int)hipDeviceSynchronize(); }
 void jt_stream(void* st) { g_stream = (hipStream_t)st; }
-void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 512; }
+void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 1024; }
 void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one tile shape; kept for the interface
 void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
 // No reference counterpart: selects the matrix-core (1, default) or dot2 (0) attention kernels at head width 64.
@@ -98,14 +98,16 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk;
-    // K-splits inside a workgroup: up to 4, while the grid has fewer than g_alvo_wg x 4 waves and each split
-    // keeps at least two K-blocks
+    // K-splits inside a workgroup: doubled (up to 4) while tiles x splits stays within g_alvo_wg and each split
+    // keeps at least four K-blocks. A split adds a group of 4 waves to the workgroup: more resident waves per SIMD
+    // to hide LDS and MFMA latency under the VALU rounding work, as long as the grid does not already fill the
+    // chip (1024 = 256 CUs x 4 SIMDs).
     const long long tiles = (long long)(M / BM) * (N / BN);
-    // (each K-split holds two stage buffers in LDS -- 11 KiB at BLK=32, 21 KiB at BLK=128, 160 KiB per workgroup --
-    // and the fused epilogues of modes 2-4 would spill at 1024 threads)
+    // (each K-split holds three stage buffers in LDS -- 11 KiB each at BLK=32, 21 KiB at BLK=128, 160 KiB per
+    // workgroup -- and the fused epilogues of modes 2-4 would spill at 1024 threads)
     const int ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
     int ks = 1;
-    while (ks < ksmax && tiles * 4 * ks < (long long)g_alvo_wg * 4 && nb >= 4 * ks) ks *= 2;
+    while (ks < ksmax && tiles * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
     const dim3 grade(N / BN, M / BM);
     const size_t lds = gemm_lds(nb, ks, g_blk);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
@@ -233,6 +235,36 @@ int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, 
 #undef L
     return fim();
 }
+// No reference counterpart: n transposes in launches of up to 64 (host array of EntradaT, device pointers inside).
+// Each entry equals jt_transpoe(X, EX, Y, EY, R, C, kid + i).
+struct EntradaT { const void* X; const void* EX; void* Y; void* EY; int R; int C; };
+int jt_transpoe_lote(const void* entradas, int n, int kid) {
+    if (n < 0 || (n > 0 && !entradas)) return (int)hipErrorInvalidValue;
+    const EntradaT* e = (const EntradaT*)entradas;
+    const int TR = g_blk == 32 ? 64 : 128;
+    for (int base = 0; base < n; base += LOTE_T) {
+        LoteT L;
+        L.n = std::min(LOTE_T, n - base);
+        long long tot = 0;
+        for (int i = 0; i < L.n; i++) {
+            const EntradaT& x = e[base + i];
+            if (x.R <= 0 || x.C <= 0 || x.R % 128 || x.C % 64) return (int)hipErrorInvalidValue;
+            if (!alinhados(x.X, x.EX, x.Y, x.EY)) return (int)hipErrorInvalidValue;
+            L.X[i] = (const int8_t*)x.X; L.EX[i] = (const int8_t*)x.EX; L.Y[i] = (int8_t*)x.Y; L.EY[i] = (int8_t*)x.EY;
+            L.R[i] = x.R; L.C[i] = x.C; L.ini[i] = (int)tot;
+            tot += (long long)(x.R / TR) * (x.C / 64);
+        }
+        if (tot > 0x7fffffff) return (int)hipErrorInvalidValue;
+        L.ini[L.n] = (int)tot;
+        if (tot == 0) continue;
+        if (g_blk == 32) k_transpoe_lote<32, 64><<<(unsigned)tot, 128, 0, g_stream>>>(L, kid + base);
+        else k_transpoe_lote<128, 128><<<(unsigned)tot, 256, 0, g_stream>>>(L, kid + base);
+        const int r = fim();
+        if (r) return r;
+    }
+    return 0;
+}
+int jt_entrada_t_bytes() { return (int)sizeof(EntradaT); }
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid) {
     if (M <= 0 || D % g_blk || D % 16) return (int)hipErrorInvalidValue;
     if (!alinhados(Wm, WE, tok, Xm, XE)) return (int)hipErrorInvalidValue;

@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     int8_t* nb_s = reinterpret_cast<int8_t*>(na_s + (size_t)nb * BM);
     char* buf = reinterpret_cast<char*>(nb_s) + (((size_t)nb * BN + 15) & ~(size_t)15);
     int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nb], EB rows [BN][nb]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
     const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
@@ -157,42 +157,61 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     int acc[2][2][4] = {};
     // stage k of this group (k = 0, 1, ...) is stage g + k KS, held in buffer k % 3. In iteration k the loads of
     // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored.
-    auto calcula = [&](const char* tile, int st) {
+    // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
+    // LDS latency of block bl + 1 runs under the VALU work of block bl. Modes 3 and 4 (larger epilogues) go block
+    // by block: holding both blocks' products would cost a resident wave per SIMD.
+    constexpr bool ADIANTA = MODO < 3;
+    auto produtos = [&](const char* tile, int bl, v4i (&p)[2][2]) {
 #pragma unroll
-        for (int bl = 0; bl < BPS; bl++) {
-            const int b = st * BPS + bl;
-            if (b >= nb) break;
-            v4i p[2][2];
+        for (int ti = 0; ti < 2; ti++)
 #pragma unroll
-            for (int ti = 0; ti < 2; ti++)
+            for (int tj = 0; tj < 2; tj++) p[ti][tj] = v4i{0, 0, 0, 0};
 #pragma unroll
-                for (int tj = 0; tj < 2; tj++) p[ti][tj] = v4i{0, 0, 0, 0};
+        for (int k = 0; k < KST; k++) {
+            const int kb = (bl * KST + k) * 32 + 8 * lg;
+            long fa[2], fb[2];
 #pragma unroll
-            for (int k = 0; k < KST; k++) {
-                const int kb = (bl * KST + k) * 32 + 8 * lg;
-                long fa[2], fb[2];
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    fa[t] = *reinterpret_cast<const long*>(tile + (16 * t + lr) * LD + kb);
-                    fb[t] = *reinterpret_cast<const long*>(tile + (BM + wc + 16 * t + lr) * LD + kb);
-                }
-#pragma unroll
-                for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-                    for (int tj = 0; tj < 2; tj++) p[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], p[ti][tj], 0, 0, 0);
+            for (int t = 0; t < 2; t++) {
+                fa[t] = *reinterpret_cast<const long*>(tile + (16 * t + lr) * LD + kb);
+                fb[t] = *reinterpret_cast<const long*>(tile + (BM + wc + 16 * t + lr) * LD + kb);
             }
-            const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
-            const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
-            const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
 #pragma unroll
             for (int ti = 0; ti < 2; ti++)
 #pragma unroll
-                for (int tj = 0; tj < 2; tj++)
+                for (int tj = 0; tj < 2; tj++) p[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], p[ti][tj], 0, 0, 0);
+        }
+    };
+    auto arredonda = [&](int b, const v4i (&p)[2][2]) {
+        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
+        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
+        const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);                     // 4 - sa - sb
-                        acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
-                    }
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);                     // 4 - sa - sb
+                    acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
+                }
+    };
+    auto calcula = [&](const char* tile, int st) {
+        if constexpr (ADIANTA) {
+            v4i p[BPS][2][2];
+#pragma unroll
+            for (int bl = 0; bl < BPS; bl++)
+                if (st * BPS + bl < nb) produtos(tile, bl, p[bl]);
+#pragma unroll
+            for (int bl = 0; bl < BPS; bl++)
+                if (st * BPS + bl < nb) arredonda(st * BPS + bl, p[bl]);
+        } else {
+#pragma unroll
+            for (int bl = 0; bl < BPS; bl++) {
+                if (st * BPS + bl >= nb) break;
+                v4i p[2][2];
+                produtos(tile, bl, p);
+                arredonda(st * BPS + bl, p);
+            }
         }
     };
     const int nk = g < ns ? (ns - g + KS - 1) / KS : 0;            // stages of this group

@@ -123,12 +123,12 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
 // block quantizations side by side; the LPB = BLK/8 lanes of a column block are consecutive lanes. Rows of the
 // LDS tile are 17 words long so the word reads spread over the banks.
 template <int BLK, int TR>
-__global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
-                                                     int8_t* __restrict__ EY, int R, int C, int kid) {
+__device__ __forceinline__ void transpoe_tile(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
+                                              int8_t* __restrict__ EY, int R, int C, int bx, int by, int kid) {
     constexpr int LPB = BLK / 8, RC = TR / 8;
     __shared__ int tile[TR][17];
     __shared__ int8_t er[TR][2];
-    const int r0 = blockIdx.y * TR, c0 = blockIdx.x * 64, tid = threadIdx.x, nbx = C / BLK;
+    const int r0 = by * TR, c0 = bx * 64, tid = threadIdx.x, nbx = C / BLK;
     {
         const int row = tid >> 1, half = tid & 1;
         const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
@@ -157,4 +157,32 @@ __global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ 
         grava_i8(Y + o, q);
         if ((rc & (LPB - 1)) == 0) EY[(size_t)col * (R / BLK) + (r0 + rc * 8) / BLK] = (int8_t)E;
     }
+}
+
+template <int BLK, int TR>
+__global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
+                                                     int8_t* __restrict__ EY, int R, int C, int kid) {
+    transpoe_tile<BLK, TR>(X, EX, Y, EY, R, C, blockIdx.x, blockIdx.y, kid);
+}
+
+// Many transposes in one launch. The tensor list travels by value in the kernel arguments (no device table, so
+// a captured graph keeps it); tensor i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over its
+// (R / TR) x (C / 64) tiles.
+constexpr int LOTE_T = 64;
+struct LoteT {
+    const int8_t* X[LOTE_T];
+    const int8_t* EX[LOTE_T];
+    int8_t* Y[LOTE_T];
+    int8_t* EY[LOTE_T];
+    int R[LOTE_T], C[LOTE_T], ini[LOTE_T + 1];
+    int n;
+};
+
+template <int BLK, int TR>
+__global__ void __launch_bounds__(2 * TR) k_transpoe_lote(const LoteT L, int kid) {
+    const int t = blockIdx.x;
+    int i = 0;                                                      // uniform: kernel arguments, scalar loads
+    while (i + 1 < L.n && L.ini[i + 1] <= t) i++;
+    const int local = t - L.ini[i], ntx = L.C[i] / 64;
+    transpoe_tile<BLK, TR>(L.X[i], L.EX[i], L.Y[i], L.EY[i], L.R[i], L.C[i], local % ntx, local / ntx, kid + i);
 }

@@ -59,6 +59,9 @@ class Modelo:
         # written to persistent raw buffers whose addresses, with the weights', momenta's and residuals', sit in
         # a device table built once. Same results as momento then peso per tensor.
         self.otimizador_fundido = hasattr(ops, "otimizador")
+        # Transposes of the weights and of the forward activations used by the backward, computed together in
+        # batched launches right after the forward (same results as one transpoe per use).
+        self.transpostas_em_lote = hasattr(ops, "transpoe_lote")
         self._gbuf, self._tabela = None, None
 
     def _prepara_otimizador(self):
@@ -114,7 +117,17 @@ class Modelo:
         perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma)
         if k_lr is None:
             return perda
-        T_ = ops.transpoe
+        prontas = {}
+        if self.transpostas_em_lote:
+            with reg.trecho("transpostas"):
+                pesos = [p[f"{w}{l}"] for l in range(self.L) for w in ("Wd", "Wup", "Wo", "Wqkv")] + [p["out"]]
+                ativ = [t for c in caches for t in (c[8], c[5], c[4], c[0])] + [nf]     # a, n2, om, n1 per layer
+                for X, Y in zip(pesos + ativ, ops.transpoe_lote(pesos) + ops.transpoe_lote(ativ)):
+                    prontas[id(X[0])] = Y
+
+        def T_(X):
+            Y = prontas.get(id(X[0]))
+            return Y if Y is not None else ops.transpoe(X)
         grads = {}
         gb = self._prepara_otimizador() if self.otimizador_fundido else None
 

@@ -27,7 +27,7 @@ LIB = os.path.join(AQUI, "libjatai.so")
 FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_back", "jt_momento", "jt_peso", "jt_transpoe",
            "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
-           "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes")
+           "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -152,6 +152,32 @@ class OpsHip:
         Y = self._novo_bloco(C, R, m.device)
         self._lanca("transpoe", "jt_transpoe", (m, E, Y[0], Y[1], R, C), dict(X=m, EX=E), (C, R))
         return Y
+
+    # no reference counterpart: many transposes in one launch (64 tensors per launch)
+    def transpoe_lote(self, Xs):
+        """[transpoe(X) for X in Xs], computed by batched launches; launch ids are consecutive, one per tensor."""
+        if not Xs:
+            return []
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        self.reg.exige(self.lib.jt_entrada_t_bytes() == 40, "transpoe_lote: tamanho de entrada inesperado")
+        Ys, tab = [], (ctypes.c_longlong * (5 * len(Xs)))()
+        kid0 = None
+        for i, X in enumerate(Xs):
+            self.reg.confere_bloco("X", X)
+            m, E = X
+            R, C = m.shape
+            self.reg.exige(R % 128 == 0 and C % 64 == 0, f"transpoe: linhas {R} nao multiplo de 128 ou colunas {C} nao multiplo de 64")
+            Y = self._novo_bloco(C, R, m.device)
+            Ys.append(Y)
+            kid = self.reg.registra("transpoe", dict(X=m, EX=E), (C, R), tempo=(i == 0))
+            kid0 = kid if kid0 is None else kid0
+            self.reg.exige(kid == kid0 + i, "transpoe_lote: ids de lancamento nao consecutivos")
+            tab[5 * i:5 * i + 5] = [m.data_ptr(), E.data_ptr(), Y[0].data_ptr(), Y[1].data_ptr(), (C << 32) | R]
+        r = self.lib.jt_transpoe_lote(ctypes.cast(tab, ctypes.c_void_p), ctypes.c_int(len(Xs)), ctypes.c_int(kid0))
+        self.reg.depois(kid0, r)
+        return Ys
 
     def quant(self, Cc):
         self.reg.confere_cru("C", Cc)

@@ -82,10 +82,11 @@ class Registro:
         if self.lib is not None:
             self.lib.jt_erro_limpa()
 
-    def registra(self, op, entradas, forma_saida):
+    def registra(self, op, entradas, forma_saida, tempo=True):
+        """tempo=False: a further launch id of a batched launch timed under the batch's first id."""
         kid = len(self.lancamentos)
         self.lancamentos.append({"op": op, "trecho": self.onde(), "entradas": entradas, "forma": forma_saida})
-        if self.perfil:
+        if self.perfil and tempo:
             ini, fim = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             ini.record()
             self.eventos.append((op, ini, fim))

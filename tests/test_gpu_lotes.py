@@ -1,0 +1,53 @@
+"""Batched launches that have no reference counterpart, against the per-tensor ops they replace (bit-exact):
+
+* transpoe_lote over 70 tensors of mixed shapes (two launches: 64 tensors per launch) equals transpoe of each,
+  at BLK 32 and 128, and each result equals the CPU oracle's transpose;
+* the model step with batched transposes leaves weights, momenta and residuals identical to one transpoe per use.
+"""
+import numpy as np
+import pytest
+import torch
+
+import recipe as R
+from backends import CPU, GPU, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_transpoe_lote_igual_a_transpoe(blk):
+    gpu, cpu = GPU(blk, vigiar=True), CPU(blk)
+    formas = [(128 * (1 + i % 4), 64 * (2 + i % 5)) for i in range(70)]
+    formas = [(r, c - c % blk if c % blk else c) for r, c in formas]
+    xs_h = [R.bloco(R.substream(7, f"lote {i}"), r, c, blk, espalha=6, e0=-6) for i, (r, c) in enumerate(formas)]
+    xs = [tuple(gpu.dev(a) for a in x) for x in xs_h]
+    lote = gpu.ops.transpoe_lote(xs)
+    um = [gpu.ops.transpoe(x) for x in xs]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(lote, um)):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"tensor {i} {formas[i]}"
+    for i in (0, 33, 69):
+        ref = cpu.ops.transpoe(tuple(cpu.dev(a) for a in xs_h[i]))
+        assert np.array_equal(host(lote[i][0]), host(ref[0])) and np.array_equal(host(lote[i][1]), host(ref[1]))
+
+
+def test_modelo_transpostas_em_lote():
+    import traco as TR
+    from jatai_amd import ops as O
+    from jatai_amd.modelo import Modelo
+    from jatai_amd.registro import Registro
+    from backends import LOGS
+    O.BLK = 128
+    reg = Registro(LOGS, "lotes", vigiar=False, eco=False)
+    ops = O.OpsHip(reg)
+    f = TR.gold()["forma"]
+    mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", ops, reg)
+    a, b = mk(), mk()
+    b.transpostas_em_lote = False
+    assert a.transpostas_em_lote
+    reg.novo_passo(0)
+    for p in range(2):
+        tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], "cuda")
+        assert float(a.passo(tok, alvo, k_lr=f["k_lr"])) == float(b.passo(tok, alvo, k_lr=f["k_lr"]))
+    est = lambda m: [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
+    assert est(a) == est(b)

@@ -1,6 +1,8 @@
 """One full training step at the BASELINE config-4 widths (D=512, 8 heads x 64, FF=2048, V=256, T=256, BLK=32),
 with 2 layers and 2 sequences: every op output of the HIP path equals the CPU oracle's (jatai_amd.modelo.Modelo
-on both backends, same init and tokens). Also checks the step is stable under hipGraph replay."""
+on both backends, same init and tokens); the step with batched transposes and the fused optimizer leaves the
+same weights, momenta and residuals. A third step replayed
+from a captured hipGraph (fused model) equals the eager op-by-op step."""
 import pytest
 import torch
 
@@ -24,6 +26,9 @@ def test_passo_config4_vs_oraculo():
     cpu = CS.Gravador(OpsOraculo(32), host)
     mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg)
     mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub())
+    mg.otimizador_fundido = mg.transpostas_em_lote = False     # op-by-op comparison: the oracle's op sequence
+    mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg)  # batched transposes + fused optimizer
+    assert mf.otimizador_fundido and mf.transpostas_em_lote
     for p in range(2):
         x = R.tokens(R.substream(31, f"b4 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
         tok = torch.from_numpy(x[:, :-1].copy()).long()
@@ -31,10 +36,26 @@ def test_passo_config4_vs_oraculo():
         gpu.log, cpu.log = [], []
         reg.novo_passo(p)
         pg = float(mg.passo(tok.cuda(), alvo.cuda(), k_lr=4))
+        pf = float(mf.passo(tok.cuda(), alvo.cuda(), k_lr=4))
         reg.fim_passo()
         pc = float(mc.passo(tok, alvo, k_lr=4))
         assert len(gpu.log) == len(cpu.log)
         for k, (a, b) in enumerate(zip(gpu.log, cpu.log)):
             assert list(a) == list(b), f"step {p}, op #{k} '{b[0]}' differs from the oracle"
         assert abs(pg - pc) <= 1e-12 * abs(pc)
+        assert pf == pg
+    est = lambda m: [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
+    assert est(mf) == est(mg), "fused step differs from the op-by-op step"
+    # a third step: the fused model as a captured hipGraph, the op-by-op model eagerly
+    from jatai_amd.modelo import PassoGravado
+    pgraf = PassoGravado(mf, Bt, T, 4)
+    x = R.tokens(R.substream(31, "b4 2"), Bt * (T + 1), V).reshape(Bt, T + 1)
+    tok, alvo = torch.from_numpy(x[:, :-1].copy()).long().cuda(), torch.from_numpy(x[:, 1:].copy()).long().cuda()
+    reg.novo_passo(2)
+    a = float(pgraf(tok, alvo))
+    torch.cuda.synchronize()
+    reg.fim_passo()
+    b = float(mg.passo(tok, alvo, k_lr=4))
+    assert a == b
+    assert est(mf) == est(mg), "graph-replayed fused step differs from the eager op-by-op step"
     O.BLK = 128

@@ -40,7 +40,8 @@ def roda(ops, reg, dev, passos, host):
     f = g["forma"]
     rec = CS.Gravador(ops, host)
     m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, rec, reg)
-    m.otimizador_fundido = False        # the trace records momento and peso per tensor, as the spec runs them
+    m.otimizador_fundido = False        # the trace records momento, peso and transpoe per tensor, in the spec's order
+    m.transpostas_em_lote = False
     init = {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()}
     out = []
     for p in range(passos):
