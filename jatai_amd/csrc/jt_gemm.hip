@@ -28,16 +28,21 @@ namespace gemm {
 constexpr int BM = 32, BN = 128, PAD = 4;
 constexpr int ROWS = BM + BN;            // rows of a stage tile: 32 of A then 128 of B
 // bytes of K per row and stage: 64 at BLK=32 (two blocks; smaller buffers, more resident waves), 128 at BLK=128
+// BLK=32: 64-byte rows, unpadded, with the 8-byte chunk c of tile row r stored at chunk c ^ ((r >> 1) & 7): the
+// MFMA fragment reads (16 rows x one chunk per half-wave) and the stage stores (8 rows x 8 chunks per wave) then
+// touch every LDS bank once. BLK=128: 128-byte rows padded by 8 bytes.
 template <int BLK> struct Est {
     static constexpr int SK = BLK == 32 ? 64 : 128;
-    static constexpr int LD = SK + 8;    // LDS row stride of a stage tile (8-byte pad spreads rows over the banks)
+    static constexpr bool SWZ = BLK == 32;
+    static constexpr int LD = SWZ ? SK : SK + 8;   // LDS row stride of a stage tile
     static constexpr int STAGE = ROWS * LD;
     static constexpr int VB = SK / 8;    // bytes each of the 8 lanes of a row moves per stage
+    __device__ static int pos(int r, int c) { return r * LD + 8 * (SWZ ? (c ^ ((r >> 1) & 7)) : c); }   // byte offset of chunk c
 };
 }
 
 template <int BLK, int MODO, int KS>
-__global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
+__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                                    const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                                    int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
@@ -71,47 +76,41 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     src[0] = A + (size_t)(row0 + vr) * K + vc;
 #pragma unroll
     for (int i = 1; i < 5; i++) src[i] = B + (size_t)(col0 + vr + 32 * (i - 1)) * K + vc;
-    int4 reg[5];
-    auto busca = [&](int st) {
-        const bool ok = st * SK + vc < K;
+    int4 reg[5], reg2[5];                                           // two register sets: loads run two stages ahead
+    // The last stage may extend past K (nb not a multiple of the blocks per stage): its vectors past K re-read the
+    // row's last vector instead (a uniform test; those bytes land in blocks >= nb, which are never computed).
+    auto busca = [&](int st, int4 (&r)[5]) {
+        int o = st * SK;
+        if (o + SK > K) o = min(o + vc, K - VB) - vc;
 #pragma unroll
         for (int i = 0; i < 5; i++) {
-            if constexpr (VB == 16) reg[i] = ok ? *reinterpret_cast<const int4*>(src[i] + (size_t)st * SK) : make_int4(0, 0, 0, 0);
+            if constexpr (VB == 16) r[i] = *reinterpret_cast<const int4*>(src[i] + o);
             else {
-                const int2 t = ok ? *reinterpret_cast<const int2*>(src[i] + (size_t)st * SK) : make_int2(0, 0);
-                reg[i] = make_int4(t.x, t.y, 0, 0);
+                const int2 t = *reinterpret_cast<const int2*>(src[i] + o);
+                r[i] = make_int4(t.x, t.y, 0, 0);
             }
         }
     };
-    auto guarda = [&](int par) {
-        char* d = meu + par * STAGE + vr * LD + vc;
+    auto guarda = [&](int par, const int4 (&r)[5]) {
+        char* d = meu + par * STAGE;
 #pragma unroll
         for (int i = 0; i < 5; i++) {
-            int2* q = reinterpret_cast<int2*>(d + 32 * i * LD);
-            q[0] = make_int2(reg[i].x, reg[i].y);
-            if constexpr (VB == 16) q[1] = make_int2(reg[i].z, reg[i].w);
+            if constexpr (VB == 16) {
+                int2* q = reinterpret_cast<int2*>(d + (vr + 32 * i) * LD + vc);
+                q[0] = make_int2(r[i].x, r[i].y);
+                q[1] = make_int2(r[i].z, r[i].w);
+            } else {
+                *reinterpret_cast<int2*>(d + Est<BLK>::pos(vr + 32 * i, vc >> 3)) = make_int2(r[i].x, r[i].y);
+            }
         }
     };
-    int4 reg2[5];                                                   // second register set: loads run two stages ahead
-    auto busca2 = [&](int st) {
-        int4 t[5];
-#pragma unroll
-        for (int i = 0; i < 5; i++) t[i] = reg[i];
-        busca(st);
-#pragma unroll
-        for (int i = 0; i < 5; i++) { reg2[i] = reg[i]; reg[i] = t[i]; }
-    };
-    if (g < ns) busca(g);                                           // first stage in flight during the exponent staging
-    if (g + KS < ns) busca2(g + KS);                                // and the second
+    if (g < ns) busca(g, reg);                                      // first stage in flight during the exponent staging
+    if (g + KS < ns) busca(g + KS, reg2);                           // and the second
 
     // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
     const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
     const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
     const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
-    int xin[16], exin = 0;
-    if constexpr (MODO == 2 || MODO == 4) {
-        if (tid < 256) { le_i8(Xm + o, xin); exin = XE[oe]; }
-    }
     // exponents of the tile's 32 rows of A and 128 rows of B: two contiguous spans (32 nb and 128 nb bytes,
     // multiples of 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span
     // re-read its last vector and store it to a junk slot after the span, so neither side branches
@@ -151,7 +150,7 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
         nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nb + b] - rb_s[c], -100);
     }
     __syncthreads();                                                // staging bytes consumed: buffers are free
-    if (g < ns) guarda(0);
+    if (g < ns) guarda(0, reg);
     __syncthreads();
 
     int acc[2][2][4] = {};
@@ -160,7 +159,7 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
     // LDS latency of block bl + 1 runs under the VALU work of block bl. Modes 3 and 4 (larger epilogues) go block
     // by block: holding both blocks' products would cost a resident wave per SIMD.
-    constexpr bool ADIANTA = MODO < 3;
+    constexpr bool ADIANTA = true;
     auto produtos = [&](const char* tile, int bl, v4i (&p)[2][2]) {
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
@@ -168,12 +167,12 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
             for (int tj = 0; tj < 2; tj++) p[ti][tj] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int k = 0; k < KST; k++) {
-            const int kb = (bl * KST + k) * 32 + 8 * lg;
+            const int ch = (bl * KST + k) * 4 + lg;                   // 8-byte chunk of K within the stage
             long fa[2], fb[2];
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                fa[t] = *reinterpret_cast<const long*>(tile + (16 * t + lr) * LD + kb);
-                fb[t] = *reinterpret_cast<const long*>(tile + (BM + wc + 16 * t + lr) * LD + kb);
+                fa[t] = *reinterpret_cast<const long*>(tile + Est<BLK>::pos(16 * t + lr, ch));
+                fb[t] = *reinterpret_cast<const long*>(tile + Est<BLK>::pos(BM + wc + 16 * t + lr, ch));
             }
 #pragma unroll
             for (int ti = 0; ti < 2; ti++)
@@ -195,8 +194,35 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
                     acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
                 }
     };
+    // BLK=32, two blocks in the stage: the two rounded products are added in fp32 before the conversion; each is
+    // an integer below 2^23 in magnitude (|p| <= 32 * 128 * 128 = 2^19, scale <= 2^4), so the sum is exact
+    auto arredonda2 = [&](int b, const v4i (&p)[2][2], const v4i (&q)[2][2]) {
+        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
+        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
+        const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
+        const v4i ma0 = *reinterpret_cast<const v4i*>(na_s + (b + 1) * BM + 4 * lg);
+        const v4i ma1 = *reinterpret_cast<const v4i*>(na_s + (b + 1) * BM + 16 + 4 * lg);
+        const int mb0 = nb_s[(b + 1) * BN + wc + lr], mb1 = nb_s[(b + 1) * BN + wc + 16 + lr];
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);
+                    const int m = (ti ? ma1[i] : ma0[i]) + (tj ? mb1 : mb0);
+                    acc[ti][tj][i] += (int)(rintf(ldexpf((float)p[ti][tj][i], n)) + rintf(ldexpf((float)q[ti][tj][i], m)));
+                }
+    };
     auto calcula = [&](const char* tile, int st) {
-        if constexpr (ADIANTA) {
+        if constexpr (ADIANTA && BPS == 2) {
+            v4i p[BPS][2][2];
+#pragma unroll
+            for (int bl = 0; bl < BPS; bl++)
+                if (st * BPS + bl < nb) produtos(tile, bl, p[bl]);
+            if (st * BPS + 1 < nb) arredonda2(st * BPS, p[0], p[1]);
+            else arredonda(st * BPS, p[0]);
+        } else if constexpr (ADIANTA) {
             v4i p[BPS][2][2];
 #pragma unroll
             for (int bl = 0; bl < BPS; bl++)
@@ -216,28 +242,27 @@ __global__ void __launch_bounds__(256 * KS) k_gemm(const int8_t* __restrict__ A,
     };
     const int nk = g < ns ? (ns - g + KS - 1) / KS : 0;            // stages of this group
     for (int k = 0; k < nk; k += 2) {
-        // even k: new loads into reg, the pending stage k + 1 sits in reg2
-        if (k + 2 < nk) busca(g + (k + 2) * KS);
+        // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
+        if (k + 2 < nk) busca(g + (k + 2) * KS, reg);
         calcula(meu + (k % 3) * STAGE, g + k * KS);
-        if (k + 1 < nk) {
-#pragma unroll
-            for (int i = 0; i < 5; i++) { const int4 t = reg2[i]; reg2[i] = reg[i]; reg[i] = t; }
-            guarda((k + 1) % 3);                                    // stores reg (stage k + 1)
-#pragma unroll
-            for (int i = 0; i < 5; i++) { const int4 t = reg2[i]; reg2[i] = reg[i]; reg[i] = t; }
-        }
+        if (k + 1 < nk) guarda((k + 1) % 3, reg2);
         __syncthreads();
         if (k + 1 >= nk) break;
         // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
-        if (k + 3 < nk) busca2(g + (k + 3) * KS);
+        if (k + 3 < nk) busca(g + (k + 3) * KS, reg2);
         calcula(meu + ((k + 1) % 3) * STAGE, g + (k + 1) * KS);
-        if (k + 2 < nk) guarda((k + 2) % 3);                        // stores reg (stage k + 2)
+        if (k + 2 < nk) guarda((k + 2) % 3, reg);
         __syncthreads();
     }
     // groups with fewer stages still take part in every barrier of the loop above
     for (int k = nk; k < (ns + KS - 1) / KS; k++) __syncthreads();
 
-    // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout
+    // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout. The X operand
+    // of modes 2 and 4 is read here, not before the K loop, so its 16 registers do not cost a resident wave.
+    int xin[16], exin = 0;
+    if constexpr (MODO == 2 || MODO == 4) {
+        if (tid < 256) { le_i8(Xm + o, xin); exin = XE[oe]; }
+    }
     int base[16];
     if (tid < 256) {
         const int ra = ra_s[orow];

@@ -136,3 +136,30 @@ def test_split_k_same_bits():
         finally:
             gpu.ops.lib.jt_gemm_split(1024)
         assert all(np.array_equal(a, b) for a, b in zip(base, out)), f"split target {alvo}"
+
+
+@pytest.mark.parametrize("blk,K", [(32, 32), (32, 96), (32, 160), (32, 1376), (128, 128), (128, 384)])
+def test_gemm_k_impar_todos_os_modos(blk, K):
+    """K-block counts that leave a partial last stage (odd at BLK=32) and K = one block: the five GEMM modes, at
+    split targets that select 1, 2 and 4 K-splits, vs the oracle."""
+    M, N = 256, 256
+    gpu, cpu = GPU(blk), CPU(blk)
+    s = lambda t: R.substream(91, f"{blk} {K} {t}")
+    An = R.bloco(s("A"), M, K, blk, espalha=4, e0=-6)
+    Bn = R.bloco(s("B"), N, K, blk, espalha=4, e0=-9)
+    Xn = R.bloco(s("X"), M, N, blk, espalha=3, e0=-4)
+    res = {}
+    for nome, be in (("cpu", cpu), ("gpu", gpu)):
+        A, B, X = (tuple(be.dev(v) for v in t) for t in (An, Bn, Xn))
+        o = be.ops
+        res[nome] = lambda o=o, A=A, B=B, X=X: [o.gemm(A, B), o.gemm(A, B, cru=True), o.gemm_soma(A, B, X),
+                                                 o.gemm_relu2(A, B), o.gemm_relu2_back(A, B, X)]
+    ref = res["cpu"]()
+    for alvo in (1, 64, 1024):
+        gpu.ops.lib.jt_gemm_split(alvo)
+        try:
+            out = res["gpu"]()
+        finally:
+            gpu.ops.lib.jt_gemm_split(1024)
+        for modo, (a, b) in enumerate(zip(out, ref)):
+            _compara(a, b, f"BLK={blk} K={K} mode {modo} split target {alvo}")
