@@ -46,39 +46,49 @@ def args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--so-passo", action="store_true", help="time the step only (no GEMM sweep, no CPU baseline): for profiling")
+    ap.add_argument("--trafego", action="store_true",
+                    help="for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB device copy (the counters' calibration), "
+                         "then each GEMM shape of the step twice in its mode; prints the dispatch order")
     return ap.parse_args()
 
 
 def gemm_formas(c):
-    """(name, M, N, K, raw) of every GEMM of one step (modelo.py:51-134), one entry per distinct shape, with counts."""
+    """(M, N, K, mode, count) of every GEMM of one step (modelo.py:51-134), one entry per distinct shape and mode:
+    mode 0 block output, 1 raw, 2 + residual add, 3 + ReLU^2, 4 ReLU^2 backward."""
     M, D, FF, V, L = c["Bt"] * c["T"], c["D"], c["FF"], c["V"], c["L"]
     f = {}
 
-    def add(n, m, nn, k, cru, cont):
-        f[n] = (m, nn, k, cru, f.get(n, (0, 0, 0, 0, 0))[4] + cont)
-    add("fwd qkv", M, 3 * D, D, False, L)
-    add("fwd out-proj+soma", M, D, D, False, L)
-    add("fwd ffn-up+relu2", M, FF, D, False, L)
-    add("fwd ffn-down+soma", M, D, FF, False, L)
-    add("logits", M, V, D, True, 1)
-    add("dX out", M, D, V, False, 1)
-    add("dX ffn-down", M, FF, D, False, L)
-    add("dX ffn-up", M, D, FF, False, L)
-    add("dX out-proj", M, D, D, False, L)
-    add("dX qkv", M, D, 3 * D, False, L)
-    add("dW qkv", 3 * D, D, M, True, L)
-    add("dW out-proj", D, D, M, True, L)
-    add("dW ffn-up", FF, D, M, True, L)
-    add("dW ffn-down", D, FF, M, True, L)
-    add("dW out", V, D, M, True, 1)
-    add("dW emb", V, D, M, True, 1)
+    def add(n, m, nn, k, modo, cont):
+        f[n] = (m, nn, k, modo, f.get(n, (0, 0, 0, 0, 0))[4] + cont)
+    add("fwd qkv", M, 3 * D, D, 0, L)
+    add("fwd out-proj+soma", M, D, D, 2, L)
+    add("fwd ffn-up+relu2", M, FF, D, 3, L)
+    add("fwd ffn-down+soma", M, D, FF, 2, L)
+    add("logits", M, V, D, 1, 1)
+    add("dX out", M, D, V, 0, 1)
+    add("dX ffn-down+relu2_back", M, FF, D, 4, L)
+    add("dX ffn-up", M, D, FF, 0, L)
+    add("dX out-proj", M, D, D, 0, L)
+    add("dX qkv", M, D, 3 * D, 0, L)
+    add("dW qkv", 3 * D, D, M, 1, L)
+    add("dW out-proj", D, D, M, 1, L)
+    add("dW ffn-up", FF, D, M, 1, L)
+    add("dW ffn-down", D, FF, M, 1, L)
+    add("dW out", V, D, M, 1, 1)
+    add("dW emb", V, D, M, 1, 1)
     return f
 
 
+def gemm_kernel(O, ops, M, N, K, modo):
+    """Symbol and grid the library launches for this shape, to match rocprof rows."""
+    ks = ops.lib.jt_gemm_divisoes(M, N, K, modo)
+    return {"symbol": f"k_gemm<{O.BLK}, {modo}, {ks}>", "workgroups": (M // 32) * (N // 128), "threads": 256 * ks}
+
+
 def mede_gemms(O, ops, c, rep=20):
-    """Average launch duration of each GEMM shape with HIP events on the launch stream (the default stream,
-    which torch.cuda.Event records on), inputs resident in HBM, and 2MNK / duration."""
-    import numpy as np
+    """Average launch duration of each GEMM shape: `rep` launches of one shape captured as one hipGraph (on the
+    stream the library launches on, so launch gaps are the graph's, as in the training step), timed with HIP
+    events on that stream around the replay; inputs resident in HBM; 2MNK / duration."""
     import torch
     blk = c["BLK"]
     out = {}
@@ -88,20 +98,77 @@ def mede_gemms(O, ops, c, rep=20):
         m = torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda()
         E = (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda()
         return m, E
-    for nome, (M, N, K, cru, cont) in gemm_formas(c).items():
-        A, B = bloco(M, K, -8), bloco(N, K, -12)
-        for _ in range(3):
-            ops.gemm(A, B, cru=cru)
+    for nome, (M, N, K, modo, cont) in gemm_formas(c).items():
+        A, B, X = bloco(M, K, -8), bloco(N, K, -12), bloco(M, N, -6)
+        saida = ops.gemm(A, B, cru=True) if modo == 1 else None
+        chama = {0: lambda: ops.gemm(A, B), 1: lambda: ops.gemm(A, B, cru=True, saida=saida), 2: lambda: ops.gemm_soma(A, B, X),
+                 3: lambda: ops.gemm_relu2(A, B), 4: lambda: ops.gemm_relu2_back(A, B, X)}[modo]
+        chama()
         torch.cuda.synchronize()
+        grafo = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(grafo):
+            ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+            try:
+                for _ in range(rep):
+                    chama()
+            finally:
+                ops.lib.jt_stream(None)
+        grafo.replay()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ev[0].record()
-        for _ in range(rep):
-            ops.gemm(A, B, cru=cru)
-        ev[1].record()
+        with torch.cuda.stream(s):
+            ev[0].record(s)
+            for _ in range(3):
+                grafo.replay()
+            ev[1].record(s)
         torch.cuda.synchronize()
-        ms = ev[0].elapsed_time(ev[1]) / rep
-        out[nome] = dict(M=M, N=N, K=K, cru=cru, por_passo=cont, ms=ms, tops=2 * M * N * K / (ms * 1e-3) / 1e12)
+        ms = ev[0].elapsed_time(ev[1]) / (3 * rep)
+        out[nome] = dict(M=M, N=N, K=K, modo=modo, por_passo=cont, ms=ms, tops=2 * M * N * K / (ms * 1e-3) / 1e12,
+                         kernel=gemm_kernel(O, ops, M, N, K, modo))
+        del grafo
     return out
+
+
+def trafego_despacha(O, ops, c):
+    """Dispatches for the HBM-traffic counter runs: one plain copy of 256 MiB, then every GEMM shape twice (the
+    second launch of each is the one summarized), printed in launch order."""
+    import torch
+    x = torch.ones(256 << 20, dtype=torch.int8, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    print("dispatch: copy 268435456 bytes", flush=True)
+    del x, y
+    blk = c["BLK"]
+    g = torch.Generator().manual_seed(3)
+
+    def bloco(R, C, e0):
+        m = torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda()
+        E = (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda()
+        return m, E
+    for nome, (M, N, K, modo, cont) in gemm_formas(c).items():
+        A, B, X = bloco(M, K, -8), bloco(N, K, -12), bloco(M, N, -6)
+        chama = {0: lambda: ops.gemm(A, B), 1: lambda: ops.gemm(A, B, cru=True), 2: lambda: ops.gemm_soma(A, B, X),
+                 3: lambda: ops.gemm_relu2(A, B), 4: lambda: ops.gemm_relu2_back(A, B, X)}[modo]
+        torch.cuda.synchronize()
+        for _ in range(2):
+            chama()
+            torch.cuda.synchronize()
+        print(f"dispatch: {nome} {gemm_kernel(O, ops, M, N, K, modo)['symbol']} x2", flush=True)
+
+
+def trafego(nome):
+    """HBM bytes per launch of a GEMM shape from the committed counter summary (rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE, each scaled by the same counter on a plain copy of known size), or None if it has no line for it."""
+    arq = os.path.join(ROOT, "profiles", "gemm_hbm_traffic.txt")
+    if not os.path.exists(arq):
+        return None
+    for linha in open(arq):
+        if linha.startswith(nome + ":") and "traffic_bytes=" in linha:
+            return int(linha.split("traffic_bytes=")[1].split()[0])
+    return None
 
 
 def cpu_baseline(c, segundos):
@@ -150,6 +217,9 @@ def main():
     O.BLK = c["BLK"]
     reg = Registro("/tmp/jatai_bench", "bench", eco=False)
     ops = O.OpsHip(reg)
+    if a.trafego:
+        trafego_despacha(O, ops, c)
+        return
     dev = "cuda"
     m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, dev, ops, reg, r16=c["r16"])
     g = torch.Generator().manual_seed(1)
@@ -190,7 +260,9 @@ def main():
     dom_nome, dom = max(gem.items(), key=lambda kv: kv[1]["ms"] * kv[1]["por_passo"])
     achieved = 2 * dom["M"] * dom["N"] * dom["K"] / (dom["ms"] * 1e-3)
     roof = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_I8 / 1e12, "unit": "TOP/s",
-            "frac": achieved / PEAK_I8, "traffic": None, "kernel": f"k_gemm {dom_nome} M={dom['M']} N={dom['N']} K={dom['K']}",
+            "frac": achieved / PEAK_I8, "traffic": trafego(dom_nome),
+            "kernel": f"{dom['kernel']['symbol']} ({dom_nome} M={dom['M']} N={dom['N']} K={dom['K']}, "
+                      f"{dom['kernel']['workgroups']} workgroups x {dom['kernel']['threads']} threads)",
             "avg_ms": dom["ms"]}
     res = {"metric": METRIC, "value": tps, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
            "ms_per_step": dt / a.steps * 1e3, "higher_is_better": True, "scaling": "weak",
@@ -201,9 +273,9 @@ def main():
                       "graph_launches": nlanc, "parallelism": "single GPU"},
            "loss_last_step": perda,
            "roofline": roof,
-           "gemm_shapes": {k: {"M": v["M"], "N": v["N"], "K": v["K"], "ms": round(v["ms"], 5), "TOPS": round(v["tops"], 2),
-                               "pct_i8_peak": round(100 * v["tops"] * 1e12 / PEAK_I8, 2), "per_step": v["por_passo"]}
-                           for k, v in gem.items()},
+           "gemm_shapes": {k: {"M": v["M"], "N": v["N"], "K": v["K"], "mode": v["modo"], "ms": round(v["ms"], 5),
+                               "TOPS": round(v["tops"], 2), "pct_i8_peak": round(100 * v["tops"] * 1e12 / PEAK_I8, 2),
+                               "per_step": v["por_passo"], "kernel": v["kernel"]} for k, v in gem.items()},
            "gemm_ms_per_step_eager_sum": tot_gemm_ms}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, a.cpu_seconds)

@@ -43,6 +43,8 @@ int jt_bloco_atual(void);
  * Requires M % 32 == 0, N % 128 == 0, K % BLK == 0, K <= 4096 (the reference: M % 64, N % 128, K % 128). */
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
               const void* Xm, const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid);
+int jt_gemm_divisoes(int M, int N, int K, int modo);   /* no reference counterpart: K-splits jt_gemm_f uses
+                                                        * for a shape (workgroup = 256 x splits threads) */
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
             int M, int N, int K, int modo, int kid);
 

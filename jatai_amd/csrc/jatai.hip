@@ -61,6 +61,19 @@ static void lds_max(K* k, size_t lds) {
 
 #define POR_BLK(CHAMADA) (g_blk == 32 ? (CHAMADA(32)) : (CHAMADA(128)))
 
+// K-splits inside a workgroup: doubled (up to 4) while tiles x splits stays within g_alvo_wg and each split
+// keeps at least four K-blocks. A split adds a group of 4 waves to the workgroup: more resident waves per SIMD to
+// hide LDS and MFMA latency under the VALU rounding work, as long as the grid does not already fill the chip
+// (1024 = 256 CUs x 4 SIMDs). (Each K-split holds three stage buffers in LDS -- 10 KiB each at BLK=32, 21 KiB at
+// BLK=128, 160 KiB per workgroup -- and the fused epilogues of modes 2-4 would spill at 1024 threads.)
+static int gemm_divisoes(int M, int N, int K, int modo) {
+    const long long tiles = (long long)(M / gemm::BM) * (N / gemm::BN);
+    const int nb = K / g_blk, ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
+    int ks = 1;
+    while (ks < ksmax && tiles * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
+    return ks;
+}
+
 extern "C" {
 
 // ---------------------------------------------------------------------------------------------- state
@@ -92,22 +105,15 @@ int jt_bloco(int blk) {
 int jt_bloco_atual() { return g_blk; }
 
 // ---------------------------------------------------------------------------------------------- GEMM
+// No reference counterpart: the K-split count jt_gemm_f uses for a shape (workgroup = 256 x splits threads).
+int jt_gemm_divisoes(int M, int N, int K, int modo) { return gemm_divisoes(M, N, K, modo); }
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
               const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
     using namespace gemm;
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk;
-    // K-splits inside a workgroup: doubled (up to 4) while tiles x splits stays within g_alvo_wg and each split
-    // keeps at least four K-blocks. A split adds a group of 4 waves to the workgroup: more resident waves per SIMD
-    // to hide LDS and MFMA latency under the VALU rounding work, as long as the grid does not already fill the
-    // chip (1024 = 256 CUs x 4 SIMDs).
-    const long long tiles = (long long)(M / BM) * (N / BN);
-    // (each K-split holds three stage buffers in LDS -- 11 KiB each at BLK=32, 21 KiB at BLK=128, 160 KiB per
-    // workgroup -- and the fused epilogues of modes 2-4 would spill at 1024 threads)
-    const int ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
-    int ks = 1;
-    while (ks < ksmax && tiles * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
+    const int ks = gemm_divisoes(M, N, K, modo);
     const dim3 grade(N / BN, M / BM);
     const size_t lds = gemm_lds(nb, ks, g_blk);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
