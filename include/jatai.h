@@ -86,8 +86,22 @@ int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, vo
 
 /* ---- causal ALiBi attention, T % 64 == 0, T <= 256 (jatai_cuda.cu:1177-1194) */
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid);
+/* no reference counterpart: jt_atencao with a caller workspace of jt_atencao_ws_bytes(Bt, T, H, D) bytes (16-byte
+ * aligned); same outputs. At head width 64 on matrix cores (T <= 512) k and v are converted once per (sequence,
+ * head) into the workspace and each 16-row query tile's keys are split over four waves; otherwise it runs
+ * jt_atencao. */
+long long jt_atencao_ws_bytes(int Bt, int T, int H, int D);
+int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                  long long ws_bytes, int kid);
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge,
                     int Bt, int T, int H, int D, int GA, int limite, int kid);
+/* no reference counterpart: jt_atencao_back with a caller workspace of jt_atencao_back_ws_bytes(Bt, T, H, D) bytes
+ * (16-byte aligned); same outputs. At head width 64 on matrix cores (T <= 512) dO, q, k, v are converted once per
+ * (sequence, head) into the workspace and each 16-row tile's partner tiles are split over four waves; otherwise
+ * it runs jt_atencao_back. */
+long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D);
+int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
+                       int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@
 #include "jt_gemm.hip"
 #include "jt_atencao.hip"
 #include "jt_atencao_hd.hip"
+#include "jt_atencao_ws.hip"
 
 __device__ Erro g_erro;
 __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long long valor, long long aux) {
@@ -370,6 +371,30 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
 #undef L
     return fim();
 }
+// No reference counterpart: jt_atencao with a caller workspace of jt_atencao_ws_bytes(Bt, T, H, D) bytes
+// (16-byte aligned). Same outputs as jt_atencao. At head width 64 on matrix cores (T % 64 == 0, T <= 512) it
+// converts k and v once per (sequence, head) into the workspace and splits each 16-row query tile's keys over
+// four waves; otherwise it runs jt_atencao and leaves the workspace untouched.
+long long jt_atencao_ws_bytes(int Bt, int T, int H, int D) {
+    if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
+    return (long long)atw::bytes_fwd((long long)Bt * H, T);
+}
+int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                  long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, kid);
+    if (!alinhados(qm, qE, Oacc, Oe, P, ws) || !ws || ws_bytes < jt_atencao_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+        return (int)hipErrorInvalidValue;
+    const long long BH = (long long)Bt * H;
+    const atw::Ws w = atw::parte(ws, BH, T);
+    k_atf_prep<<<(unsigned)(BH * (T / 64)), 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, T, H, D, g_blk, GA);
+    const unsigned g = (unsigned)(BH * (T / 16));
+#define L(NTW) k_atf<NTW><<<g, 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, \
+                                                g_blk, GA, kid)
+    if (T <= 256) L(4); else L(8);
+#undef L
+    return fim();
+}
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
     if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
@@ -434,4 +459,37 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     return fim();
 }
 
+// No reference counterpart: jt_atencao_back with a caller workspace of jt_atencao_back_ws_bytes(Bt, T, H, D)
+// bytes (16-byte aligned). Same outputs as jt_atencao_back. At head width 64 on matrix cores (T % 64 == 0,
+// T <= 512) it converts dO, q, k, v once per (sequence, head) into the workspace and splits each 16-row tile's
+// partner tiles over four waves (4 launches, 5 for the exact variant); otherwise it runs jt_atencao_back.
+long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D) {
+    if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
+    return (long long)atw::bytes_back((long long)Bt * H, T);
+}
+int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
+                       int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
+    if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge, ws) || !ws || ws_bytes < jt_atencao_back_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+        return (int)hipErrorInvalidValue;
+    const long long BH = (long long)Bt * H;
+    const atw::WsB w = atw::parte_b(ws, BH, T);
+    const int dsb = 12 - std::max(0, ilog2(T) - 7);
+    const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
+    const uint8_t* P8 = (const uint8_t*)P;
+    const unsigned gp = (unsigned)(BH * (T / 64)), gt = (unsigned)(BH * (T / 16));
+#define FASES(NTW, LM)                                                                                                    \
+    {                                                                                                                     \
+        k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                              \
+        if (!LM) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                                          \
+        k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \
+        k_atbq<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, (int*)Gacc, (int16_t*)Ge, T, H, D, dsb, kid);                     \
+        k_atbkv<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, (int*)Gacc, (int16_t*)Ge, T, H, D, dsb, kid);                    \
+    }
+    if (T <= 256) { if (limite) FASES(4, 1) else FASES(4, 0) }
+    else { if (limite) FASES(8, 1) else FASES(8, 0) }
+#undef FASES
+    return fim();
+}
 }  // extern "C"

@@ -54,7 +54,13 @@ __device__ __forceinline__ int emx_cabeca(const int8_t* E, int ld, int col0, int
     constexpr int DL = HD / 4;
     const int r = threadIdx.x & 3, nbl = ld / blk, cb = (col0 + DL * r) / blk;
     int m = SEM_TOPO;
-    for (int t = threadIdx.x >> 2; t < T; t += blockDim.x >> 2) m = max(m, (int)E[(size_t)(b0 + t) * nbl + cb]);
+    const int passo = blockDim.x >> 2;
+    int t = threadIdx.x >> 2;
+    for (; t + 3 * passo < T; t += 4 * passo) {                      // four independent loads per round
+        const int8_t* e = E + (size_t)(b0 + t) * nbl + cb;
+        m = max(max(m, (int)e[0]), max((int)e[(size_t)passo * nbl], max((int)e[(size_t)2 * passo * nbl], (int)e[(size_t)3 * passo * nbl])));
+    }
+    for (; t < T; t += passo) m = max(m, (int)E[(size_t)(b0 + t) * nbl + cb]);
     return wg_max(m, red);
 }
 

@@ -1,0 +1,680 @@
+// Causal ALiBi attention at head width 64 with a caller-provided workspace (the arithmetic of k_atencao_mf: the
+// declared head-width-64 generalization of ops.py:186-258).
+//
+// Forward in two launches:
+//   (1) k_atf_prep, one workgroup per (sequence, head, 64 tokens): the head-wide exponent maxima of q, k, v (one
+//       pass, one reduction), k as m8 << L fragments (int8 [T][64] + L [T][2]) and v aligned as f16, transposed
+//       ([64][T]), into the workspace -- converted once instead of once per query block;
+//   (2) k_atf, one workgroup of 4 waves per (sequence, head, 16 query rows): wave w takes the key tiles
+//       t = w, w + 4, ... up to the diagonal. The row maxima and row sums combine across the waves through LDS
+//       (integer max and sum: exact in any order); each wave multiplies its P tiles by V on f16 MFMA, and the
+//       four partial outputs are added in fp32: every partial and their sum are integers below 2^20 (P <= 255,
+//       |v| <= 2032, a row of P sums to at most 256 + T/2), so the sum is exact and equals the one-pass result.
+// 4096 waves at config 4 (4 per SIMD) instead of 1024, each with a quarter of the serial score/softmax chain.
+#include "jt_comum.h"
+
+namespace atw {
+// workspace parts, each 256-byte aligned: km8 int8 [BH][T][64]; kl int8 [BH][T][2]; vt f16 [BH][64][T];
+// mx int [BH][4] (emq, emk, emv)
+struct Ws {
+    int8_t *km8, *kl;
+    _Float16* vt;
+    int* mx;
+};
+inline size_t alinha256(size_t n) { return (n + 255) & ~(size_t)255; }
+inline size_t bytes_fwd(long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    return alinha256(n * 64) + alinha256(n * 2) + alinha256(n * 64 * 2) + alinha256((size_t)BH * 16);
+}
+inline Ws parte(void* base, long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    char* p = (char*)base;
+    Ws w;
+    w.km8 = (int8_t*)p; p += alinha256(n * 64);
+    w.kl = (int8_t*)p; p += alinha256(n * 2);
+    w.vt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    w.mx = (int*)p;
+    return w;
+}
+}
+
+// Largest block exponents of three head slices (columns c0 + [0, 64) of E, one per slice) over the T tokens of
+// sequence b0 / T: one pass and one workgroup reduction (256 threads).
+__device__ __forceinline__ void emx3(const int8_t* E, int ld, int ca, int cb, int cc, int blk, int b0, int T, int (&red)[3][4], int& a, int& b,
+                                     int& c) {
+    const int r = threadIdx.x & 3, nbl = ld / blk, ba = (ca + 16 * r) / blk, bb = (cb + 16 * r) / blk, bc = (cc + 16 * r) / blk;
+    int ma = SEM_TOPO, mb = SEM_TOPO, mc = SEM_TOPO;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {                                    // T <= 512: all loads issued together
+        const int t = (threadIdx.x >> 2) + 64 * k;
+        if (t < T) {
+            const int8_t* e = E + (size_t)(b0 + t) * nbl;
+            ma = max(ma, (int)e[ba]); mb = max(mb, (int)e[bb]); mc = max(mc, (int)e[bc]);
+        }
+    }
+    ma = g_max<64>(ma); mb = g_max<64>(mb); mc = g_max<64>(mc);
+    if ((threadIdx.x & 63) == 0) { red[0][threadIdx.x >> 6] = ma; red[1][threadIdx.x >> 6] = mb; red[2][threadIdx.x >> 6] = mc; }
+    __syncthreads();
+    a = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+    b = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+    c = max(max(red[2][0], red[2][1]), max(red[2][2], red[2][3]));
+}
+
+__global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, int T, int H, int D,
+                                                  int blk, int GA) {
+    constexpr int HD = 64;
+    __shared__ int red[3][4];
+    const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, nbl = ld / blk, tid = threadIdx.x;
+    int emq, emk, emv;
+    emx3(qE, ld, h * HD, D + h * HD, 2 * D + h * HD, blk, b0, T, red, emq, emk, emv);
+    if (part == 0 && tid == 0) { w.mx[bh * 4] = emq; w.mx[bh * 4 + 1] = emk; w.mx[bh * 4 + 2] = emv; }
+    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t
+    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
+    const size_t base = (size_t)(b0 + t) * ld, tt = (size_t)bh * T + t;
+    {
+        const int col = D + h * HD + 16 * c4;
+        int v[16];
+        le_i8(qm + base + col, v);
+        const int sh = emk - (int)qE[(size_t)(b0 + t) * nbl + col / blk];
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
+        grava_i8(w.km8 + tt * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) w.kl[tt * 2 + half] = (int8_t)L;
+    }
+    {
+        const int col = 2 * D + h * HD + 16 * c4;
+        int v[16];
+        le_i8(qm + base + col, v);
+        const int sv = emv - (int)qE[(size_t)(b0 + t) * nbl + col / blk];
+#pragma unroll
+        for (int k = 0; k < 16; k++) w.vt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), sv);
+    }
+}
+
+// NTW = key tiles a wave can own (T / 64)
+template <int NTW>
+__global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, int* __restrict__ Oacc,
+                                             int16_t* __restrict__ Oe, uint8_t* __restrict__ P, int T, int H, int D, int blk, int GA, int kid) {
+    constexpr int HD = 64, LP = 16 * (NTW + 1);                     // LDS row length of a wave's P (one pad tile)
+    __shared__ int sred[4][16];
+    __shared__ __align__(16) _Float16 pw[4][16][LP];
+    __shared__ float so[4][16][64];
+    // workgroups in decreasing work across all heads (the query tile qt costs qt + 1 key tiles): the ones resident
+    // together on a CU then mix long and short rows
+    const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, qt = nqt - 1 - (int)(blockIdx.x / BH);
+    const int b = bh / H, h = bh % H, b0 = b * T;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4;
+    const int eq = w.mx[bh * 4] - GA, ek = w.mx[bh * 4 + 1] - GA, ev = w.mx[bh * 4 + 2] - GA;
+    const int su = -(eq + ek - 3 + 8), incl = 8 - (8 * h) / H;     // log2(64) / 2 = 3
+    const size_t hb = (size_t)bh * T;
+    const int ia = 16 * qt + lr, i0 = 16 * qt + 4 * lg;              // A-fragment row; this lane's 4 score rows
+    const int nv = qt >= wv ? (qt - wv) / 4 + 1 : 0;                 // this wave's key tiles wv + 4 n, n < nv
+    // V fragments of the PV pairs, loaded first (they depend on nothing): pair m, k-index kk = 8 lg + e is key
+    // 16 (wv + 4 (2m + kk / 16)) + kk % 16; a pad tile (P = 0 there) reads the wave's first tile of V
+    constexpr int NPAR = (NTW + 1) / 2;
+    h8_t vb[NPAR][4];
+#pragma unroll
+    for (int m = 0; m < NPAR; m++) {
+        if (2 * m >= nv) continue;
+        int tv = wv + 4 * (2 * m + (lg >> 1));
+        if (tv >= nqt) tv = wv;
+        const int j = 16 * tv + 8 * (lg & 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) vb[m][dt] = *reinterpret_cast<const h8_t*>(w.vt + ((size_t)bh * 64 + 16 * dt + lr) * T + j);
+    }
+    // K fragments of this wave's key tiles, loaded at entry as well
+    long kb[NTW][2];
+    int lk[NTW][2];
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const size_t j = hb + 16 * (wv + 4 * n) + lr;
+        kb[n][0] = *reinterpret_cast<const long*>(w.km8 + j * 64 + 8 * lg);
+        kb[n][1] = *reinterpret_cast<const long*>(w.km8 + j * 64 + 32 + 8 * lg);
+        lk[n][0] = w.kl[j * 2];
+        lk[n][1] = w.kl[j * 2 + 1];
+    }
+    // q fragments of the tile's 16 rows, converted here: A row lr = query ia, dimensions 32 c + 8 lg .. + 7
+    __shared__ int qL[16][2];
+    long qa[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        int L;
+        qa[c] = m8L_frag(qm, qE, 3 * D, h * HD, blk, b0 + ia, eq + GA, GA, c, lg, L);
+        if (lg == 0) qL[lr][c] = L;
+    }
+    __syncthreads();
+    int lq[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lq[v][0] = qL[4 * lg + v][0]; lq[v][1] = qL[4 * lg + v][1]; }
+    const long long idx = (long long)(b0 + i0) * D + h * HD;
+    int uu[NTW][4], mx[4] = {U_MIN, U_MIN, U_MIN, U_MIN};
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;                                       // guarded, not break: uu stays in registers
+        const int j = 16 * (wv + 4 * n) + lr;
+        const int lk0 = lk[n][0], lk1 = lk[n][1];
+        const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[0], kb[n][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+        const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[1], kb[n][1], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int i = i0 + v;
+            const int s = shl(p0[v], lq[v][0] + lk0) + shl(p1[v], lq[v][1] + lk1);
+            const int r = su >= 0 ? rnd_d(s, su) : rnd(s, su, kid, idx);
+            const int u = j <= i ? r - ((i - j) << incl) : U_MIN;
+            uu[n][v] = u;
+            mx[v] = max(mx[v], u);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) mx[v] = g_max<16>(mx[v]);
+    if (lr == 0)
+#pragma unroll
+        for (int v = 0; v < 4; v++) sred[wv][4 * lg + v] = mx[v];
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; v++) mx[v] = max(max(sred[0][4 * lg + v], sred[1][4 * lg + v]), max(sred[2][4 * lg + v], sred[3][4 * lg + v]));
+    __syncthreads();                                                 // sred is reused for the sums
+    int soma[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int ex = uu[n][v] == U_MIN ? 0 : exp_dif(mx[v], uu[n][v]) >> 3;
+            uu[n][v] = ex;
+            soma[v] += ex;
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) soma[v] = g_sum<16>(soma[v]);
+    if (lr == 0)
+#pragma unroll
+        for (int v = 0; v < 4; v++) sred[wv][4 * lg + v] = soma[v];
+    __syncthreads();
+    int inv[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int s = sred[0][4 * lg + v] + sred[1][4 * lg + v] + sred[2][4 * lg + v] + sred[3][4 * lg + v];
+        if (s <= 0) { if (lr == 0 && wv == 0) reporta(E_DIV, kid, idx + (long long)v * D, s, mx[v]); s = 1; }
+        inv[v] = (1 << 28) / s;
+    }
+    uint8_t* Pb = P + (size_t)bh * T * T;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const int j = 16 * (wv + 4 * n) + lr;
+        unsigned pk = 0;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int p = min((uu[n][v] * inv[v] + (1 << 19)) >> 20, 255);
+            pk |= (unsigned)p << (8 * v);
+            pw[wv][4 * lg + v][16 * n + lr] = (_Float16)p;
+        }
+        *reinterpret_cast<unsigned*>(Pb + (size_t)j * T + i0) = pk;
+    }
+    for (int t = wv + 4 * nv; t < nqt; t += 4) *reinterpret_cast<unsigned*>(Pb + (size_t)(16 * t + lr) * T + i0) = 0u;   // above the diagonal
+    if (nv & 1)
+#pragma unroll
+        for (int v = 0; v < 4; v++) pw[wv][4 * lg + v][16 * nv + lr] = (_Float16)0;
+    __syncthreads();
+    // partial O = P V over this wave's tiles, in pairs
+    f4_t o[4] = {};
+#pragma unroll
+    for (int m = 0; m < NPAR; m++) {
+        if (2 * m >= nv) continue;
+        const h8_t a = *reinterpret_cast<const h8_t*>(&pw[wv][lr][32 * m + 8 * lg]);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vb[m][dt], o[dt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) so[wv][4 * lg + v][16 * dt + lr] = o[dt][v];
+    __syncthreads();
+    // wave wv writes the 16 dimensions 16 wv .. 16 wv + 15
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int r = 4 * lg + v, c = 16 * wv + lr;
+        const int ov = (int)(so[0][r][c] + so[1][r][c] + so[2][r][c] + so[3][r][c]);
+        const size_t x = (size_t)(b0 + i0 + v) * D + h * HD + c;
+        if (ov >= LIM || ov <= -LIM) reporta(E_ACUM, kid, x, ov, -3);
+        Oacc[x] = ov;
+        Oe[x] = (int16_t)(ev - 8);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- backward
+// The arithmetic of k_atb_mf_linhas / _gq / _gkv / k_atb_exp, in launches that read converted operands from the
+// workspace and split each 16-row tile's partner tiles over four waves:
+//   (0) k_atb_prep: head maxima of dO, q, k, v; dO, v as m8 << L fragments; k, q, dO aligned as f16 [64][T];
+//       for the bound variant (LIMITE), per 64 tokens max |dO| and max ||v||_1 (ops.py:231-235);
+//   (1) k_atb1 (exact variant): per query tile, max |gP| over its causal pairs;
+//   (2) k_atb2: s_i = rnd(sum_j P_ij rnd(gP_ij, sh), 8) per row, and per query tile the maxima that set dS's
+//       shrink (max |P (gP' - s)|, or max P, max |gP'|, max |s| for LIMITE);
+//   (3a) k_atbq: gq_i = sum_j dS_ij k_j and the exponents of the q columns;
+//   (3b) k_atbkv: gk_j = sum_i dS_ij q_i, gv_j = sum_i P_ij dO_i and the exponents of the k and v columns.
+// Partial maxima sit in per-tile slots (no atomics, no clearing); the consumers reduce over the slots. The four
+// waves' partial sums are exact integers and are added in int64 through LDS.
+namespace atw {
+constexpr int SLOTS = 32;            // per head and kind: T / 16 <= 32 query tiles
+struct WsB {
+    int8_t *gm8, *gL, *vm8, *vL;     // dO, v: m8 [BH][T][64], L [BH][T][2]
+    _Float16 *kt, *qt, *gt;          // k, q, dO aligned: f16 [BH][64][T]
+    int* sl;                         // s_i [BH][T]
+    int* mx;                         // [BH][4]: ego, eq, ek, ev (head maxima - GA)
+    int* p1a;                        // [BH][SLOTS]: max |gP| per query tile, or max |dO| per 64 tokens (LIMITE)
+    int* p1b;                        // [BH][SLOTS]: max ||v||_1 per 64 tokens (LIMITE)
+    int *p2a, *p2b, *p2c;            // [BH][SLOTS]: max |P (gP' - s)|, or max P, max |gP'|, max |s| (LIMITE)
+};
+inline size_t bytes_back(long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    return 2 * (alinha256(n * 64) + alinha256(n * 2)) + 3 * alinha256(n * 64 * 2) + alinha256(n * 4) + alinha256((size_t)BH * 16) +
+           5 * alinha256((size_t)BH * SLOTS * 4);
+}
+inline WsB parte_b(void* base, long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    char* p = (char*)base;
+    WsB w;
+    w.gm8 = (int8_t*)p; p += alinha256(n * 64);
+    w.gL = (int8_t*)p; p += alinha256(n * 2);
+    w.vm8 = (int8_t*)p; p += alinha256(n * 64);
+    w.vL = (int8_t*)p; p += alinha256(n * 2);
+    w.kt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    w.qt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    w.gt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    w.sl = (int*)p; p += alinha256(n * 4);
+    w.mx = (int*)p; p += alinha256((size_t)BH * 16);
+    w.p1a = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
+    w.p1b = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
+    w.p2a = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
+    w.p2b = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
+    w.p2c = (int*)p;
+    return w;
+}
+// maximum over n slots of head bh (all lanes read the same addresses)
+__device__ __forceinline__ int max_slots(const int* s, int bh, int n) {
+    int m = 0;
+    for (int i = 0; i < n; i++) m = max(m, s[bh * SLOTS + i]);
+    return m;
+}
+template <int LIMITE>
+__device__ __forceinline__ int sh_gp_ws(const WsB& w, int bh, int T) {
+    if (LIMITE) return max(bitlen(max_slots(w.p1a, bh, T / 64) * max_slots(w.p1b, bh, T / 64)) - 15, 0);
+    return max(bitlen(max_slots(w.p1a, bh, T / 16)) - 15, 0);
+}
+template <int LIMITE>
+__device__ __forceinline__ int sh_ds_ws(const WsB& w, int bh, int T, int dsb) {
+    const int n = T / 16;
+    if (LIMITE) return max(bitlen(max_slots(w.p2a, bh, n) * (max_slots(w.p2b, bh, n) + max_slots(w.p2c, bh, n))) - dsb, 0);
+    return max(bitlen(max_slots(w.p2a, bh, n)) - dsb, 0);
+}
+}
+
+// workgroup maximum of a non-negative value (256 threads); red[4]
+__device__ __forceinline__ int wg_max4(int v, int (&red)[4]) {
+    v = g_max<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const int r = max(max(red[0], red[1]), max(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+template <int LIMITE>
+__global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
+                                                  const int8_t* __restrict__ qE, atw::WsB w, int T, int H, int D, int blk, int GA) {
+    constexpr int HD = 64;
+    __shared__ int red[3][4];
+    __shared__ int red1[4];
+    const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, tid = threadIdx.x;
+    int emq, emk, emv;
+    emx3(qE, ld, h * HD, D + h * HD, 2 * D + h * HD, blk, b0, T, red, emq, emk, emv);
+    int emg;
+    {
+        const int r = tid & 3, nbl = D / blk, cb = (h * HD + 16 * r) / blk;
+        int m = SEM_TOPO;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int t = (tid >> 2) + 64 * k;
+            if (t < T) m = max(m, (int)goE[(size_t)(b0 + t) * nbl + cb]);
+        }
+        emg = wg_max4(m - SEM_TOPO, red1) + SEM_TOPO;                // wg_max4 takes non-negative values
+    }
+    if (part == 0 && tid == 0) { w.mx[bh * 4] = emg - GA; w.mx[bh * 4 + 1] = emq - GA; w.mx[bh * 4 + 2] = emk - GA; w.mx[bh * 4 + 3] = emv - GA; }
+    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
+    const size_t tt = (size_t)bh * T + t;
+    int amax = 0, v1 = 0;
+    {   // dO: m8 << L fragments and aligned f16
+        const int col = h * HD + 16 * c4;
+        int v[16];
+        le_i8(gom + (size_t)(b0 + t) * D + col, v);
+        const int s = emg - (int)goE[(size_t)(b0 + t) * (D / blk) + col / blk];
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
+            const int al = rnd_d(shl(v[k], GA), s);
+            amax = max(amax, abs(al));
+            w.gt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)al;
+        }
+        grava_i8(w.gm8 + tt * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
+    }
+    {   // v: m8 << L fragments (and ||v||_1 for LIMITE)
+        const int col = 2 * D + h * HD + 16 * c4;
+        int v[16];
+        le_i8(qm + (size_t)(b0 + t) * ld + col, v);
+        const int s = emv - (int)qE[(size_t)(b0 + t) * (ld / blk) + col / blk];
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
+            if (LIMITE) v1 += abs(rnd_d(shl(v[k], GA), s));
+        }
+        grava_i8(w.vm8 + tt * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) w.vL[tt * 2 + half] = (int8_t)L;
+    }
+#pragma unroll
+    for (int x = 0; x < 2; x++) {   // q (x = 0), k (x = 1): aligned f16, transposed
+        const int col = x * D + h * HD + 16 * c4;
+        int v[16];
+        le_i8(qm + (size_t)(b0 + t) * ld + col, v);
+        const int s = (x ? emk : emq) - (int)qE[(size_t)(b0 + t) * (ld / blk) + col / blk];
+        _Float16* dst = x ? w.kt : w.qt;
+#pragma unroll
+        for (int k = 0; k < 16; k++) dst[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), s);
+    }
+    if (LIMITE) {
+        v1 = quad_soma(v1);
+        const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
+        if (tid == 0) { w.p1a[bh * atw::SLOTS + part] = a; w.p1b[bh * atw::SLOTS + part] = c; }
+    }
+}
+
+// gP tile of query rows i0 .. i0 + 3 (this lane) x key j = 16 t + lr from the workspace fragments
+struct FragQ {                                      // dO fragments of a query tile (A operand) and their L
+    long ga[2];
+    int lx[4][2];
+};
+__device__ __forceinline__ FragQ frag_q(const atw::WsB& w, size_t hb, int qt, int lr, int lg) {
+    FragQ f;
+    const size_t ia = hb + 16 * qt + lr, i0 = hb + 16 * qt + 4 * lg;
+    f.ga[0] = *reinterpret_cast<const long*>(w.gm8 + ia * 64 + 8 * lg);
+    f.ga[1] = *reinterpret_cast<const long*>(w.gm8 + ia * 64 + 32 + 8 * lg);
+#pragma unroll
+    for (int v = 0; v < 4; v++) { f.lx[v][0] = w.gL[(i0 + v) * 2]; f.lx[v][1] = w.gL[(i0 + v) * 2 + 1]; }
+    return f;
+}
+__device__ __forceinline__ void gp_tile(const atw::WsB& w, size_t hb, const FragQ& f, int t, int lr, int lg, int (&o)[4]) {
+    const size_t j = hb + 16 * t + lr;
+    tile_xyt(f.ga[0], f.ga[1], *reinterpret_cast<const long*>(w.vm8 + j * 64 + 8 * lg), *reinterpret_cast<const long*>(w.vm8 + j * 64 + 32 + 8 * lg),
+             f.lx, w.vL[j * 2], w.vL[j * 2 + 1], o);
+}
+// query tile of this workgroup, in decreasing work across all heads (tile qt pairs with qt + 1 key tiles)
+#define ATB_TILE_Q                                                                                                     \
+    const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, qt = nqt - 1 - (int)(blockIdx.x / BH);          \
+    const int b = bh / H, h = bh % H, b0 = b * T;                                                                      \
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4; \
+    const size_t hb = (size_t)bh * T;                                                                                  \
+    const int i0 = 16 * qt + 4 * lg, nv = qt >= wv ? (qt - wv) / 4 + 1 : 0;
+
+template <int NTW>
+__global__ void __launch_bounds__(256) k_atb1(atw::WsB w, int T, int H) {
+    __shared__ int red[4];
+    ATB_TILE_Q
+    (void)b0;
+    const FragQ f = frag_q(w, hb, qt, lr, lg);
+    int mg = 0;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const int t = wv + 4 * n, j = 16 * t + lr;
+        int o[4];
+        gp_tile(w, hb, f, t, lr, lg, o);
+#pragma unroll
+        for (int v = 0; v < 4; v++) if (j <= i0 + v) mg = max(mg, abs(o[v]));
+    }
+    mg = wg_max4(mg, red);
+    if (tid == 0) w.p1a[bh * atw::SLOTS + qt] = mg;
+}
+
+template <int NTW, int LIMITE>
+__global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restrict__ P, int T, int H, int D, int kid) {
+    __shared__ int red[4];
+    __shared__ int sred[4][16];
+    ATB_TILE_Q
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T);
+    const FragQ f = frag_q(w, hb, qt, lr, lg);
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+    int x[NTW][4];
+    unsigned pr[NTW];
+    int s[4] = {0, 0, 0, 0}, pm = 0, gm = 0;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const int t = wv + 4 * n, j = 16 * t + lr;
+        int o[4];
+        gp_tile(w, hb, f, t, lr, lg, o);
+        pr[n] = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);     // P_ij, rows i0 .. i0 + 3
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int xv = j <= i0 + v ? rnd_d(o[v], sh) : 0;
+            const int p = (pr[n] >> (8 * v)) & 255;
+            x[n][v] = xv;
+            s[v] += p * xv;
+            if (LIMITE) { pm = max(pm, p); gm = max(gm, abs(xv)); }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) s[v] = g_sum<16>(s[v]);
+    if (lr == 0)
+#pragma unroll
+        for (int v = 0; v < 4; v++) sred[wv][4 * lg + v] = s[v];
+    __syncthreads();
+    const int ld = 3 * D;
+    int sl[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int tot = sred[0][4 * lg + v] + sred[1][4 * lg + v] + sred[2][4 * lg + v] + sred[3][4 * lg + v];
+        if ((tot >= LIM || tot <= -LIM) && lr == 0 && wv == 0) reporta(E_ACUM, kid, (long long)(b0 + i0 + v) * ld + h * 64, tot, -4);
+        sl[v] = rnd_d(tot, 8);
+        if (lr == 0 && wv == 0) w.sl[hb + i0 + v] = sl[v];
+    }
+    if (LIMITE) {
+        const int a = wg_max4(pm, red), c = wg_max4(gm, red);
+        const int d = wg_max4(max(max(abs(sl[0]), abs(sl[1])), max(abs(sl[2]), abs(sl[3]))), red);
+        if (tid == 0) { w.p2a[bh * atw::SLOTS + qt] = a; w.p2b[bh * atw::SLOTS + qt] = c; w.p2c[bh * atw::SLOTS + qt] = d; }
+    } else {
+        int md = 0;
+#pragma unroll
+        for (int n = 0; n < NTW; n++) {
+            if (n >= nv) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) md = max(md, abs((int)((pr[n] >> (8 * v)) & 255) * (x[n][v] - sl[v])));
+        }
+        md = wg_max4(md, red);
+        if (tid == 0) w.p2a[bh * atw::SLOTS + qt] = md;
+    }
+}
+
+// sums the four waves' int64 partials parc[w][16][64] (this lane: rows 4 lg + v, column 16 dt + lr of wave wv's
+// registers) -- written by every wave, then wave wv adds column group 16 wv .. 16 wv + 15 -- into out[v]
+__device__ __forceinline__ void soma_ondas(long long (&parc)[4][16][64], const long long (&mine)[4][4], int wv, int lr, int lg, long long (&out)[4]) {
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) parc[wv][4 * lg + v][16 * dt + lr] = mine[dt][v];
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int r = 4 * lg + v, c = 16 * wv + lr;
+        out[v] = parc[0][r][c] + parc[1][r][c] + parc[2][r][c] + parc[3][r][c];
+    }
+    __syncthreads();
+}
+
+template <int NTW, int LIMITE>
+__global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge, int T,
+                                              int H, int D, int dsb, int kid) {
+    constexpr int LP = 16 * (NTW + 1);
+    __shared__ __align__(16) short dw[4][16][LP];
+    __shared__ long long parc[4][16][64];
+    ATB_TILE_Q
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
+    const int eds = ego + ev + sh - 9 + sh2;
+    const FragQ f = frag_q(w, hb, qt, lr, lg);
+    int sl[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) sl[v] = w.sl[hb + i0 + v];
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const int t = wv + 4 * n, j = 16 * t + lr;
+        int o[4];
+        gp_tile(w, hb, f, t, lr, lg, o);
+        const unsigned pr = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int p = (pr >> (8 * v)) & 255;
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? rnd_d(p * (rnd_d(o[v], sh) - sl[v]), sh2) : 0);
+        }
+    }
+    if (nv & 1)
+#pragma unroll
+        for (int v = 0; v < 4; v++) dw[wv][4 * lg + v][16 * nv + lr] = 0;
+    __syncthreads();
+    // gq partial = dS K over this wave's key tiles, in pairs; dS = a 256 + b 16 + c (see the MFMA backward above)
+    f4_t acc[4][3] = {};
+#pragma unroll
+    for (int m = 0; m < (NTW + 1) / 2; m++) {
+        if (2 * m >= nv) continue;
+        h8_t pa, pb, pc;
+        pedacos_ds(*reinterpret_cast<const s8_t*>(&dw[wv][lr][32 * m + 8 * lg]), pa, pb, pc);
+        int tk = wv + 4 * (2 * m + (lg >> 1));
+        if (tk >= nqt) tk = wv;                                      // pad tile: dS = 0 there
+        const int j = 16 * tk + 8 * (lg & 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const h8_t kv = *reinterpret_cast<const h8_t*>(w.kt + ((size_t)bh * 64 + 16 * dt + lr) * T + j);
+            acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, kv, acc[dt][0], 0, 0, 0);
+            acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, kv, acc[dt][1], 0, 0, 0);
+            acc[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, kv, acc[dt][2], 0, 0, 0);
+        }
+    }
+    long long mine[4][4], gq[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
+    soma_ondas(parc, mine, wv, lr, lg, gq);
+    const int ld = 3 * D;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const size_t o = (size_t)(b0 + i0 + v) * ld + h * 64 + 16 * wv + lr;
+        if (gq[v] >= LIM || gq[v] <= -LIM) reporta(E_ACUM, kid, o, gq[v], -5);
+        Gacc[o] = (int)gq[v];
+        Ge[o] = (int16_t)(eds + ek);
+    }
+}
+
+template <int NTW, int LIMITE>
+__global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
+                                               int T, int H, int D, int dsb, int kid) {
+    constexpr int LP = 16 * (NTW + 1);
+    __shared__ __align__(16) short dw[4][16][LP];
+    __shared__ __align__(16) uint8_t pw[4][16][LP];
+    __shared__ long long parc[4][16][64];
+    // key tile kt pairs with the query tiles kt .. nqt - 1: decreasing work is increasing kt
+    const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, kt = (int)(blockIdx.x / BH);
+    const int b = bh / H, h = bh % H, b0 = b * T;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4;
+    const size_t hb = (size_t)bh * T;
+    const int nv = (nqt - kt - wv + 3) / 4;                          // this wave's query tiles kt + wv + 4 n, n < nv
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const int ego = w.mx[bh * 4], eq = w.mx[bh * 4 + 1], ev = w.mx[bh * 4 + 3];
+    const int eds = ego + ev + sh - 9 + sh2;
+    // v fragments of the tile's 16 keys as the A operand (rows = keys)
+    const size_t ja = hb + 16 * kt + lr;
+    const int jr = 16 * kt + 4 * lg;                                 // this lane's 4 keys jr .. jr + 3
+    const long va0 = *reinterpret_cast<const long*>(w.vm8 + ja * 64 + 8 * lg), va1 = *reinterpret_cast<const long*>(w.vm8 + ja * 64 + 32 + 8 * lg);
+    int lx[4][2];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { lx[v][0] = w.vL[(hb + jr + v) * 2]; lx[v][1] = w.vL[(hb + jr + v) * 2 + 1]; }
+    const uint8_t* Pb = P + (size_t)bh * T * T;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        const int t = kt + wv + 4 * n, i = 16 * t + lr;               // this lane's query (column)
+        const size_t ig = hb + i;
+        int o[4];
+        tile_xyt(va0, va1, *reinterpret_cast<const long*>(w.gm8 + ig * 64 + 8 * lg), *reinterpret_cast<const long*>(w.gm8 + ig * 64 + 32 + 8 * lg),
+                 lx, w.gL[ig * 2], w.gL[ig * 2 + 1], o);
+        const int sl = w.sl[ig];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int j = jr + v;
+            const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? rnd_d(p * (rnd_d(o[v], sh) - sl), sh2) : 0);
+            pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)p;
+        }
+    }
+    if (nv & 1)
+#pragma unroll
+        for (int v = 0; v < 4; v++) { dw[wv][4 * lg + v][16 * nv + lr] = 0; pw[wv][4 * lg + v][16 * nv + lr] = 0; }
+    __syncthreads();
+    f4_t ak[4][3] = {}, av[4][2] = {};
+#pragma unroll
+    for (int m = 0; m < (NTW + 1) / 2; m++) {
+        if (2 * m >= nv) continue;
+        h8_t pa, pb, pc, ph, pl;
+        pedacos_ds(*reinterpret_cast<const s8_t*>(&dw[wv][lr][32 * m + 8 * lg]), pa, pb, pc);
+        const uint8_t* pp = &pw[wv][lr][32 * m + 8 * lg];
+#pragma unroll
+        for (int k = 0; k < 8; k++) { ph[k] = (_Float16)(pp[k] >> 4); pl[k] = (_Float16)(pp[k] & 15); }
+        int tq = kt + wv + 4 * (2 * m + (lg >> 1));
+        if (tq >= nqt) tq = kt + wv;                                 // pad tile: dS = P = 0 there
+        const int i = 16 * tq + 8 * (lg & 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const size_t r = ((size_t)bh * 64 + 16 * dt + lr) * T + i;
+            const h8_t qv = *reinterpret_cast<const h8_t*>(w.qt + r);
+            const h8_t gv = *reinterpret_cast<const h8_t*>(w.gt + r);
+            ak[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, qv, ak[dt][0], 0, 0, 0);
+            ak[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, qv, ak[dt][1], 0, 0, 0);
+            ak[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, qv, ak[dt][2], 0, 0, 0);
+            av[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, gv, av[dt][0], 0, 0, 0);
+            av[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, gv, av[dt][1], 0, 0, 0);
+        }
+    }
+    long long mine[4][4], gk[4], gvv[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
+    soma_ondas(parc, mine, wv, lr, lg, gk);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+    soma_ondas(parc, mine, wv, lr, lg, gvv);
+    const int ld = 3 * D;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const size_t o = (size_t)(b0 + jr + v) * ld + h * 64 + 16 * wv + lr;
+        if (gk[v] >= LIM || gk[v] <= -LIM) reporta(E_ACUM, kid, o + D, gk[v], -5);
+        if (gvv[v] >= LIM || gvv[v] <= -LIM) reporta(E_ACUM, kid, o + 2 * D, gvv[v], -5);
+        Gacc[o + D] = (int)gk[v];
+        Gacc[o + 2 * D] = (int)gvv[v];
+        Ge[o + D] = (int16_t)(eds + eq);
+        Ge[o + 2 * D] = (int16_t)(ego - 8);
+    }
+}

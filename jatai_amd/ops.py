@@ -21,13 +21,17 @@ BLK = 128
 E_ZERO = -127
 GA = 4
 ATENCAO_LIMITE = False
+# attention through the workspace entry points (jt_atencao_ws): same outputs, faster at head width 64; False runs
+# the reference ABI's jt_atencao
+ATENCAO_WS = True
 AQUI = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(AQUI, "libjatai.so")
 
 FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_back", "jt_momento", "jt_peso", "jt_transpoe",
            "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
-           "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes")
+           "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
+           "jt_atencao_ws", "jt_atencao_back_ws")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -49,6 +53,8 @@ def carrega_lib(caminho=LIB):
         getattr(lib, f).restype = None
     lib.jt_stream.argtypes = [ctypes.c_void_p]
     lib.jt_erro_le.argtypes = [ctypes.c_void_p]
+    lib.jt_atencao_ws_bytes.restype = ctypes.c_longlong
+    lib.jt_atencao_back_ws_bytes.restype = ctypes.c_longlong
     return lib
 
 
@@ -279,7 +285,13 @@ class OpsHip:
         oacc = torch.empty(Bt * T, D, dtype=torch.int32, device=m.device)
         oe = torch.empty(Bt * T, D, dtype=torch.int16, device=m.device)
         P = torch.empty(Bt * H, T, T, dtype=torch.uint8, device=m.device)
-        self._lanca("atencao", "jt_atencao", (m, E, oacc, oe, P, Bt, T, H, D, GA), dict(qkv=m, qkvE=E), (Bt * T, D))
+        if ATENCAO_WS:
+            nws = self.lib.jt_atencao_ws_bytes(Bt, T, H, D)
+            ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+            self._lanca("atencao", "jt_atencao_ws", (m, E, oacc, oe, P, Bt, T, H, D, GA, ws, nws), dict(qkv=m, qkvE=E), (Bt * T, D),
+                        longos=(11,))
+        else:
+            self._lanca("atencao", "jt_atencao", (m, E, oacc, oe, P, Bt, T, H, D, GA), dict(qkv=m, qkvE=E), (Bt * T, D))
         return (oacc, oe), P
 
     def _formas_atencao(self, op, m, Bt, T, H, D):
@@ -299,8 +311,14 @@ class OpsHip:
                        f"atencao_back: P com forma {tuple(P.shape)}, esperado {(Bt * H, T, T)} uint8")
         acc = torch.empty(Bt * T, 3 * D, dtype=torch.int32, device=m.device)
         e = torch.empty(Bt * T, 3 * D, dtype=torch.int16, device=m.device)
-        self._lanca("atencao_back", "jt_atencao_back", (gm, gE, m, E, P, acc, e, Bt, T, H, D, GA, int(ATENCAO_LIMITE)),
-                    dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D))
+        if ATENCAO_WS:
+            nws = self.lib.jt_atencao_back_ws_bytes(Bt, T, H, D)
+            ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+            self._lanca("atencao_back", "jt_atencao_back_ws", (gm, gE, m, E, P, acc, e, Bt, T, H, D, GA, int(ATENCAO_LIMITE), ws, nws),
+                        dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D), longos=(14,))
+        else:
+            self._lanca("atencao_back", "jt_atencao_back", (gm, gE, m, E, P, acc, e, Bt, T, H, D, GA, int(ATENCAO_LIMITE)),
+                        dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D))
         return acc, e
 
     def softmax_ce(self, L, alvo):

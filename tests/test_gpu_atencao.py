@@ -16,6 +16,16 @@ def _cmp(a, b, nome):
     assert d is None, f"{nome}: (flat index, gpu, oracle, count) = {d}"
 
 
+@pytest.fixture(params=[True, False], ids=["ws", "abi"])
+def via_ws(request):
+    """True: OpsHip's default path (jt_atencao_ws, workspace kernels at head width 64); False: the reference
+    ABI's jt_atencao."""
+    from jatai_amd import ops as O
+    old, O.ATENCAO_WS = O.ATENCAO_WS, request.param
+    yield request.param
+    O.ATENCAO_WS = old
+
+
 # exponents e0 +- espalha stay in the range where the int32 sentinels stay silent (e0 + espalha <= 2, as the
 # reference's own spread cases, teste_ops.py:86-87); GPU() reads the device error record after every op
 @pytest.mark.parametrize("blk,Bt,T,H,D,esp,e0,limite", [
@@ -24,8 +34,10 @@ def _cmp(a, b, nome):
     (128, 2, 128, 8, 512, 6, -7, False),
     (32, 1, 256, 4, 256, 12, -10, True),
     (32, 2, 128, 16, 512, 2, -7, False),
-], ids=["cfg4", "cfg4-limite-espalhado", "blk128-T128", "H4-espalhado-limite", "hd32"])
-def test_atencao_hd_vs_oraculo(blk, Bt, T, H, D, esp, e0, limite):
+    (32, 1, 512, 4, 256, 3, -7, False),
+    (32, 1, 192, 4, 256, 3, -7, False),
+], ids=["cfg4", "cfg4-limite-espalhado", "blk128-T128", "H4-espalhado-limite", "hd32", "T512", "T192"])
+def test_atencao_hd_vs_oraculo(blk, Bt, T, H, D, esp, e0, limite, via_ws):
     M = Bt * T
     seed = R.substream(555, f"{blk} {Bt} {T} {H} {D} {esp} {limite}")
     qn = R.bloco(R.substream(seed, "qkv"), M, 3 * D, blk, espalha=esp, e0=e0, zera=0.05)
