@@ -48,6 +48,12 @@ int jt_gemm_divisoes(int M, int N, int K, int modo);   /* no reference counterpa
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
             int M, int N, int K, int modo, int kid);
 
+/* ---- no reference counterpart: n raw-output GEMMs sharing K, in launches of up to 48. `entradas` is a HOST array of
+ * n entries {const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad;} (device pointers inside); entry i
+ * equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i). For the weight gradients of a step. */
+int jt_gemm_lote(const void* entradas, int n, int kid);
+int jt_entrada_g_bytes(void);          /* sizeof of one entry (64) */
+
 /* ---- element-wise, nblocos = elements / BLK (jatai_cuda.cu:1128-1154, 1074-1086) */
 int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid);
 int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);

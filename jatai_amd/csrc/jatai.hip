@@ -144,6 +144,45 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
     return jt_gemm_f(A, EA, B, EB, Cm, CE, C32, Ce, nullptr, nullptr, nullptr, nullptr, M, N, K, modo, kid);
 }
 
+// No reference counterpart: n raw-output GEMMs sharing K in launches of up to 48 (host array of EntradaG, device
+// pointers inside); entry i equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i).
+struct EntradaG { const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad; };
+int jt_gemm_lote(const void* entradas, int n, int kid) {
+    using namespace gemm;
+    if (n < 0 || (n > 0 && !entradas)) return (int)hipErrorInvalidValue;
+    const EntradaG* e = (const EntradaG*)entradas;
+    for (int base = 0; base < n; base += LOTE_G) {
+        LoteG L;
+        L.n = std::min(LOTE_G, n - base);
+        L.K = e[base].K;
+        long long tot = 0;
+        for (int i = 0; i < L.n; i++) {
+            const EntradaG& x = e[base + i];
+            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || x.K > 4096 || x.K <= 0) return (int)hipErrorInvalidValue;
+            if (!alinhados(x.A, x.EA, x.B, x.EB, x.C32, x.Ce)) return (int)hipErrorInvalidValue;
+            L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
+            L.C32[i] = (int*)x.C32; L.Ce[i] = (int16_t*)x.Ce; L.M[i] = x.M; L.N[i] = x.N; L.ini[i] = (int)tot;
+            tot += (long long)(x.M / BM) * (x.N / BN);
+        }
+        if (tot > 0x7fffffff) return (int)hipErrorInvalidValue;
+        L.ini[L.n] = (int)tot;
+        if (tot == 0) continue;
+        // K-splits for the whole group, by the rule of jt_gemm_f with the group's tile count
+        const int nb = L.K / g_blk, ksmax = g_blk == 32 ? 4 : 2;
+        int ks = 1;
+        while (ks < ksmax && tot * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
+        const size_t lds = gemm_lds(nb, ks, g_blk);
+#define L_(BL, S) (lds_max(k_gemm_lote<BL, S>, lds), k_gemm_lote<BL, S><<<(unsigned)tot, 256 * S, lds, g_stream>>>(L, kid + base))
+        if (g_blk == 32) { if (ks == 1) L_(32, 1); else if (ks == 2) L_(32, 2); else L_(32, 4); }
+        else { if (ks == 1) L_(128, 1); else L_(128, 2); }
+#undef L_
+        const int r = fim();
+        if (r) return r;
+    }
+    return 0;
+}
+int jt_entrada_g_bytes() { return (int)sizeof(EntradaG); }
+
 // ---------------------------------------------------------------------------------------------- element-wise
 int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;

@@ -41,12 +41,13 @@ template <int BLK> struct Est {
 };
 }
 
+// The body of one workgroup's tile (rows row0 .., columns col0 ..), shared by k_gemm and the grouped k_gemm_lote.
 template <int BLK, int MODO, int KS>
-__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
-                                                   const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
-                                                   int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
-                                                   const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
-                                                   int N, int K, int kid) {
+__device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
+                                           const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
+                                           int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
+                                           const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
+                                           int K, int kid, const int row0, const int col0) {
     using namespace gemm;
     constexpr int SK = Est<BLK>::SK, LD = Est<BLK>::LD, STAGE = Est<BLK>::STAGE, VB = Est<BLK>::VB;
     extern __shared__ __align__(16) char smem[];
@@ -64,7 +65,6 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
     char* buf = reinterpret_cast<char*>(nb_s) + (((size_t)nb * BN + 15) & ~(size_t)15);
     int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nb], EB rows [BN][nb]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
-    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
     const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
     char* meu = buf + (size_t)g * 3 * STAGE;                        // this group's three stage buffers
@@ -345,6 +345,41 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
             if (lider) CE[oe] = (int8_t)Eg;
         }
     }
+}
+
+template <int BLK, int MODO, int KS>
+__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
+                                                   const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
+                                                   int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
+                                                   const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
+                                                   int N, int K, int kid) {
+    gemm_corpo<BLK, MODO, KS>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * gemm::BM, blockIdx.x * gemm::BN);
+}
+
+// Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels
+// by value in the kernel arguments; GEMM i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over
+// its (M / 32) x (N / 128) tiles. Same tiles, same arithmetic as k_gemm<BLK, 1, KS>.
+constexpr int LOTE_G = 48;
+struct LoteG {
+    const int8_t* A[LOTE_G];
+    const int8_t* EA[LOTE_G];
+    const int8_t* B[LOTE_G];
+    const int8_t* EB[LOTE_G];
+    int* C32[LOTE_G];
+    int16_t* Ce[LOTE_G];
+    int M[LOTE_G], N[LOTE_G], ini[LOTE_G + 1];
+    int n, K;
+};
+
+template <int BLK, int KS>
+__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_lote(const LoteG L, int kid) {
+    const int t = blockIdx.x;
+    int i = 0;                                                      // uniform: kernel arguments, scalar loads
+    for (int s = 32; s; s >>= 1)
+        if (i + s < L.n && L.ini[i + s] <= t) i += s;
+    const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
+    gemm_corpo<BLK, 1, KS>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i], L.N[i],
+                           L.K, kid + i, (local / ntx) * gemm::BM, (local % ntx) * gemm::BN);
 }
 
 // dynamic LDS bytes for nb K-blocks and KS K-splits

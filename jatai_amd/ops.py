@@ -31,7 +31,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
-           "jt_atencao_ws", "jt_atencao_back_ws")
+           "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -123,6 +123,35 @@ class OpsHip:
             C = self._novo_bloco(M, N, a.device)
             self._lanca("gemm", "jt_gemm", (a, ea, b, eb, C[0], C[1], None, None, M, N, K, 0), dict(A=a, EA=ea, B=b, EB=eb), (M, N))
         return C
+
+    # no reference counterpart: many raw GEMMs sharing K in one launch (48 per launch)
+    def gemm_cru_lote(self, pares):
+        """[gemm(A, B, cru=True, saida=S) for (A, B, S) in pares]; S may be None. Launch ids are consecutive."""
+        if not pares:
+            return []
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        self.reg.exige(self.lib.jt_entrada_g_bytes() == 64, "gemm_cru_lote: tamanho de entrada inesperado")
+        tab = (ctypes.c_longlong * (8 * len(pares)))()
+        saidas, kid0 = [], None
+        for i, (A, B, S) in enumerate(pares):
+            self.reg.confere_bloco("A", A); self.reg.confere_bloco("B", B)
+            (a, ea), (b, eb) = A, B
+            M, N, K = self._formas_gemm("gemm", a, b)
+            if S is None:
+                S = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(M, N, dtype=torch.int16, device=a.device))
+            self.reg.exige(S[0].dtype == torch.int32 and S[1].dtype == torch.int16 and tuple(S[0].shape) == (M, N)
+                           and tuple(S[1].shape) == (M, N) and S[0].is_contiguous() and S[1].is_contiguous(),
+                           f"gemm_cru_lote: saida deve ser (int32, int16) contiguos de forma {(M, N)}")
+            saidas.append(S)
+            kid = self.reg.registra("gemm_cru", dict(A=a, EA=ea, B=b, EB=eb), (M, N), tempo=(i == 0))
+            kid0 = kid if kid0 is None else kid0
+            tab[8 * i:8 * i + 8] = [a.data_ptr(), ea.data_ptr(), b.data_ptr(), eb.data_ptr(), S[0].data_ptr(), S[1].data_ptr(),
+                                    (N << 32) | M, K]
+        r = self.lib.jt_gemm_lote(ctypes.cast(tab, ctypes.c_void_p), ctypes.c_int(len(pares)), ctypes.c_int(kid0))
+        self.reg.depois(kid0, r)
+        return saidas
 
     def _gemm_fundida(self, op, modo, A, B, X=None, saida2=False):
         reg = self.reg

@@ -2,7 +2,9 @@
 
 * transpoe_lote over 70 tensors of mixed shapes (two launches: 64 tensors per launch) equals transpoe of each,
   at BLK 32 and 128, and each result equals the CPU oracle's transpose;
-* the model step with batched transposes leaves weights, momenta and residuals identical to one transpoe per use.
+* the model step with batched transposes leaves weights, momenta and residuals identical to one transpoe per use;
+* gemm_cru_lote over 50 GEMMs (two launches) equals one raw gemm each, at BLK 32 and 128, and a model step
+  with the deferred grouped weight-gradient GEMMs equals the step with one GEMM per gradient.
 """
 import numpy as np
 import pytest
@@ -45,6 +47,45 @@ def test_modelo_transpostas_em_lote():
     a, b = mk(), mk()
     b.transpostas_em_lote = False
     assert a.transpostas_em_lote
+    reg.novo_passo(0)
+    for p in range(2):
+        tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], "cuda")
+        assert float(a.passo(tok, alvo, k_lr=f["k_lr"])) == float(b.passo(tok, alvo, k_lr=f["k_lr"]))
+    est = lambda m: [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
+    assert est(a) == est(b)
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_gemm_cru_lote_igual_a_gemm(blk):
+    gpu = GPU(blk, vigiar=True)
+    K = 512
+    formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(50)]
+    pares, ref = [], []
+    for i, (M, N) in enumerate(formas):
+        A = tuple(gpu.dev(a) for a in R.bloco(R.substream(8, f"A {i}"), M, K, blk, espalha=4, e0=-6))
+        B = tuple(gpu.dev(a) for a in R.bloco(R.substream(8, f"B {i}"), N, K, blk, espalha=4, e0=-9))
+        pares.append((A, B, None))
+        ref.append(gpu.ops.gemm(A, B, cru=True))
+    out = gpu.ops.gemm_cru_lote(pares)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(out, ref)):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"GEMM {i} {formas[i]}"
+
+
+def test_modelo_dw_em_lote():
+    import traco as TR
+    from jatai_amd import ops as O
+    from jatai_amd.modelo import Modelo
+    from jatai_amd.registro import Registro
+    from backends import LOGS
+    O.BLK = 128
+    reg = Registro(LOGS, "lotes", vigiar=False, eco=False)
+    ops = O.OpsHip(reg)
+    f = TR.gold()["forma"]
+    mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", ops, reg)
+    a, b = mk(), mk()
+    b.dw_em_lote = False
+    assert a.dw_em_lote
     reg.novo_passo(0)
     for p in range(2):
         tok, alvo = TR.lote(p, f["Bt"], f["T"], f["V"], "cuda")

@@ -42,6 +42,7 @@ def roda(ops, reg, dev, passos, host):
     m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, rec, reg)
     m.otimizador_fundido = False        # the trace records momento, peso and transpoe per tensor, in the spec's order
     m.transpostas_em_lote = False
+    m.dw_em_lote = False
     init = {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()}
     out = []
     for p in range(passos):
