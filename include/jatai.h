@@ -53,6 +53,13 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
  * equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i). For the weight gradients of a step. */
 int jt_gemm_lote(const void* entradas, int n, int kid);
 int jt_entrada_g_bytes(void);          /* sizeof of one entry (64) */
+/* ---- no reference counterpart: n weight-gradient GEMMs sharing K with momento + peso in the epilogue, in launches of
+ * up to 32. `entradas` is a HOST array of n entries {const void *A, *EA, *B, *EB; void *Mm, *ME, *Wm, *WE, *Rm, *RE;
+ * int M, N, K, pad;}; entry i equals jt_gemm(A, EA, B, EB, NULL, NULL, G32, Ge, M, N, K, 1, kid + i), then
+ * jt_momento(G32, Ge, Mm, ME) and jt_peso(Wm, WE, Mm, ME, Rm, RE, k_lr, ef) on the [M, N] weight (ops.py:273-290),
+ * without storing the gradient. */
+int jt_gemm_otim_lote(const void* entradas, int n, int k_lr, int ef, int kid);
+int jt_entrada_go_bytes(void);         /* sizeof of one entry (96) */
 
 /* ---- element-wise, nblocos = elements / BLK (jatai_cuda.cu:1128-1154, 1074-1086) */
 int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid);

@@ -183,6 +183,47 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
 }
 int jt_entrada_g_bytes() { return (int)sizeof(EntradaG); }
 
+// No reference counterpart: n weight-gradient GEMMs sharing K with the optimizer applied in the epilogue, in launches
+// of up to 32 (host array of EntradaGO). Entry i equals jt_gemm(A, EA, B, EB, NULL, NULL, G32, Ge, M, N, K, 1,
+// kid + i) followed by jt_momento(G32, Ge, Mm, ME, ...) and jt_peso(Wm, WE, Mm, ME, Rm, RE, k_lr, ef, ...) on the
+// [M, N] weight, without storing the gradient.
+struct EntradaGO { const void *A, *EA, *B, *EB; void *Mm, *ME, *Wm, *WE, *Rm, *RE; int M, N, K, pad; };
+int jt_gemm_otim_lote(const void* entradas, int n, int k_lr, int ef, int kid) {
+    using namespace gemm;
+    if (n < 0 || (n > 0 && !entradas)) return (int)hipErrorInvalidValue;
+    const EntradaGO* e = (const EntradaGO*)entradas;
+    for (int base = 0; base < n; base += LOTE_GO) {
+        LoteGO L;
+        L.n = std::min(LOTE_GO, n - base);
+        L.K = e[base].K;
+        long long tot = 0;
+        for (int i = 0; i < L.n; i++) {
+            const EntradaGO& x = e[base + i];
+            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || x.K > 4096 || x.K <= 0) return (int)hipErrorInvalidValue;
+            if (!alinhados(x.A, x.EA, x.B, x.EB, x.Mm, x.ME, x.Wm, x.WE) || !alinhados(x.Rm, x.RE)) return (int)hipErrorInvalidValue;
+            L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
+            L.ot[i] = Otim{(int8_t*)x.Mm, (int8_t*)x.ME, (int8_t*)x.Wm, (int8_t*)x.WE, (int8_t*)x.Rm, (int8_t*)x.RE};
+            L.M[i] = x.M; L.N[i] = x.N; L.ini[i] = (int)tot;
+            tot += (long long)(x.M / BM) * (x.N / BN);
+        }
+        if (tot > 0x7fffffff) return (int)hipErrorInvalidValue;
+        L.ini[L.n] = (int)tot;
+        if (tot == 0) continue;
+        const int nb = L.K / g_blk;
+        int ks = 1;                                                  // mode 5: the epilogue is a fused one, at most 2 splits
+        while (ks < 2 && tot * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
+        const size_t lds = gemm_lds(nb, ks, g_blk);
+#define L_(BL, S) (lds_max(k_gemm_otim_lote<BL, S>, lds), k_gemm_otim_lote<BL, S><<<(unsigned)tot, 256 * S, lds, g_stream>>>(L, k_lr, ef, kid + base))
+        if (g_blk == 32) { if (ks == 1) L_(32, 1); else L_(32, 2); }
+        else { if (ks == 1) L_(128, 1); else L_(128, 2); }
+#undef L_
+        const int r = fim();
+        if (r) return r;
+    }
+    return 0;
+}
+int jt_entrada_go_bytes() { return (int)sizeof(EntradaGO); }
+
 // ---------------------------------------------------------------------------------------------- element-wise
 int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;

@@ -251,6 +251,84 @@ struct TabOtim {
     long long inicio, nblocos;
 };
 
+// momento then peso for NV consecutive values of one block, the block held by NL consecutive lanes: g raw with
+// exponents eg; o = offset of the first value in the tensor, w = its block, lider = the block's first lane. Used by
+// k_otimizador (NV = 8) and by the weight-gradient GEMM's epilogue (NV = 16).
+struct Otim {
+    int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE;
+};
+// the optimizer's inputs of NV values: loaded before any store (the three tensors are distinct, but the compiler
+// cannot know it and would otherwise order each load after the previous tensor's store)
+template <int NV>
+struct OtimEnt {
+    unsigned mm[NV / 4], wv[NV / 4], rv[NV / 4];                   // int8 values, 4 per register
+    int me, we, re;
+    __device__ int m(int i) const { return (int)(int8_t)(mm[i >> 2] >> (8 * (i & 3))); }
+    __device__ int w(int i) const { return (int)(int8_t)(wv[i >> 2] >> (8 * (i & 3))); }
+    __device__ int r(int i) const { return (int)(int8_t)(rv[i >> 2] >> (8 * (i & 3))); }
+};
+template <int NV>
+__device__ __forceinline__ void le_pk(const int8_t* p, unsigned (&d)[NV / 4]) {
+#pragma unroll
+    for (int k = 0; k < NV / 4; k += 2) {
+        const uint2 t = *reinterpret_cast<const uint2*>(p + 4 * k);
+        d[k] = t.x;
+        d[k + 1] = t.y;
+    }
+}
+template <int NV>
+__device__ __forceinline__ OtimEnt<NV> otim_le(const Otim& d, long long o, long long w, int ef) {
+    OtimEnt<NV> x;
+    le_pk<NV>(d.Mm + o, x.mm);
+    le_pk<NV>(d.Wm + o, x.wv);
+    if (ef) le_pk<NV>(d.Rm + o, x.rv);
+    else
+#pragma unroll
+        for (int i = 0; i < NV / 4; i++) x.rv[i] = 0;
+    x.me = d.ME[w];
+    x.we = d.WE[w];
+    x.re = ef ? (int)d.RE[w] : E_ZERO;
+    return x;
+}
+template <int NV, int NL>
+__device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)[NV], const OtimEnt<NV>& x, const Otim& d, long long o, long long w,
+                                             bool lider, int k_lr, int ef, int kid) {
+    int v[NV], ee[NV];
+    const int em = x.me - 3;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
+        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
+        v[i] = rnd(x.m(i) * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
+        ee[i] = ec;
+    }
+    int8_t q[NV];
+    const int Em = quant8<NV, NL>(v, ee, q, kid, o);
+    grava_i8(d.Mm + o, q);
+    if (lider) d.ME[w] = (int8_t)Em;
+    // peso with the new momentum
+    int alvo[NV];
+    const int ew = x.we, emk = Em - k_lr, er = x.re;
+    const int ec = max(max(ew + 7, emk + 7), er + 7) - 27;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        alvo[i] = rnd(x.w(i), ec - ew, kid, o + i) - rnd(q[i], ec - emk, kid, o + i) + (ef ? rnd(x.r(i), ec - er, kid, o + i) : 0);
+        ee[i] = ec;
+    }
+    int8_t qw[NV];
+    const int Ew = quant8<NV, NL>(alvo, ee, qw, kid, o);
+    grava_i8(d.Wm + o, qw);
+    if (lider) d.WE[w] = (int8_t)Ew;
+    if (!ef) return;
+    int dif[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) dif[i] = alvo[i] - (qw[i] == 0 ? 0 : rnd(qw[i], ec - Ew, kid, o + i));
+    int8_t r[NV];
+    const int Er = quant8<NV, NL>(dif, ee, r, kid, o);
+    grava_i8(d.Rm + o, r);
+    if (lider) d.RE[w] = (int8_t)Er;
+}
+
 template <int BLK>
 __global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ tab, int ntab, long long nblocos, int k_lr, int ef, int kid) {
     constexpr int LPB = BLK / VPL;
@@ -262,47 +340,10 @@ __global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ 
         if (t + s < ntab && tab[t + s].inicio <= wg) t += s;
     const TabOtim d = tab[t];
     const long long w = wg - d.inicio, o = w * BLK + (og % BLK);
-    int mm[VPL], g[VPL], eg[VPL], v[VPL], ee[VPL];
-    le_i8(d.Mm + o, mm);
+    const Otim ot{d.Mm, d.ME, d.Wm, d.WE, d.Rm, d.RE};
+    const OtimEnt<VPL> x = otim_le<VPL>(ot, o, w, ef);
+    int g[VPL], eg[VPL];
     le_i32(d.gacc + o, g);
     le_i16(d.ge + o, eg);
-    const int em = d.ME[w] - 3;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
-        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
-        v[i] = rnd(mm[i] * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
-        ee[i] = ec;
-    }
-    int8_t q[VPL];
-    const int Em = quant8<VPL, LPB>(v, ee, q, kid, o);
-    grava_i8(d.Mm + o, q);
-    const bool lider = (threadIdx.x & (LPB - 1)) == 0;
-    if (lider) d.ME[w] = (int8_t)Em;
-    // peso with the new momentum
-    int wv[VPL], rv[VPL], alvo[VPL];
-    le_i8(d.Wm + o, wv);
-    if (ef) le_i8(d.Rm + o, rv);
-    else
-#pragma unroll
-        for (int i = 0; i < VPL; i++) rv[i] = 0;
-    const int ew = d.WE[w], emk = Em - k_lr, er = ef ? (int)d.RE[w] : E_ZERO;
-    const int ec = max(max(ew + 7, emk + 7), er + 7) - 27;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        alvo[i] = rnd(wv[i], ec - ew, kid, o + i) - rnd(q[i], ec - emk, kid, o + i) + (ef ? rnd(rv[i], ec - er, kid, o + i) : 0);
-        ee[i] = ec;
-    }
-    int8_t qw[VPL];
-    const int Ew = quant8<VPL, LPB>(alvo, ee, qw, kid, o);
-    grava_i8(d.Wm + o, qw);
-    if (lider) d.WE[w] = (int8_t)Ew;
-    if (!ef) return;
-    int dif[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; i++) dif[i] = alvo[i] - (qw[i] == 0 ? 0 : rnd(qw[i], ec - Ew, kid, o + i));
-    int8_t r[VPL];
-    const int Er = quant8<VPL, LPB>(dif, ee, r, kid, o);
-    grava_i8(d.Rm + o, r);
-    if (lider) d.RE[w] = (int8_t)Er;
+    otim_valores<VPL, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid);
 }

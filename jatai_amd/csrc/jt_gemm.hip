@@ -47,7 +47,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                                            const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                            const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
-                                           int K, int kid, const int row0, const int col0) {
+                                           int K, int kid, const int row0, const int col0, const Otim ot = Otim{}, int k_lr = 0,
+                                           int ef = 0) {
     using namespace gemm;
     constexpr int SK = Est<BLK>::SK, LD = Est<BLK>::LD, STAGE = Est<BLK>::STAGE, VB = Est<BLK>::VB;
     extern __shared__ __align__(16) char smem[];
@@ -277,6 +278,10 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         for (int tj = 0; tj < 2; tj++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
+    OtimEnt<16> otx;                                               // mode 5: the optimizer's inputs, in flight during the LDS round trip
+    if constexpr (MODO == 5) {
+        if (tid < 256) otx = otim_le<16>(ot, (long long)o, (long long)(o / BLK), ef);
+    }
     __syncthreads();
     if constexpr (MODO == 1) {
         // raw output, coalesced: thread t writes column t % 128 of rows 16 (t / 128) .. +15 (64 consecutive ints per wave)
@@ -307,6 +312,13 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         constexpr int LPB = BLK / 16;
         const bool lider = (tid & (LPB - 1)) == 0;
+        if constexpr (MODO == 5) {                                 // weight gradient straight into momento + peso
+            int eg[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) eg[j] = max(-30000, base[j]);   // the raw output's int16 exponent
+            otim_valores<16, LPB>(v, eg, otx, ot, (long long)o, (long long)(o / BLK), lider, k_lr, ef, kid);
+            return;
+        }
         int8_t m[16];
         const int E = quant8<16, LPB>(v, base, m, kid, o);
         if constexpr (MODO == 0 || MODO == 3) {
@@ -380,6 +392,30 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
     gemm_corpo<BLK, 1, KS>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i], L.N[i],
                            L.K, kid + i, (local / ntx) * gemm::BM, (local % ntx) * gemm::BN);
+}
+
+// The weight gradients of a step with the optimizer in the epilogue (mode 5): GEMM i's tile goes through
+// momento + peso of tensor i (ops.py:273-290) instead of to memory -- the raw gradient is never stored.
+constexpr int LOTE_GO = 32;
+struct LoteGO {
+    const int8_t* A[LOTE_GO];
+    const int8_t* EA[LOTE_GO];
+    const int8_t* B[LOTE_GO];
+    const int8_t* EB[LOTE_GO];
+    Otim ot[LOTE_GO];
+    int M[LOTE_GO], N[LOTE_GO], ini[LOTE_GO + 1];
+    int n, K;
+};
+
+template <int BLK, int KS>
+__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_otim_lote(const LoteGO L, int k_lr, int ef, int kid) {
+    const int t = blockIdx.x;
+    int i = 0;
+    for (int s = 16; s; s >>= 1)
+        if (i + s < L.n && L.ini[i + s] <= t) i += s;
+    const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
+    gemm_corpo<BLK, 5, KS>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.M[i], L.N[i],
+                           L.K, kid + i, (local / ntx) * gemm::BM, (local % ntx) * gemm::BN, L.ot[i], k_lr, ef);
 }
 
 // dynamic LDS bytes for nb K-blocks and KS K-splits

@@ -31,7 +31,8 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_embed", "jt_um_quente", "jt_rms", "jt_rms_back", "jt_atencao", "jt_atencao_back", "jt_softmax_ce", "jt_erro_le",
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
-           "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes")
+           "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
+           "jt_gemm_otim_lote", "jt_entrada_go_bytes")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -152,6 +153,33 @@ class OpsHip:
         r = self.lib.jt_gemm_lote(ctypes.cast(tab, ctypes.c_void_p), ctypes.c_int(len(pares)), ctypes.c_int(kid0))
         self.reg.depois(kid0, r)
         return saidas
+
+    # no reference counterpart: weight-gradient GEMMs with momento + peso in the epilogue (32 per launch)
+    def gemm_otim_lote(self, itens, k, ef):
+        """For (A, B, Mom, W, R) in itens: momento(gemm(A, B, cru=True), Mom) then peso(W, Mom, R, k, ef), in place,
+        without storing the gradient. Launch ids are consecutive, one per item."""
+        if not itens:
+            return
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        self.reg.exige(self.lib.jt_entrada_go_bytes() == 96, "gemm_otim_lote: tamanho de entrada inesperado")
+        tab = (ctypes.c_longlong * (12 * len(itens)))()
+        kid0 = None
+        for i, (A, B, Mom, W, R) in enumerate(itens):
+            self.reg.confere_bloco("A", A); self.reg.confere_bloco("B", B)
+            for n_, t in (("momento", Mom), ("W", W), ("residuo", R)):
+                self.reg.confere_bloco(n_, t)
+            (a, ea), (b, eb) = A, B
+            M, N, K = self._formas_gemm("gemm", a, b)
+            self.reg.exige(all(tuple(t[0].shape) == (M, N) for t in (Mom, W, R)), f"gemm_otim_lote: peso de forma diferente de {(M, N)}")
+            kid = self.reg.registra("gemm_cru+otimizador", dict(A=a, EA=ea, B=b, EB=eb), (M, N), tempo=(i == 0))
+            kid0 = kid if kid0 is None else kid0
+            tab[12 * i:12 * i + 12] = [a.data_ptr(), ea.data_ptr(), b.data_ptr(), eb.data_ptr(), Mom[0].data_ptr(), Mom[1].data_ptr(),
+                                       W[0].data_ptr(), W[1].data_ptr(), R[0].data_ptr(), R[1].data_ptr(), (N << 32) | M, K]
+        r = self.lib.jt_gemm_otim_lote(ctypes.cast(tab, ctypes.c_void_p), ctypes.c_int(len(itens)), ctypes.c_int(k), ctypes.c_int(int(ef)),
+                                       ctypes.c_int(kid0))
+        self.reg.depois(kid0, r)
 
     def _gemm_fundida(self, op, modo, A, B, X=None, saida2=False):
         reg = self.reg

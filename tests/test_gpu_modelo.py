@@ -5,8 +5,9 @@
   (trace written from OpsRef + Modelo.passo, the reference's `conferir 2` protocol, treino_cuda.py:48-60);
 * the hipGraph-captured step replays to the same bits as eager steps, for every replay, with eager work and
   synchronization between replays; and the per-step (d_alvo, soma) of the golden loss trace;
-* the fused optimizer (momento + peso of all 50 tensors in one launch) leaves weights, momenta and residuals
-  bit-identical to momento then peso per tensor, with and without error feedback;
+* the fused optimizer (momento + peso of all 50 tensors in one launch, or in the epilogue of the grouped
+  weight-gradient GEMMs) leaves weights, momenta and residuals bit-identical to momento then peso per tensor, with
+  and without error feedback;
 * a token outside the vocabulary inside a replayed graph raises ErroJatai naming op embed, scope
   "forward / embedding", row 401, value 300 (the reference's teste_erro_grafo.py:13-30).
 """
@@ -103,8 +104,9 @@ def test_erro_no_grafo():
     assert "operacao : embed" in msg
 
 
+@pytest.mark.parametrize("dw_lote", [True, False], ids=["otimizador-no-gemm", "tabela"])
 @pytest.mark.parametrize("ef", [True, False])
-def test_otimizador_fundido_igual_por_tensor(ef):
+def test_otimizador_fundido_igual_por_tensor(ef, dw_lote):
     from jatai_amd.modelo import Modelo
     g = TR.gold()
     f = g["forma"]
@@ -112,7 +114,8 @@ def test_otimizador_fundido_igual_por_tensor(ef):
     mk = lambda: Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", ops, reg)
     fundido, separado = mk(), mk()
     separado.otimizador_fundido = False
-    assert fundido.otimizador_fundido
+    fundido.otim_no_gemm = dw_lote                  # True: momento + peso in the grouped GEMM's epilogue
+    assert fundido.otimizador_fundido and fundido._otim_no_gemm() == dw_lote
     for m in (fundido, separado):
         m.error_feedback = ef
     reg.novo_passo(0)
