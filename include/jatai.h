@@ -108,6 +108,10 @@ int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P,
                   long long ws_bytes, int kid);
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge,
                     int Bt, int T, int H, int D, int GA, int limite, int kid);
+/* no reference counterpart: jt_atencao_ws writing the output already quantized (Om int8 [M, D], OE int8 [M, D/32]),
+ * equal to jt_quant of the raw output; head width 64 on matrix cores at BLK = 32 only, else hipErrorNotSupported. */
+int jt_atencao_ws_q(const void* qm, const void* qE, void* Om, void* OE, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                    long long ws_bytes, int kid);
 /* no reference counterpart: jt_atencao_back with a caller workspace of jt_atencao_back_ws_bytes(Bt, T, H, D) bytes
  * (16-byte aligned); same outputs. At head width 64 on matrix cores (T <= 512) dO, q, k, v are converted once per
  * (sequence, head) into the workspace and each 16-row tile's partner tiles are split over four waves; otherwise
@@ -115,6 +119,10 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
 long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D);
 int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
                        int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid);
+/* no reference counterpart: jt_atencao_back_ws writing the gradient already quantized (Gm int8 [M, 3D], GE int8
+ * [M, 3D/32]), equal to jt_quant of the raw gradient; same support as jt_atencao_ws_q. */
+int jt_atencao_back_ws_q(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
+                         int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid);
 
 #ifdef __cplusplus
 }

@@ -459,21 +459,34 @@ long long jt_atencao_ws_bytes(int Bt, int T, int H, int D) {
     if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
     return (long long)atw::bytes_fwd((long long)Bt * H, T);
 }
-int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
-                  long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
-    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, kid);
-    if (!alinhados(qm, qE, Oacc, Oe, P, ws) || !ws || ws_bytes < jt_atencao_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+static int atencao_ws(const void* qm, const void* qE, void* O1, void* O2, void* P, int Bt, int T, int H, int D, int GA, void* ws, long long ws_bytes,
+                      bool bloco, int kid) {
+    if (!alinhados(qm, qE, O1, O2, P, ws) || !ws || ws_bytes < jt_atencao_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
         return (int)hipErrorInvalidValue;
     const long long BH = (long long)Bt * H;
     const atw::Ws w = atw::parte(ws, BH, T);
     k_atf_prep<<<(unsigned)(BH * (T / 64)), 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, T, H, D, g_blk, GA);
     const unsigned g = (unsigned)(BH * (T / 16));
-#define L(NTW) k_atf<NTW><<<g, 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, \
-                                                g_blk, GA, kid)
-    if (T <= 256) L(4); else L(8);
+#define L(NTW, B) k_atf<NTW, B><<<g, 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, O1, O2, (uint8_t*)P, T, H, D, g_blk, GA, kid)
+    if (bloco) { if (T <= 256) L(4, true); else L(8, true); }
+    else { if (T <= 256) L(4, false); else L(8, false); }
 #undef L
     return fim();
+}
+int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                  long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, kid);
+    return atencao_ws(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, ws, ws_bytes, false, kid);
+}
+// No reference counterpart: jt_atencao_ws writing the output quantized to block format (Om int8 [M, D], OE int8
+// [M, D/32]), equal to jt_quant of the raw output. Head width 64 on matrix cores at BLK = 32 only (a block is then
+// half a head); hipErrorNotSupported otherwise.
+int jt_atencao_ws_q(const void* qm, const void* qE, void* Om, void* OE, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                    long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
+    return atencao_ws(qm, qE, Om, OE, P, Bt, T, H, D, GA, ws, ws_bytes, true, kid);
 }
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
@@ -547,11 +560,9 @@ long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D) {
     if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
     return (long long)atw::bytes_back((long long)Bt * H, T);
 }
-int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
-                       int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
-    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
-    if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge, ws) || !ws || ws_bytes < jt_atencao_back_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+static int atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* G1, void* G2, int Bt, int T,
+                           int H, int D, int GA, int limite, void* ws, long long ws_bytes, bool bloco, int kid) {
+    if (!alinhados(gom, goE, qm, qE, P, G1, G2, ws) || !ws || ws_bytes < jt_atencao_back_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
         return (int)hipErrorInvalidValue;
     const long long BH = (long long)Bt * H;
     const atw::WsB w = atw::parte_b(ws, BH, T);
@@ -559,17 +570,34 @@ int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const v
     const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
     const uint8_t* P8 = (const uint8_t*)P;
     const unsigned gp = (unsigned)(BH * (T / 64)), gt = (unsigned)(BH * (T / 16));
-#define FASES(NTW, LM)                                                                                                    \
+#define FASES(NTW, LM, B)                                                                                                 \
     {                                                                                                                     \
         k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                              \
         if (!LM) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                                          \
         k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \
-        k_atbq<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, (int*)Gacc, (int16_t*)Ge, T, H, D, dsb, kid);                     \
-        k_atbkv<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, (int*)Gacc, (int16_t*)Ge, T, H, D, dsb, kid);                    \
+        k_atbq<NTW, LM, B><<<gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);                    \
+        k_atbkv<NTW, LM, B><<<gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);                   \
     }
-    if (T <= 256) { if (limite) FASES(4, 1) else FASES(4, 0) }
-    else { if (limite) FASES(8, 1) else FASES(8, 0) }
+#define VAR(B) { if (T <= 256) { if (limite) FASES(4, 1, B) else FASES(4, 0, B) } else { if (limite) FASES(8, 1, B) else FASES(8, 0, B) } }
+    if (bloco) VAR(true) else VAR(false)
+#undef VAR
 #undef FASES
     return fim();
 }
+int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
+                       int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
+    return atencao_back_ws(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, ws, ws_bytes, false, kid);
+}
+// No reference counterpart: jt_atencao_back_ws writing the gradient quantized to block format (Gm int8 [M, 3D],
+// GE int8 [M, 3D/32]), equal to jt_quant of the raw gradient. Head width 64 on matrix cores at BLK = 32 only;
+// hipErrorNotSupported otherwise.
+int jt_atencao_back_ws_q(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
+                         int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
+    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
+    return atencao_back_ws(gom, goE, qm, qE, P, Gm, GE, Bt, T, H, D, GA, limite, ws, ws_bytes, true, kid);
+}
+
 }  // extern "C"

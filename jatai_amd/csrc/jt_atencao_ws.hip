@@ -95,9 +95,22 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
 }
 
 // NTW = key tiles a wave can own (T / 64)
-template <int NTW>
-__global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, int* __restrict__ Oacc,
-                                             int16_t* __restrict__ Oe, uint8_t* __restrict__ P, int T, int H, int D, int blk, int GA, int kid) {
+// Outputs of 16 rows x the head's 64 columns in block format (BLK = 32: two blocks per row): thread t holds row
+// t / 16, columns 4 (t % 16) .. + 3; the 8 lanes of a block are consecutive. Same result as quant of the raw
+// output (ops.py:125-126) with the block's common exponent e.
+__device__ __forceinline__ void grava_bloco4(const int (&v)[4], int e, int8_t* __restrict__ Mm, int8_t* __restrict__ ME, size_t x, size_t xe,
+                                             int kid) {
+    int ee[4] = {e, e, e, e};
+    int8_t q[4];
+    const int E = quant8<4, 8>(v, ee, q, kid, (long long)x);
+    grava_i8(Mm + x, q);
+    if ((threadIdx.x & 7) == 0) ME[xe] = (int8_t)E;
+}
+
+// BLOCO: the output in block format (Oacc, Oe are then the mantissas and exponents, int8) instead of raw
+template <int NTW, bool BLOCO = false>
+__global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, void* __restrict__ Oacc_,
+                                             void* __restrict__ Oe_, uint8_t* __restrict__ P, int T, int H, int D, int blk, int GA, int kid) {
     constexpr int HD = 64, LP = 16 * (NTW + 1);                     // LDS row length of a wave's P (one pad tile)
     __shared__ int sred[4][16];
     __shared__ __align__(16) _Float16 pw[4][16][LP];
@@ -235,6 +248,20 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 #pragma unroll
         for (int v = 0; v < 4; v++) so[wv][4 * lg + v][16 * dt + lr] = o[dt][v];
     __syncthreads();
+    if constexpr (BLOCO) {
+        const int r = tid >> 4, c = 4 * (tid & 15);
+        int ov[4];
+        const size_t x = (size_t)(b0 + 16 * qt + r) * D + h * HD + c;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            ov[k] = (int)(so[0][r][c + k] + so[1][r][c + k] + so[2][r][c + k] + so[3][r][c + k]);
+            if (ov[k] >= LIM || ov[k] <= -LIM) reporta(E_ACUM, kid, x + k, ov[k], -3);
+        }
+        grava_bloco4(ov, ev - 8, (int8_t*)Oacc_, (int8_t*)Oe_, x, (size_t)(b0 + 16 * qt + r) * (D / 32) + (h * HD + c) / 32, kid);
+        return;
+    }
+    int* Oacc = (int*)Oacc_;
+    int16_t* Oe = (int16_t*)Oe_;
     // wave wv writes the 16 dimensions 16 wv .. 16 wv + 15
 #pragma unroll
     for (int v = 0; v < 4; v++) {
@@ -520,7 +547,21 @@ __device__ __forceinline__ void soma_ondas(long long (&parc)[4][16][64], const l
     __syncthreads();
 }
 
-template <int NTW, int LIMITE>
+// as soma_ondas, read back in the block layout of grava_bloco4: out[k] = row tid / 16, column 4 (tid % 16) + k
+__device__ __forceinline__ void soma_ondas_bloco(long long (&parc)[4][16][64], const long long (&mine)[4][4], int wv, int lr, int lg,
+                                                 long long (&out)[4]) {
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) parc[wv][4 * lg + v][16 * dt + lr] = mine[dt][v];
+    __syncthreads();
+    const int r = threadIdx.x >> 4, c = 4 * (threadIdx.x & 15);
+#pragma unroll
+    for (int k = 0; k < 4; k++) out[k] = parc[0][r][c + k] + parc[1][r][c + k] + parc[2][r][c + k] + parc[3][r][c + k];
+    __syncthreads();
+}
+
+template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge, int T,
                                               int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
@@ -575,8 +616,21 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int v = 0; v < 4; v++) mine[dt][v] = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
-    soma_ondas(parc, mine, wv, lr, lg, gq);
     const int ld = 3 * D;
+    if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
+        soma_ondas_bloco(parc, mine, wv, lr, lg, gq);
+        const int r = tid >> 4, c = 4 * (tid & 15);
+        const size_t x = (size_t)(b0 + 16 * qt + r) * ld + h * 64 + c;
+        int g4[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (gq[k] >= LIM || gq[k] <= -LIM) reporta(E_ACUM, kid, x + k, gq[k], -5);
+            g4[k] = (int)gq[k];
+        }
+        grava_bloco4(g4, eds + ek, (int8_t*)Gacc, (int8_t*)Ge, x, (size_t)(b0 + 16 * qt + r) * (ld / 32) + (h * 64 + c) / 32, kid);
+        return;
+    }
+    soma_ondas(parc, mine, wv, lr, lg, gq);
 #pragma unroll
     for (int v = 0; v < 4; v++) {
         const size_t o = (size_t)(b0 + i0 + v) * ld + h * 64 + 16 * wv + lr;
@@ -586,7 +640,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
     }
 }
 
-template <int NTW, int LIMITE>
+template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
                                                int T, int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
@@ -660,13 +714,34 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int v = 0; v < 4; v++) mine[dt][v] = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
+    const int ld = 3 * D;
+    if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
+        soma_ondas_bloco(parc, mine, wv, lr, lg, gk);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) mine[dt][v] = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+        soma_ondas_bloco(parc, mine, wv, lr, lg, gvv);
+        const int r = tid >> 4, c = 4 * (tid & 15);
+        const size_t x = (size_t)(b0 + 16 * kt + r) * ld + h * 64 + c, xe = (size_t)(b0 + 16 * kt + r) * (ld / 32) + (h * 64 + c) / 32;
+        int a4[4], b4[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (gk[k] >= LIM || gk[k] <= -LIM) reporta(E_ACUM, kid, x + D + k, gk[k], -5);
+            if (gvv[k] >= LIM || gvv[k] <= -LIM) reporta(E_ACUM, kid, x + 2 * D + k, gvv[k], -5);
+            a4[k] = (int)gk[k];
+            b4[k] = (int)gvv[k];
+        }
+        grava_bloco4(a4, eds + eq, (int8_t*)Gacc, (int8_t*)Ge, x + D, xe + D / 32, kid);
+        grava_bloco4(b4, ego - 8, (int8_t*)Gacc, (int8_t*)Ge, x + 2 * D, xe + 2 * D / 32, kid);
+        return;
+    }
     soma_ondas(parc, mine, wv, lr, lg, gk);
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int v = 0; v < 4; v++) mine[dt][v] = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
     soma_ondas(parc, mine, wv, lr, lg, gvv);
-    const int ld = 3 * D;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
         const size_t o = (size_t)(b0 + jr + v) * ld + h * 64 + 16 * wv + lr;

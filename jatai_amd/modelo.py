@@ -69,6 +69,8 @@ class Modelo:
         # 4). Off by default: the optimizer is bound by its own arithmetic, so the separate pass is as fast
         # (measured 0.80 ms vs 0.82 ms per step at config 4).
         self.otim_no_gemm = False
+        # attention kernels that write their outputs quantized (quant(atencao), quant(atencao_back)): same results
+        self.quant_na_atencao = hasattr(ops, "atencao_q")
         self._gbuf, self._tabela = None, None
 
     def _otim_no_gemm(self):
@@ -103,8 +105,11 @@ class Modelo:
                     with reg.trecho("atencao"):
                         n1, c1 = ops.rms(ops.para8(x16) if r16 else x)
                         qkv = ops.gemm(n1, p[f"Wqkv{l}"])
-                        oc, P = ops.atencao(qkv, Bt, T, self.H)
-                        om = ops.quant(oc)
+                        if self.quant_na_atencao:
+                            om, P = ops.atencao_q(qkv, Bt, T, self.H)
+                        else:
+                            oc, P = ops.atencao(qkv, Bt, T, self.H)
+                            om = ops.quant(oc)
                         if r16:
                             x16 = ops.soma16(x16, ops.gemm(om, p[f"Wo{l}"]))
                             x = ops.para8(x16) if self.estatisticas else None
@@ -174,7 +179,10 @@ class Modelo:
                     with reg.trecho("atencao"):
                         grads[f"Wo{l}"] = grad_w(f"Wo{l}", T_(gx), T_(om))
                         go = ops.gemm(gx, T_(p[f"Wo{l}"]))
-                        gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
+                        if self.quant_na_atencao:
+                            gq = ops.atencao_back_q(go, qkv, P, Bt, T, self.H)
+                        else:
+                            gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
                         grads[f"Wqkv{l}"] = grad_w(f"Wqkv{l}", T_(gq), T_(n1))
                         gn = ops.gemm(gq, T_(p[f"Wqkv{l}"]))
                         if r16:

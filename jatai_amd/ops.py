@@ -32,7 +32,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
-           "jt_gemm_otim_lote", "jt_entrada_go_bytes")
+           "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -350,6 +350,45 @@ class OpsHip:
         else:
             self._lanca("atencao", "jt_atencao", (m, E, oacc, oe, P, Bt, T, H, D, GA), dict(qkv=m, qkvE=E), (Bt * T, D))
         return (oacc, oe), P
+
+    # no reference counterpart: attention whose outputs come already quantized (quant(atencao(...)) in one launch
+    # sequence); where the kernels cannot (not head width 64 at BLK = 32), the op-by-op composition runs instead
+    def _q_suportado(self, T, H, D):
+        return ATENCAO_WS and BLK == 32 and H and D % H == 0 and D // H == 64 and T <= 512
+
+    def atencao_q(self, QKV, Bt, T, H):
+        """(quant(O), P) for (O, P) = atencao(QKV, Bt, T, H)."""
+        m, E = QKV
+        D = m.shape[1] // 3
+        if not self._q_suportado(T, H, D):
+            oc, P = self.atencao(QKV, Bt, T, H)
+            return self.quant(oc), P
+        self.reg.confere_bloco("qkv", QKV)
+        self._formas_atencao("atencao", m, Bt, T, H, D)
+        Om = self._novo_bloco(Bt * T, D, m.device)
+        P = torch.empty(Bt * H, T, T, dtype=torch.uint8, device=m.device)
+        nws = self.lib.jt_atencao_ws_bytes(Bt, T, H, D)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+        self._lanca("atencao+quant", "jt_atencao_ws_q", (m, E, Om[0], Om[1], P, Bt, T, H, D, GA, ws, nws), dict(qkv=m, qkvE=E), (Bt * T, D),
+                    longos=(11,))
+        return Om, P
+
+    def atencao_back_q(self, GO, QKV, P, Bt, T, H):
+        """quant(atencao_back(GO, QKV, P, Bt, T, H))."""
+        (gm, gE), (m, E) = GO, QKV
+        D = gm.shape[1]
+        if not self._q_suportado(T, H, D):
+            return self.quant(self.atencao_back(GO, QKV, P, Bt, T, H))
+        self.reg.confere_bloco("go", GO); self.reg.confere_bloco("qkv", QKV)
+        self._formas_atencao("atencao_back", m, Bt, T, H, D)
+        self.reg.exige(tuple(P.shape) == (Bt * H, T, T) and P.dtype == torch.uint8 and P.is_contiguous(),
+                       f"atencao_back: P com forma {tuple(P.shape)}, esperado {(Bt * H, T, T)} uint8")
+        G = self._novo_bloco(Bt * T, 3 * D, m.device)
+        nws = self.lib.jt_atencao_back_ws_bytes(Bt, T, H, D)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+        self._lanca("atencao_back+quant", "jt_atencao_back_ws_q", (gm, gE, m, E, P, G[0], G[1], Bt, T, H, D, GA, int(ATENCAO_LIMITE), ws, nws),
+                    dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D), longos=(14,))
+        return G
 
     def _formas_atencao(self, op, m, Bt, T, H, D):
         """Head width hd = D/H: 4 is the spec's shape (T <= 256); 16, 32 and 64 run the generalized kernels

@@ -55,3 +55,25 @@ def test_atencao_hd_vs_oraculo(blk, Bt, T, H, D, esp, e0, limite, via_ws):
         res.append((oacc, oe, P, gacc, ge))
     for nome, a, b in zip(("oacc", "oe", "P", "gacc", "ge"), *res):
         _cmp(a, b, nome)
+
+
+@pytest.mark.parametrize("T,H,limite", [(256, 8, False), (256, 8, True), (512, 4, False)])
+def test_atencao_q_igual_a_quant(T, H, limite):
+    """atencao_q / atencao_back_q (outputs quantized inside the attention kernels) equal quant of the raw outputs."""
+    blk, Bt, D = 32, 2, 64 * H
+    gpu = GPU(blk, vigiar=True)
+    seed = R.substream(556, f"q {T} {H} {limite}")
+    qkv = tuple(gpu.dev(v) for v in R.bloco(R.substream(seed, "qkv"), Bt * T, 3 * D, blk, espalha=4, e0=-7, zera=0.05))
+    go = tuple(gpu.dev(v) for v in R.bloco(R.substream(seed, "go"), Bt * T, D, blk, espalha=4, e0=-20, zera=0.05))
+    o = gpu.ops
+    old = gpu.limite(limite)
+    try:
+        om, P = o.atencao_q(qkv, Bt, T, H)
+        oc, P2 = o.atencao(qkv, Bt, T, H)
+        ref = o.quant(oc)
+        gq = o.atencao_back_q(go, qkv, P, Bt, T, H)
+        gref = o.quant(o.atencao_back(go, qkv, P, Bt, T, H))
+    finally:
+        gpu.limite(old)
+    for nome, a, b in (("om", om[0], ref[0]), ("omE", om[1], ref[1]), ("P", P, P2), ("gq", gq[0], gref[0]), ("gqE", gq[1], gref[1])):
+        _cmp(a, b, nome)

@@ -43,6 +43,7 @@ def roda(ops, reg, dev, passos, host):
     m.otimizador_fundido = False        # the trace records momento, peso and transpoe per tensor, in the spec's order
     m.transpostas_em_lote = False
     m.dw_em_lote = False
+    m.quant_na_atencao = False
     init = {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()}
     out = []
     for p in range(passos):
