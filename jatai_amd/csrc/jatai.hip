@@ -114,7 +114,9 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk;
-    const int ks = gemm_divisoes(M, N, K, modo);
+    // mode 4 with Om2: the transposed copy needs a single K-split (BLK = 32 only)
+    if (modo == 4 && (Om2 || OE2) && (g_blk != 32 || !Om2 || !OE2)) return (int)hipErrorInvalidValue;
+    const int ks = (modo == 4 && Om2) ? 1 : gemm_divisoes(M, N, K, modo);
     const dim3 grade(N / BN, M / BM);
     const size_t lds = gemm_lds(nb, ks, g_blk);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \

@@ -355,6 +355,32 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             if (Eg > 126 && lider) reporta(E_EXP, kid, (long long)o, Eg, -8);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Eg;
+            if constexpr (KS == 1 && BLK == 32) {
+                // Om2 given: also the transpose T(gh) [N, M] blocked along M. The tile's 32 rows are one block of each
+                // of its 128 columns: the same requantization as k_transpoe (quant(m^T, expand(E)^T), ops.py:121-123),
+                // from the quantized tile staged in LDS. KS = 1: every thread is here, so the barriers are uniform.
+                if (Om2 != nullptr) {
+                    int8_t* qs = reinterpret_cast<int8_t*>(buf);           // [BM][BN + 16] mantissas
+                    int8_t* es = qs + BM * (BN + 16);                       // [BM][BN / 32] exponents
+                    __syncthreads();                                        // acc_s fully read before the reuse
+                    grava_i8(qs + orow * (BN + 16) + oc, q);
+                    if (lider) es[orow * (BN / 32) + oc / 32] = (int8_t)Eg;
+                    __syncthreads();
+                    const int c = tid >> 1, hf = tid & 1;                   // column c, rows 16 hf .. 16 hf + 15
+                    int tv[16], te[16];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) {
+                        const int r = 16 * hf + k;
+                        tv[k] = qs[r * (BN + 16) + c];
+                        te[k] = es[r * (BN / 32) + (c >> 5)];
+                    }
+                    int8_t t8[16];
+                    const long long ot = (long long)(col0 + c) * M + row0 + 16 * hf;
+                    const int Et = quant8<16, 2>(tv, te, t8, kid, ot);
+                    grava_i8(Om2 + ot, t8);
+                    if (hf == 0) OE2[(size_t)(col0 + c) * (M / 32) + row0 / 32] = (int8_t)Et;
+                }
+            }
         }
     }
 }

@@ -71,6 +71,8 @@ class Modelo:
         self.otim_no_gemm = False
         # attention kernels that write their outputs quantized (quant(atencao), quant(atencao_back)): same results
         self.quant_na_atencao = hasattr(ops, "atencao_q")
+        # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand)
+        self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
         self._gbuf, self._tabela = None, None
 
     def _otim_no_gemm(self):
@@ -167,7 +169,11 @@ class Modelo:
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("mlp"):
                         grads[f"Wd{l}"] = grad_w(f"Wd{l}", T_(gx), T_(a))
-                        gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
+                        if self.transposta_na_gemm:
+                            gh, tgh = ops.gemm_relu2_back_t(gx, T_(p[f"Wd{l}"]), h)
+                            prontas[id(gh[0])] = tgh
+                        else:
+                            gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
                         grads[f"Wup{l}"] = grad_w(f"Wup{l}", T_(gh), T_(n2))
                         gn = ops.gemm(gh, T_(p[f"Wup{l}"]))
                         if r16:

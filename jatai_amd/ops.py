@@ -203,6 +203,21 @@ class OpsHip:
     def gemm_relu2(self, A, B):
         return self._gemm_fundida("gemm_relu2", 3, A, B, saida2=True)
 
+    # no reference counterpart: (gemm_relu2_back(A, B, Hh), its transpose) from one launch at BLK = 32
+    def gemm_relu2_back_t(self, A, B, Hh):
+        if BLK != 32:
+            G = self.gemm_relu2_back(A, B, Hh)
+            return G, self.transpoe(G)
+        reg = self.reg
+        reg.confere_bloco("A", A); reg.confere_bloco("B", B); reg.confere_bloco("X", Hh)
+        (a, ea), (b, eb) = A, B
+        M, N, K = self._formas_gemm("gemm_relu2_back", a, b)
+        reg.exige(tuple(Hh[0].shape) == (M, N), f"gemm_relu2_back: X com forma {tuple(Hh[0].shape)}, esperado {(M, N)}")
+        C, Ct = self._novo_bloco(M, N, a.device), self._novo_bloco(N, M, a.device)
+        self._lanca("gemm_relu2_back+transpoe", "jt_gemm_f", (a, ea, b, eb, C[0], C[1], None, None, Hh[0], Hh[1], Ct[0], Ct[1], M, N, K, 4),
+                    dict(A=a, EA=ea, B=b, EB=eb, X=Hh[0], XE=Hh[1]), (M, N))
+        return C, Ct
+
     def gemm_relu2_back(self, A, B, Hh):
         return self._gemm_fundida("gemm_relu2_back", 4, A, B, X=Hh)
 

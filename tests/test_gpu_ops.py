@@ -163,3 +163,25 @@ def test_gemm_k_impar_todos_os_modos(blk, K):
             gpu.ops.lib.jt_gemm_split(1024)
         for modo, (a, b) in enumerate(zip(out, ref)):
             _compara(a, b, f"BLK={blk} K={K} mode {modo} split target {alvo}")
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 512), (256, 384, 96), (64, 128, 32)])
+def test_gemm_relu2_back_t(M, N, K):
+    """Mode 4 with the transposed copy (BLK = 32): the block output equals gemm_relu2_back and the copy equals
+    transpoe of it."""
+    blk = 32
+    gpu = GPU(blk, vigiar=True)
+    s = lambda t: R.substream(92, f"{M} {N} {K} {t}")
+    A = tuple(gpu.dev(v) for v in R.bloco(s("A"), M, K, blk, espalha=4, e0=-6))
+    B = tuple(gpu.dev(v) for v in R.bloco(s("B"), N, K, blk, espalha=4, e0=-9))
+    Hh = tuple(gpu.dev(v) for v in R.bloco(s("H"), M, N, blk, espalha=3, e0=-4, zera=0.1))
+    o = gpu.ops
+    G, Gt = o.gemm_relu2_back_t(A, B, Hh)
+    ref = o.gemm_relu2_back(A, B, Hh)
+    reft = o.transpoe(ref) if M % 128 == 0 else None
+    _compara(G, ref, "gemm_relu2_back")
+    if reft is not None:
+        _compara(Gt, reft, "transpoe")
+    else:                                                            # transpoe needs R % 128: check against the oracle
+        cpu = CPU(blk)
+        _compara(Gt, cpu.ops.transpoe(tuple(torch.from_numpy(host(t)) for t in ref)), "transpoe (oracle)")
