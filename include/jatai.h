@@ -95,6 +95,9 @@ int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid);
 int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid);
 int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om,
                 void* oE, int M, int D, int log2D, int G, int GB, int kid);
+/* no reference counterpart: om = soma(x, rms_back(g, y, cache)) in one launch (kid: rms_back part, kid + 1: soma) */
+int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, const void* xm,
+                     const void* xE, void* om, void* oE, int M, int D, int log2D, int G, int GB, int kid);
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V,
                   int log2M, int kid);
 

@@ -408,6 +408,23 @@ int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, 
 #undef K3
     return fim();
 }
+// No reference counterpart: soma(x, rms_back(g, y, cache)) in one launch (the backward's residual update); equals
+// jt_rms_back into a temporary then jt_soma(x, temporary). Launch ids: kid for the rms_back part, kid + 1 for soma.
+int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, const void* xm,
+                     const void* xE, void* om, void* oE, int M, int D, int log2D, int G, int GB, int kid) {
+    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE) || !alinhados(xm, xE)) return (int)hipErrorInvalidValue;
+#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                       \
+        if (g_blk == 32) k_rms_back<VP, LP, 32, true><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,       \
+            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm,         \
+            (const int8_t*)xE, kid + 1);                                                                                                     \
+        else k_rms_back<VP, LP, 128, true><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,                  \
+            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm,         \
+            (const int8_t*)xE, kid + 1); }
+    POR_LINHA(D, K3)
+#undef K3
+    return fim();
+}
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V, int log2M,
                   int kid) {
     if (M <= 0 || V % g_blk) return (int)hipErrorInvalidValue;

@@ -35,11 +35,13 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
     if (lr == 0) { cr[row] = r; cemax[row] = emax; }
 }
 
-// RMSNorm backward: dx = (g - y * mean(g y)) / rms in the spec's integer steps (ops.py:167-184)
-template <int VPR, int LPR, int BLK>
+// RMSNorm backward: dx = (g - y * mean(g y)) / rms in the spec's integer steps (ops.py:167-184). SOMA: the output
+// is soma(x, dx) instead (ops.py:128-132, x given by xm, xE), as the backward's residual update uses it.
+template <int VPR, int LPR, int BLK, bool SOMA = false>
 __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ ym,
                                                   const int8_t* __restrict__ yE, const int* __restrict__ cr, const int* __restrict__ cemax,
-                                                  int8_t* __restrict__ om, int8_t* __restrict__ oE, int M, int log2D, int G, int GB, int kid) {
+                                                  int8_t* __restrict__ om, int8_t* __restrict__ oE, int M, int log2D, int G, int GB, int kid,
+                                                  const int8_t* __restrict__ xm = nullptr, const int8_t* __restrict__ xE = nullptr, int kid2 = 0) {
     constexpr int D = VPR * LPR, nb = D / BLK, LPB = BLK / VPR;
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
     if (row >= M) return;
@@ -71,6 +73,17 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
     }
     int8_t q[VPR];
     const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    if constexpr (SOMA) {                                            // z = soma(x, dx): ec = max(xE, E) - 21
+        int a[VPR], zs[VPR];
+        le_i8(xm + o, a);
+        const int ex = xE[(long long)row * nb + b], ec = max(ex, Eo) - 21;
+#pragma unroll
+        for (int i = 0; i < VPR; i++) { zs[i] = rnd(a[i], ec - ex, kid2, o + i) + rnd((int)q[i], ec - Eo, kid2, o + i); ee[i] = ec; }
+        const int Ez = quant8<VPR, LPB>(zs, ee, q, kid2, o);
+        grava_i8(om + o, q);
+        if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Ez;
+        return;
+    }
     grava_i8(om + o, q);
     if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Eo;
 }

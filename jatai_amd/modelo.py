@@ -73,6 +73,8 @@ class Modelo:
         self.quant_na_atencao = hasattr(ops, "atencao_q")
         # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand)
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
+        # the residual update of the backward, soma(gx, rms_back(...)), in one launch
+        self.rms_soma = hasattr(ops, "rms_back_soma")
         self._gbuf, self._tabela = None, None
 
     def _otim_no_gemm(self):
@@ -180,7 +182,7 @@ class Modelo:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n2, c2))
                             gx = ops.para8(gx16)
                         else:
-                            gx = ops.soma(gx, ops.rms_back(gn, n2, c2))
+                            gx = ops.rms_back_soma(gn, n2, c2, gx) if self.rms_soma else ops.soma(gx, ops.rms_back(gn, n2, c2))
                         self._st(f"c{l}.grad_mlp", gh, zeros_normais=True)
                     with reg.trecho("atencao"):
                         grads[f"Wo{l}"] = grad_w(f"Wo{l}", T_(gx), T_(om))
@@ -195,7 +197,7 @@ class Modelo:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n1, c1))
                             gx = ops.para8(gx16)
                         else:
-                            gx = ops.soma(gx, ops.rms_back(gn, n1, c1))
+                            gx = ops.rms_back_soma(gn, n1, c1, gx) if self.rms_soma else ops.soma(gx, ops.rms_back(gn, n1, c1))
                         self._st(f"c{l}.grad_qkv", gq); self._st(f"c{l}.grad_residuo", gx)
             with reg.trecho("embedding"):
                 um = ops.um_quente(tok, self.V)

@@ -32,7 +32,8 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_erro_limpa", "jt_sincroniza", "jt_para16", "jt_para8", "jt_soma16", "jt_res_estocastico", "jt_bloco",
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
-           "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q")
+           "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
+           "jt_rms_back_soma")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -347,6 +348,24 @@ class OpsHip:
         O = self._novo_bloco(M, D, g.device)
         self._lanca("rms_back", "jt_rms_back", (g, gE, y, yE, cache[0], cache[1], O[0], O[1], M, D, int(math.log2(D)), G, GB),
                     dict(g=g, gE=gE, y=y, yE=yE, r=cache[0], emax=cache[1]), (M, D))
+        return O
+
+    # no reference counterpart: soma(X, rms_back(Gg, Y, cache)) in one launch; launch ids for both parts
+    def rms_back_soma(self, Gg, Y, cache, X):
+        self.reg.confere_bloco("g", Gg); self.reg.confere_bloco("y", Y); self.reg.confere_bloco("x", X)
+        (g, gE), (y, yE), (x, xE) = Gg, Y, X
+        M, D = g.shape
+        self.reg.exige(tuple(x.shape) == (M, D), f"rms_back_soma: x com forma {tuple(x.shape)}, esperado {(M, D)}")
+        G, GB = g_rms(D)
+        O = self._novo_bloco(M, D, g.device)
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        kid = self.reg.registra("rms_back", dict(g=g, gE=gE, y=y, yE=yE, r=cache[0], emax=cache[1]), (M, D))
+        self.reg.registra("soma", dict(x=x, xE=xE), (M, D), tempo=False)
+        r = self.lib.jt_rms_back_soma(*[self._a(t) for t in (g, gE, y, yE, cache[0], cache[1], x, xE, O[0], O[1])], M, D, int(math.log2(D)),
+                                      G, GB, ctypes.c_int(kid))
+        self.reg.depois(kid, r)
         return O
 
     def atencao(self, QKV, Bt, T, H):

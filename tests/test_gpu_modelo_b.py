@@ -26,9 +26,9 @@ def test_passo_config4_vs_oraculo():
     cpu = CS.Gravador(OpsOraculo(32), host)
     mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg)
     mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub())
-    mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = False   # op by op, as the oracle
+    mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.rms_soma = False   # op by op, as the oracle
     mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg)  # batched transposes + fused optimizer
-    assert mf.otimizador_fundido and mf.transpostas_em_lote and mf.dw_em_lote and mf.quant_na_atencao and mf.transposta_na_gemm
+    assert mf.otimizador_fundido and mf.transpostas_em_lote and mf.dw_em_lote and mf.quant_na_atencao and mf.transposta_na_gemm and mf.rms_soma
     for p in range(2):
         x = R.tokens(R.substream(31, f"b4 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
         tok = torch.from_numpy(x[:, :-1].copy()).long()

@@ -185,3 +185,17 @@ def test_gemm_relu2_back_t(M, N, K):
     else:                                                            # transpoe needs R % 128: check against the oracle
         cpu = CPU(blk)
         _compara(Gt, cpu.ops.transpoe(tuple(torch.from_numpy(host(t)) for t in ref)), "transpoe (oracle)")
+
+
+@pytest.mark.parametrize("blk,D", [(32, 512), (128, 256), (32, 1024)])
+def test_rms_back_soma(blk, D):
+    """soma(x, rms_back(g, y, cache)) in one launch equals the two ops."""
+    gpu = GPU(blk, vigiar=True)
+    M = 512
+    s = lambda t: R.substream(93, f"{blk} {D} {t}")
+    X0 = tuple(gpu.dev(v) for v in R.bloco(s("x0"), M, D, blk, espalha=3, e0=-6))
+    G = tuple(gpu.dev(v) for v in R.bloco(s("g"), M, D, blk, espalha=4, e0=-20))
+    X = tuple(gpu.dev(v) for v in R.bloco(s("x"), M, D, blk, espalha=3, e0=-18, zera=0.05))
+    o = gpu.ops
+    Y, cache = o.rms(X0)
+    _compara(o.rms_back_soma(G, Y, cache, X), o.soma(X, o.rms_back(G, Y, cache)), "rms_back_soma")
