@@ -153,14 +153,15 @@ class Modelo:
 
         adiados = []
 
-        def grad_w(n, A, B):        # weight gradient, raw: into the persistent buffer when the optimizer is fused
-            if self.dw_em_lote:
-                adiados.append((n, A, B))
+        def grad_w(n, X, Y):        # weight gradient T(X) . T(Y)^T, raw (into the persistent buffer when the optimizer is fused)
+            if self.dw_em_lote:     # deferred: the transposes and the GEMMs run batched at the end of the backward
+                adiados.append((n, X, Y))
                 return None
+            A, B = T_(X), T_(Y)
             return ops.gemm(A, B, cru=True, saida=gb[n]) if gb else ops.gemm(A, B, cru=True)
         with reg.trecho("backward"):
             with reg.trecho("saida"):
-                grads["out"] = grad_w("out", T_(g), T_(nf))
+                grads["out"] = grad_w("out", g, nf)
                 gx = ops.gemm(g, T_(p["out"]))
                 gx = ops.rms_back(gx, nf, cf)
                 self._st("grad_saida", gx)
@@ -170,13 +171,13 @@ class Modelo:
                 n1, c1, qkv, P, om, n2, c2, h, a = caches[l]
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("mlp"):
-                        grads[f"Wd{l}"] = grad_w(f"Wd{l}", T_(gx), T_(a))
+                        grads[f"Wd{l}"] = grad_w(f"Wd{l}", gx, a)
                         if self.transposta_na_gemm:
                             gh, tgh = ops.gemm_relu2_back_t(gx, T_(p[f"Wd{l}"]), h)
                             prontas[id(gh[0])] = tgh
                         else:
                             gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
-                        grads[f"Wup{l}"] = grad_w(f"Wup{l}", T_(gh), T_(n2))
+                        grads[f"Wup{l}"] = grad_w(f"Wup{l}", gh, n2)
                         gn = ops.gemm(gh, T_(p[f"Wup{l}"]))
                         if r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n2, c2))
@@ -185,13 +186,13 @@ class Modelo:
                             gx = ops.rms_back_soma(gn, n2, c2, gx) if self.rms_soma else ops.soma(gx, ops.rms_back(gn, n2, c2))
                         self._st(f"c{l}.grad_mlp", gh, zeros_normais=True)
                     with reg.trecho("atencao"):
-                        grads[f"Wo{l}"] = grad_w(f"Wo{l}", T_(gx), T_(om))
+                        grads[f"Wo{l}"] = grad_w(f"Wo{l}", gx, om)
                         go = ops.gemm(gx, T_(p[f"Wo{l}"]))
                         if self.quant_na_atencao:
                             gq = ops.atencao_back_q(go, qkv, P, Bt, T, self.H)
                         else:
                             gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
-                        grads[f"Wqkv{l}"] = grad_w(f"Wqkv{l}", T_(gq), T_(n1))
+                        grads[f"Wqkv{l}"] = grad_w(f"Wqkv{l}", gq, n1)
                         gn = ops.gemm(gq, T_(p[f"Wqkv{l}"]))
                         if r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n1, c1))
@@ -201,7 +202,18 @@ class Modelo:
                         self._st(f"c{l}.grad_qkv", gq); self._st(f"c{l}.grad_residuo", gx)
             with reg.trecho("embedding"):
                 um = ops.um_quente(tok, self.V)
-                grads["emb"] = grad_w("emb", T_(um), T_(gx))
+                grads["emb"] = grad_w("emb", um, gx)
+        if adiados and self.transpostas_em_lote:          # every transpose still missing, in one batched launch
+            with reg.trecho("transpostas"):
+                falta, vistos = [], set()
+                for _, X, Y in adiados:
+                    for Z in (X, Y):
+                        if id(Z[0]) not in prontas and id(Z[0]) not in vistos:
+                            vistos.add(id(Z[0]))
+                            falta.append(Z)
+                for Z, Zt in zip(falta, ops.transpoe_lote(falta)):
+                    prontas[id(Z[0])] = Zt
+        adiados = [(n, T_(X), T_(Y)) for n, X, Y in adiados]
         if adiados and self._otim_no_gemm():
             with reg.trecho("gradientes dos pesos + otimizador"):
                 ops.gemm_otim_lote([(A, B, self.mom[n], self.p[n], self.res[n]) for n, A, B in adiados], k_lr, self.error_feedback)
