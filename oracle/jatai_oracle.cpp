@@ -20,6 +20,7 @@
 #include <cstring>
 #include <algorithm>
 #include <vector>
+#include <immintrin.h>
 
 typedef int64_t i64;
 static const i64 E_ZERO = -127;
@@ -91,6 +92,94 @@ static void quant_linhas(const i64* v, const i64* e, i64 R, int C, int blk, MT* 
             quant_bloco<MT>(v + r * C + b * blk, e + r * C + b * blk, blk, m + r * C + b * blk, E + r * nb + b, mbits, lim);
 }
 
+// rnd(x, s) of 8 int32 lanes for 0 <= s and |x| < 2^26: the GEMM's per-block rounding. Every s >= 27 gives 0
+// there, so s is clamped to 30, where x + 2^(s-1) still fits int32.
+static inline __m256i rnd8(__m256i x, __m256i s) {
+    const __m256i um = _mm256_set1_epi32(1), zero = _mm256_setzero_si256();
+    s = _mm256_min_epi32(s, _mm256_set1_epi32(30));
+    __m256i meio = _mm256_srli_epi32(_mm256_sllv_epi32(um, s), 1);          // 2^(s-1), 0 at s = 0
+    __m256i t = _mm256_add_epi32(x, meio);
+    __m256i q = _mm256_srav_epi32(t, s);
+    __m256i resto = _mm256_sub_epi32(t, _mm256_sllv_epi32(q, s));
+    __m256i par = _mm256_and_si256(_mm256_cmpeq_epi32(resto, zero),
+                                   _mm256_and_si256(_mm256_cmpeq_epi32(_mm256_and_si256(q, um), um), _mm256_cmpgt_epi32(s, zero)));
+    return _mm256_add_epi32(q, par);                                           // ties to even: q - 1 where q is odd
+}
+
+// acc[i, j] = sum_q rnd(16 * dot(A_iq, B_jq), (RA_i - ea_iq) + (RB_j - eb_jq)) for an even block size <= 128:
+// the scalar loop of or_gemm, evaluated 4 rows x 16 columns at a time with 16-bit pair products (vpmaddwd).
+static void gemm_acc_avx2(const int8_t* a, const int8_t* ea, const int8_t* b, const int8_t* eb, int M, int N, int K, int blk,
+                          const i64* RA, const i64* RB, i64* acc) {
+    const int nb = K / blk, K2 = K / 2, NT = (N + 15) / 16, MT = (M + 3) / 4, B2 = blk / 2;
+    std::vector<int32_t> Ap((size_t)M * K2);                 // (a[2k], a[2k+1]) as two int16 in one int32
+    std::vector<int16_t> Bp((size_t)NT * K2 * 32);           // tile t, pair k: 16 columns x (b[2k], b[2k+1])
+    std::vector<int32_t> SB((size_t)NT * nb * 16);           // RB_j - eb_jq; padded columns 0
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int k = 0; k < K2; k++)
+            Ap[(size_t)i * K2 + k] = (int32_t)(((uint32_t)(uint16_t)(int16_t)a[(i64)i * K + 2 * k]) |
+                                               ((uint32_t)(uint16_t)(int16_t)a[(i64)i * K + 2 * k + 1] << 16));
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < NT; t++) {
+        for (int k = 0; k < K2; k++)
+            for (int c = 0; c < 16; c++) {
+                int j = t * 16 + c;
+                int16_t* d = &Bp[((size_t)t * K2 + k) * 32 + 2 * c];
+                d[0] = j < N ? b[(i64)j * K + 2 * k] : 0;
+                d[1] = j < N ? b[(i64)j * K + 2 * k + 1] : 0;
+            }
+        for (int q = 0; q < nb; q++)
+            for (int c = 0; c < 16; c++) {
+                int j = t * 16 + c;
+                SB[((size_t)t * nb + q) * 16 + c] = j < N ? (int32_t)(RB[j] - eb[(i64)j * nb + q]) : 0;
+            }
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int u = 0; u < MT; u++) {
+        int rows[4];
+        for (int r = 0; r < 4; r++) rows[r] = std::min(4 * u + r, M - 1);
+        for (int t = 0; t < NT; t++) {
+            __m256i s64[4][4];
+            for (int r = 0; r < 4; r++)
+                for (int h = 0; h < 4; h++) s64[r][h] = _mm256_setzero_si256();
+            for (int q = 0; q < nb; q++) {
+                __m256i p[4][2];
+                for (int r = 0; r < 4; r++) p[r][0] = p[r][1] = _mm256_setzero_si256();
+                const int16_t* bq = &Bp[((size_t)t * K2 + (size_t)q * B2) * 32];
+                const int32_t* aq[4];
+                for (int r = 0; r < 4; r++) aq[r] = &Ap[(size_t)rows[r] * K2 + (size_t)q * B2];
+                for (int k = 0; k < B2; k++) {
+                    __m256i b0 = _mm256_loadu_si256((const __m256i*)(bq + k * 32));
+                    __m256i b1 = _mm256_loadu_si256((const __m256i*)(bq + k * 32 + 16));
+                    for (int r = 0; r < 4; r++) {
+                        __m256i av = _mm256_set1_epi32(aq[r][k]);
+                        p[r][0] = _mm256_add_epi32(p[r][0], _mm256_madd_epi16(av, b0));
+                        p[r][1] = _mm256_add_epi32(p[r][1], _mm256_madd_epi16(av, b1));
+                    }
+                }
+                const int32_t* sb = &SB[((size_t)t * nb + q) * 16];
+                __m256i sb0 = _mm256_loadu_si256((const __m256i*)sb), sb1 = _mm256_loadu_si256((const __m256i*)(sb + 8));
+                for (int r = 0; r < 4; r++) {
+                    __m256i sa = _mm256_set1_epi32((int32_t)(RA[rows[r]] - ea[(i64)rows[r] * nb + q]));
+                    __m256i r0 = rnd8(_mm256_slli_epi32(p[r][0], 4), _mm256_add_epi32(sa, sb0));
+                    __m256i r1 = rnd8(_mm256_slli_epi32(p[r][1], 4), _mm256_add_epi32(sa, sb1));
+                    s64[r][0] = _mm256_add_epi64(s64[r][0], _mm256_cvtepi32_epi64(_mm256_castsi256_si128(r0)));
+                    s64[r][1] = _mm256_add_epi64(s64[r][1], _mm256_cvtepi32_epi64(_mm256_extracti128_si256(r0, 1)));
+                    s64[r][2] = _mm256_add_epi64(s64[r][2], _mm256_cvtepi32_epi64(_mm256_castsi256_si128(r1)));
+                    s64[r][3] = _mm256_add_epi64(s64[r][3], _mm256_cvtepi32_epi64(_mm256_extracti128_si256(r1, 1)));
+                }
+            }
+            for (int r = 0; r < 4; r++) {
+                int i = 4 * u + r;
+                if (i >= M) break;
+                alignas(32) i64 o[16];
+                for (int h = 0; h < 4; h++) _mm256_store_si256((__m256i*)(o + 4 * h), s64[r][h]);
+                for (int c = 0; c < 16 && t * 16 + c < N; c++) acc[(i64)i * N + t * 16 + c] = o[c];
+            }
+        }
+    }
+}
+
 extern "C" {
 
 // ---------------------------------------------------------------- primitives (exposed for the tests)
@@ -115,19 +204,26 @@ void or_gemm(const int8_t* a, const int8_t* ea, const int8_t* b, const int8_t* e
     for (int i = 0; i < M; i++) { i64 r = -1000; for (int q = 0; q < nb; q++) r = std::max<i64>(r, ea[(i64)i * nb + q]); RA[i] = r; }
     for (int j = 0; j < N; j++) { i64 r = -1000; for (int q = 0; q < nb; q++) r = std::max<i64>(r, eb[(i64)j * nb + q]); RB[j] = r; }
     std::vector<i64> acc((i64)M * N), base((i64)M * N);
+    // p = exact int32 dot product of one K-block (|p| <= blk 128^2 <= 2^21), then the spec's per-block rounding
+    if (blk % 2 == 0 && blk <= 128) {
+        gemm_acc_avx2(a, ea, b, eb, M, N, K, blk, RA.data(), RB.data(), acc.data());
+        for (int i = 0; i < M; i++)
+            for (int j = 0; j < N; j++) base[(i64)i * N + j] = RA[i] + RB[j] - 4;
+    } else {
 #pragma omp parallel for schedule(dynamic, 4)
-    for (int i = 0; i < M; i++) {
-        const int8_t* ar = a + (i64)i * K;
-        for (int j = 0; j < N; j++) {
-            const int8_t* br = b + (i64)j * K;
-            i64 s = 0;
-            for (int q = 0; q < nb; q++) {
-                int32_t p = 0;
-                for (int k = 0; k < blk; k++) p += (int32_t)ar[q * blk + k] * (int32_t)br[q * blk + k];
-                s += rnd((i64)p << 4, (RA[i] - ea[(i64)i * nb + q]) + (RB[j] - eb[(i64)j * nb + q]));
+        for (int i = 0; i < M; i++) {
+            const int8_t* ar = a + (i64)i * K;
+            for (int j = 0; j < N; j++) {
+                const int8_t* br = b + (i64)j * K;
+                i64 s = 0;
+                for (int q = 0; q < nb; q++) {
+                    int32_t p = 0;
+                    for (int k = 0; k < blk; k++) p += (int32_t)ar[q * blk + k] * (int32_t)br[q * blk + k];
+                    s += rnd((i64)p << 4, (RA[i] - ea[(i64)i * nb + q]) + (RB[j] - eb[(i64)j * nb + q]));
+                }
+                acc[(i64)i * N + j] = s;
+                base[(i64)i * N + j] = RA[i] + RB[j] - 4;
             }
-            acc[(i64)i * N + j] = s;
-            base[(i64)i * N + j] = RA[i] + RB[j] - 4;
         }
     }
     if (cru) {
@@ -178,11 +274,22 @@ void or_relu2_back(const int8_t* gm, const int8_t* gE, const int8_t* hm, const i
 
 // transpoe: quant(m^T, expande(E)^T) (ops.py:121-123). X [R,C] -> Y [C,R]
 void or_transpoe(const int8_t* xm, const int8_t* xE, int R, int C, int blk, int8_t* ym, int8_t* yE) {
-    const int nbx = C / blk;
-    std::vector<i64> v((i64)R * C), e((i64)R * C);
-    for (int c = 0; c < C; c++)
-        for (int r = 0; r < R; r++) { v[(i64)c * R + r] = xm[(i64)r * C + c]; e[(i64)c * R + r] = xE[(i64)r * nbx + c / blk]; }
-    quant_linhas<int8_t>(v.data(), e.data(), C, R, blk, ym, yE);
+    const int nbx = C / blk, nby = R / blk;
+    // output row c, block b gathers column c of source rows b*blk .. b*blk+blk-1 with their own exponents;
+    // 64 output rows at a time, so each source row contributes one contiguous 64-byte run
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < nby; b++)
+        for (int c0 = 0; c0 < C; c0 += 64) {
+            std::vector<i64> v(blk), e(blk);
+            for (int c = c0; c < std::min(C, c0 + 64); c++) {
+                for (int k = 0; k < blk; k++) {
+                    i64 r = (i64)b * blk + k;
+                    v[k] = xm[r * C + c];
+                    e[k] = xE[r * nbx + c / blk];
+                }
+                quant_bloco<int8_t>(v.data(), e.data(), blk, ym + (i64)c * R + (i64)b * blk, yE + (i64)c * nby + b);
+            }
+        }
 }
 
 // embed: row gather (ops.py:143-145). Returns the number of out-of-vocabulary tokens (their rows are zeroed).

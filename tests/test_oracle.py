@@ -134,6 +134,33 @@ def test_gemm_equal_exponents_is_integer_matmul(blk):
     assert np.all(host(e) == -9 - 5 - 4)
 
 
+@pytest.mark.parametrize("blk", [32, 128])
+def test_gemm_spread_exponents_brute_force(blk):
+    """Ragged shapes (M not a multiple of 4, N not of 16) and exponents spread over the whole int8 range, so
+    alignment shifts run from 0 to past the mantissa width: each raw output equals the sum over K-blocks of the
+    exact rational 16 * dot / 2^shift rounded half to even (Python's round on a Fraction)."""
+    M, N, K = 7, 19, 4 * blk
+    a = R.uniform_int(41, (M, K), -128, 127).astype(np.int8)
+    b = R.uniform_int(42, (N, K), -128, 127).astype(np.int8)
+    ea = R.uniform_int(43, (M, K // blk), -127, 60).astype(np.int8)
+    eb = R.uniform_int(44, (N, K // blk), -127, 60).astype(np.int8)
+    ea[0, :] = -127
+    eb[3, 1] = 60
+    ops = OpsOraculo(blk)
+    acc, e = ops.gemm((torch.from_numpy(a), torch.from_numpy(ea)), (torch.from_numpy(b), torch.from_numpy(eb)), cru=True)
+    acc, e = host(acc).astype(np.int64), host(e).astype(np.int64)
+    RA, RB = ea.astype(np.int64).max(1), eb.astype(np.int64).max(1)
+    for i in range(M):
+        for j in range(N):
+            s = 0
+            for q in range(K // blk):
+                p = int(np.dot(a[i, q * blk:(q + 1) * blk].astype(np.int64), b[j, q * blk:(q + 1) * blk].astype(np.int64)))
+                sh = int(RA[i] - ea[i, q]) + int(RB[j] - eb[j, q])
+                s += round(Fraction(16 * p, 2 ** sh))
+            assert acc[i, j] == s, (i, j)
+            assert e[i, j] == max(RA[i] + RB[j] - 4, -30000)
+
+
 def test_gemm_raw_split_invariance():
     """The raw output over K equals the sum of raw outputs over K halves when RA/RB are held fixed: the spec's
     per-block rounding makes the sum over K-blocks associative (the split-K argument)."""
