@@ -130,6 +130,155 @@ def mede_gemms(O, ops, c, rep=20):
     return out
 
 
+def mede_ops(O, ops, c, reg, rep=20, giga=1 << 30):
+    """the fused element-wise and row ops at M=2048, D=512 (relu2 / relu2_back on [2048, FF],
+    the optimizer on a [512, FF] weight), and the same ops on large inputs rotated over sets totalling at least
+    `giga` bytes, so that the 256 MB last-level cache cannot hold them and HBM serves every byte. Each average is
+    the launches of one hipGraph (captured on the library's stream) timed with HIP events on a side stream.
+    Algorithmic bytes per element, b = 1 + 1/BLK for a block tensor: quant 6+b, soma 3b, relu2 2b, relu2_back 3b,
+    rms 2b+8/D, rms_back 3b+8/D, rms_back+soma 4b+8/D, transpoe 2b, softmax_ce 6+b+12/V, momento 6+2b,
+    peso 5b, otimizador (momento + peso fused) 6+6b. The attention ops are timed at the config-2 shape only
+    (not HBM-bound: their work grows with T^2)."""
+    import torch
+    blk, D, FF, V = c["BLK"], c["D"], c["FF"], c["V"]
+    b = 1 + 1 / blk
+    g = torch.Generator().manual_seed(5)
+
+    def bloco(R, C, e0=-8):
+        m = torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda()
+        E = (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda()
+        return m, E
+
+    def cru(R, C):
+        return (torch.randint(-(1 << 20), 1 << 20, (R, C), generator=g, dtype=torch.int32).cuda(),
+                torch.randint(-20, -10, (R, C), generator=g).to(torch.int16).cuda())
+
+    def f_quant(R, C):
+        x = cru(R, C)
+        return lambda: ops.quant(x)
+
+    def f_soma(R, C):
+        x, y = bloco(R, C), bloco(R, C)
+        return lambda: ops.soma(x, y)
+
+    def f_relu2(R, C):
+        h = bloco(R, C)
+        return lambda: ops.relu2(h)
+
+    def f_relu2_back(R, C):
+        gg, h = bloco(R, C), bloco(R, C)
+        return lambda: ops.relu2_back(gg, h)
+
+    def f_rms(R, C):
+        x = bloco(R, C)
+        return lambda: ops.rms(x)
+
+    def f_rms_back(R, C, soma=False):
+        x = bloco(R, C)
+        y, cache = ops.rms(x)
+        gg = bloco(R, C)
+        if soma:
+            return lambda: ops.rms_back_soma(gg, y, cache, x)
+        return lambda: ops.rms_back(gg, y, cache)
+
+    def f_transpoe(R, C):
+        x = bloco(R, C)
+        return lambda: ops.transpoe(x)
+
+    def f_softmax(R, C):
+        lg = cru(R, C)
+        alvo = torch.randint(0, C, (R,), generator=g).to(torch.int32).cuda()
+        return lambda: ops.softmax_ce(lg, alvo)
+
+    def f_momento(R, C):
+        gc, mom = cru(R, C), bloco(R, C)
+        return lambda: ops.momento(gc, mom)
+
+    def f_peso(R, C):
+        w, mom, r = bloco(R, C), bloco(R, C, -12), bloco(R, C, -20)
+        return lambda: ops.peso(w, mom, r, 4, True)
+
+    def f_otim(R, C):
+        gc, mom, w, r = cru(R, C), bloco(R, C), bloco(R, C, -6), bloco(R, C, -20)
+        tab = ops.tabela_otimizador([(gc, mom, w, r)])
+        return lambda: ops.otimizador(tab, 4, True)
+
+    M = c["Bt"] * c["T"]
+    casos = [  # name, builder, config-2 shape, large shape, algorithmic bytes per element
+        ("quant", f_quant, (M, FF), (16384, 2048), 6 + b),
+        ("soma", f_soma, (M, D), (65536, D), 3 * b),
+        ("relu2", f_relu2, (M, FF), (16384, 2048), 2 * b),
+        ("relu2_back", f_relu2_back, (M, FF), (16384, 2048), 3 * b),
+        ("rms", f_rms, (M, D), (65536, D), 2 * b + 8 / D),
+        ("rms_back", f_rms_back, (M, D), (65536, D), 3 * b + 8 / D),
+        ("rms_back+soma", lambda R, C: f_rms_back(R, C, True), (M, D), (65536, D), 4 * b + 8 / D),
+        ("transpoe", f_transpoe, (M, D), (65536, D), 2 * b),
+        ("softmax_ce", f_softmax, (M, V), (131072, V), 6 + b + 12 / V),
+        ("momento", f_momento, (D, FF), (16384, 2048), 6 + 2 * b),
+        ("peso", f_peso, (D, FF), (16384, 2048), 5 * b),
+        ("otimizador", f_otim, (D, FF), (16384, 2048), 6 + 6 * b),
+    ]
+
+    def tempo(chamadas, vezes):
+        """Average ms per call of `chamadas` captured `vezes` times in one graph."""
+        reg.novo_passo(0)
+        for f in chamadas:
+            f()
+        torch.cuda.synchronize()
+        grafo = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(grafo):
+            ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+            try:
+                for _ in range(vezes):
+                    for f in chamadas:
+                        f()
+            finally:
+                ops.lib.jt_stream(None)
+        grafo.replay()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        with torch.cuda.stream(s):
+            ev[0].record(s)
+            for _ in range(3):
+                grafo.replay()
+            ev[1].record(s)
+        torch.cuda.synchronize()
+        reg.fim_passo()
+        del grafo
+        return ev[0].elapsed_time(ev[1]) / (3 * vezes * len(chamadas))
+
+    out = {}
+    for nome, f, (R, C), (RG, CG), bpe in casos:
+        print(f"bench: op {nome} at {R}x{C}, then {RG}x{CG} rotated", file=sys.stderr, flush=True)
+        ms = tempo([f(R, C)], rep)
+        ent = {"shape": [R, C], "us": round(ms * 1e3, 3), "GB_s": round(bpe * R * C / (ms * 1e-3) / 1e9, 1),
+               "frac_hbm": round(bpe * R * C / (ms * 1e-3) / PEAK_HBM, 4)}
+        conj = max(2, math.ceil(giga / (bpe * RG * CG)))
+        fs = [f(RG, CG) for _ in range(conj)]
+        msg = tempo(fs, 2)
+        ent["large"] = {"shape": [RG, CG], "sets": conj, "us": round(msg * 1e3, 2),
+                        "GB_s": round(bpe * RG * CG / (msg * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(bpe * RG * CG / (msg * 1e-3) / PEAK_HBM, 4)}
+        ent["bytes_per_element"] = round(bpe, 4)
+        out[nome] = ent
+        del fs
+        torch.cuda.empty_cache()
+    # attention at the config-2 shape (Bt 8, T 256, 8 heads x 64)
+    Bt, T, H = c["Bt"], c["T"], c["H"]
+    print(f"bench: attention at Bt={Bt} T={T} H={H}", file=sys.stderr, flush=True)
+    qkv, go = bloco(Bt * T, 3 * D), bloco(Bt * T, D)
+    _, P = ops.atencao(qkv, Bt, T, H)
+    forma = [Bt, T, H, D // H]
+    out["atencao"] = {"shape": forma, "us": round(tempo([lambda: ops.atencao(qkv, Bt, T, H)], rep) * 1e3, 3)}
+    out["atencao_back"] = {"shape": forma, "us": round(tempo([lambda: ops.atencao_back(go, qkv, P, Bt, T, H)], rep) * 1e3, 3)}
+    if ops._q_suportado(T, H, D):      # the variants the fused step runs: block-quantized outputs
+        out["atencao_q"] = {"shape": forma, "us": round(tempo([lambda: ops.atencao_q(qkv, Bt, T, H)], rep) * 1e3, 3)}
+        out["atencao_back_q"] = {"shape": forma,
+                                 "us": round(tempo([lambda: ops.atencao_back_q(go, qkv, P, Bt, T, H)], rep) * 1e3, 3)}
+    return out
+
+
 def trafego_despacha(O, ops, c):
     """Dispatches for the HBM-traffic counter runs: one plain copy of 256 MiB, then every GEMM shape twice (the
     second launch of each is the one summarized), printed in launch order."""
@@ -200,6 +349,84 @@ def cpu_baseline(c, segundos):
     return dict(value=n * bt * c["T"] / dt, unit="tokens/s", cores=threads, kind="port",
                 sample=f"{n} training steps of the same {c['L']}-layer model at Bt={bt} x T={c['T']} on the int64 CPU oracle "
                        f"(oracle/jatai_oracle.cpp, OpenMP {threads} threads), {dt:.1f} s")
+
+
+def cpu_modelo():
+    try:
+        for linha in open("/proc/cpuinfo"):
+            if linha.startswith("model name"):
+                return linha.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_baseline_fp32(c, segundos):
+    """PyTorch float32 on the host cores: the reference's fp32 comparison model (ModeloFloat,
+    treino_int8_gpu/jatai_int8.py:399-428, without its ablation quantization points) at the same shape and batch,
+    initialised from the integer model's seed-0 weights dequantized (m * 2^E), trained with
+    SGD(lr=2^-4, momentum=0.875) as jatai_cuda/treino_cuda.py:153-162. ALiBi slopes and the 1/sqrt(head width)
+    score scale follow the integer attention (slope 2^-floor(8h/H); 1/2 at the reference's head width 4).
+    One warm-up step, then whole steps until `segundos` of wall time (at least two)."""
+    import torch
+    import torch.nn.functional as F
+    from jatai_amd.modelo import inicial
+    V, D, H, FF, L, T, bt = (c[k] for k in ("V", "D", "H", "FF", "L", "T", "Bt"))
+    HD = D // H
+    g = torch.Generator().manual_seed(0)
+    deq = lambda t: (t[0].float() * torch.pow(2.0, t[1][:, :1].float())).contiguous().requires_grad_()
+    w = {"emb": deq(inicial(g, V, D, "cpu", emb=True))}
+    for l in range(L):
+        for n in ("Wq", "Wk", "Wv", "Wo"):
+            w[f"{n}{l}"] = deq(inicial(g, D, D, "cpu"))
+        w[f"Wup{l}"] = deq(inicial(g, FF, D, "cpu"))
+        w[f"Wd{l}"] = deq(inicial(g, D, FF, "cpu"))
+    w["out"] = deq(inicial(g, V, D, "cpu"))
+    pos = torch.arange(T)
+    dist = pos[:, None] - pos[None, :]
+    mascara = dist < 0
+    inclinacao = torch.pow(2.0, -((8 * torch.arange(H)) // H).float())
+    vies = -(dist.clamp(min=0)[None].float() * inclinacao[:, None, None])
+    escala = HD ** -0.5
+
+    def perda(tok, alvo):
+        rms = lambda x: x * torch.rsqrt((x * x).mean(-1, keepdim=True))
+        cab = lambda x: x.reshape(bt, T, H, HD).transpose(1, 2)
+        x = w["emb"][tok]
+        for l in range(L):
+            xn = rms(x)
+            q, k, v = (cab(xn @ w[f"{n}{l}"].t()) for n in ("Wq", "Wk", "Wv"))
+            z = (q @ k.transpose(-1, -2)) * escala + vies
+            a = torch.softmax(z.masked_fill(mascara, float("-inf")), -1)
+            x = x + (a @ v).transpose(1, 2).reshape(bt, T, D) @ w[f"Wo{l}"].t()
+            xn = rms(x)
+            x = x + torch.relu(xn @ w[f"Wup{l}"].t()).square() @ w[f"Wd{l}"].t()
+        logits = rms(x) @ w["out"].t()
+        return F.cross_entropy(logits.reshape(-1, V), alvo.reshape(-1))
+
+    opt = torch.optim.SGD(list(w.values()), lr=2.0 ** -4, momentum=0.875)
+    gen = torch.Generator().manual_seed(11)
+
+    def passo():
+        x = torch.randint(0, V, (bt, T + 1), generator=gen)
+        p = perda(x[:, :-1], x[:, 1:])
+        opt.zero_grad()
+        p.backward()
+        opt.step()
+        return float(p.detach())
+    passo()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ultima = passo()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= segundos and n >= 2:
+            break
+    threads = torch.get_num_threads()
+    return dict(value=n * bt * T / dt, unit="tokens/s", cores=threads, kind="port",
+                sample=f"{n} float32 training steps (forward, backward, SGD) of the same {L}-layer model at "
+                       f"Bt={bt} x T={T} after one warm-up, PyTorch {torch.__version__} on {threads} threads of "
+                       f"{cpu_modelo()}, {dt:.1f} s; last loss {ultima:.4f}")
 
 
 def main():
@@ -276,10 +503,13 @@ def main():
            "gemm_shapes": {k: {"M": v["M"], "N": v["N"], "K": v["K"], "mode": v["modo"], "ms": round(v["ms"], 5),
                                "TOPS": round(v["tops"], 2), "pct_i8_peak": round(100 * v["tops"] * 1e12 / PEAK_I8, 2),
                                "per_step": v["por_passo"], "kernel": v["kernel"]} for k, v in gem.items()},
-           "gemm_ms_per_step_eager_sum": tot_gemm_ms}
+           "gemm_ms_per_step_eager_sum": tot_gemm_ms,
+           "ops_config2": mede_ops(O, ops, c, reg)}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, a.cpu_seconds)
         res["speedup_vs_cpu_baseline"] = tps / res["cpu_baseline"]["value"]
+        res["cpu_baseline_fp32"] = cpu_baseline_fp32(c, a.cpu_seconds)
+        res["speedup_vs_cpu_fp32"] = tps / res["cpu_baseline_fp32"]["value"]
     print(json.dumps(res), flush=True)
 
 

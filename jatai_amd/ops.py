@@ -473,6 +473,7 @@ class OpsHip:
     # no reference counterpart: momento + peso of every tensor in one launch
     def tabela_otimizador(self, itens):
         """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] with fixed addresses (updated in place)."""
+        itens = [tuple(it) for it in itens]
         linhas, inicio = [], 0
         for Gc, Mom, W, R in itens:
             self.reg.confere_cru("grad", Gc)
@@ -485,10 +486,11 @@ class OpsHip:
         self.reg.exige(0 < len(linhas) <= 256, "otimizador: de 1 a 256 tensores")
         self.reg.exige(self.lib.jt_tab_otim_bytes() == 80, "otimizador: tamanho de entrada da tabela inesperado")
         tab = torch.tensor(linhas, dtype=torch.int64).to(W[0].device)
-        return tab, len(linhas), inicio
+        # the table keeps every tensor whose address it holds alive for as long as it exists
+        return tab, len(linhas), inicio, tuple(t for it in itens for x in it for t in x)
 
     def otimizador(self, tabela, k, ef):
-        tab, ntab, nblocos = tabela
+        tab, ntab, nblocos = tabela[:3]
         self._lanca("otimizador", "jt_otimizador", (tab, ntab, nblocos, k, int(ef)), dict(), (nblocos * BLK,), longos=(2,))
 
     def peso(self, W, Mom, R, k, ef):

@@ -199,3 +199,28 @@ def test_rms_back_soma(blk, D):
     o = gpu.ops
     Y, cache = o.rms(X0)
     _compara(o.rms_back_soma(G, Y, cache, X), o.soma(X, o.rms_back(G, Y, cache)), "rms_back_soma")
+
+
+def test_tabela_otimizador_mantem_tensores():
+    """The fused optimizer's device table keeps alive every tensor whose address it holds: built from tensors the
+    caller then drops, with torch's allocator cache emptied (as entering graph capture does), the update still
+    lands in those tensors and equals momento then peso on copies."""
+    import gc
+    blk, D, FF = 32, 512, 2048
+    gpu = GPU(blk)
+    s = lambda t: R.substream(91, t)
+    ins = dict(w=R.bloco(s("w"), D, FF, blk, e0=-9), mom=R.bloco(s("mom"), D, FF, blk, e0=-15),
+               res=R.bloco(s("res"), D, FF, blk, e0=-20, zera=0.3), gw=R.cru(s("gw"), D, FF, bits=28, e0=-50))
+    d = {k: tuple(gpu.dev(v) for v in t) for k, t in ins.items()}
+    w, mom, res = (tuple(t.clone() for t in d[k]) for k in ("w", "mom", "res"))
+    gpu.ops.momento(d["gw"], mom)
+    gpu.ops.peso(w, mom, res, 4, True)
+    esperado = [R.sha(host(t)) for t in (*w, *mom, *res)]
+    tab = gpu.ops.tabela_otimizador([tuple(tuple(t.clone() for t in d[k]) for k in ("gw", "mom", "w", "res"))])
+    gc.collect()
+    torch.cuda.empty_cache()
+    gpu.ops.otimizador(tab, 4, True)
+    torch.cuda.synchronize()
+    assert len(tab[3]) == 8
+    mom2, w2, res2 = tab[3][2:4], tab[3][4:6], tab[3][6:8]
+    assert [R.sha(host(t)) for t in (*w2, *mom2, *res2)] == esperado
