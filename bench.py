@@ -46,6 +46,7 @@ def args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--so-passo", action="store_true", help="time the step only (no GEMM sweep, no CPU baseline): for profiling")
+    ap.add_argument("--so-ops", action="store_true", help="the config-2 op sweep only (one JSON line)")
     ap.add_argument("--trafego", action="store_true",
                     help="for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB device copy (the counters' calibration), "
                          "then each GEMM shape of the step twice in its mode; prints the dispatch order")
@@ -446,6 +447,9 @@ def main():
     ops = O.OpsHip(reg)
     if a.trafego:
         trafego_despacha(O, ops, c)
+        return
+    if a.so_ops:
+        print(json.dumps({"config": c["nome"], "ops_config2": mede_ops(O, ops, c, reg)}), flush=True)
         return
     dev = "cuda"
     m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, dev, ops, reg, r16=c["r16"])

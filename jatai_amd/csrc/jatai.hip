@@ -41,6 +41,8 @@ static bool alinhado(const void* p) { return ((uintptr_t)p & 15) == 0; }
 template <typename... P>
 static bool alinhados(P... p) { return (alinhado(p) && ...); }
 static unsigned grade_elem(long long nblocos) { return (unsigned)((nblocos * g_blk + 2047) / 2048); }
+// kernels with 16 values per lane (soma, relu2, relu2_back, peso)
+static unsigned grade_u(long long nblocos) { return (unsigned)((nblocos * g_blk + 4095) / 4096); }
 static int ilog2(long long n) { int l = 0; while ((2LL << l) <= n) l++; return l; }
 
 // Dynamic LDS above 64 KiB must be allowed per kernel (gfx950 has 160 KiB per CU): raised once per kernel and
@@ -238,7 +240,7 @@ int jt_quant(const void* acc, const void* e, void* m, void* E, long long nblocos
 int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(xm, xE, ym, yE, zm, zE)) return (int)hipErrorInvalidValue;
-#define C(BL) (k_soma<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
+#define C(BL) (k_soma<BL><<<grade_u(nblocos), 256, 0, g_stream>>>((const int8_t*)xm, (const int8_t*)xE, (const int8_t*)ym, (const int8_t*)yE, \
                                                                       (int8_t*)zm, (int8_t*)zE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -247,7 +249,7 @@ int jt_soma(const void* xm, const void* xE, const void* ym, const void* yE, void
 int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(hm, hE, am, aE)) return (int)hipErrorInvalidValue;
-#define C(BL) (k_relu2<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)hm, (const int8_t*)hE, (int8_t*)am, (int8_t*)aE, nblocos, kid), 0)
+#define C(BL) (k_relu2<BL><<<grade_u(nblocos), 256, 0, g_stream>>>((const int8_t*)hm, (const int8_t*)hE, (int8_t*)am, (int8_t*)aE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
     return fim();
@@ -255,7 +257,7 @@ int jt_relu2(const void* hm, const void* hE, void* am, void* aE, long long nbloc
 int jt_relu2_back(const void* gm, const void* gE, const void* hm, const void* hE, void* om, void* oE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(gm, gE, hm, hE, om, oE)) return (int)hipErrorInvalidValue;
-#define C(BL) (k_relu2_back<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)hm, \
+#define C(BL) (k_relu2_back<BL><<<grade_u(nblocos), 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)hm, \
                                                                             (const int8_t*)hE, (int8_t*)om, (int8_t*)oE, nblocos, kid), 0)
     POR_BLK(C);
 #undef C
@@ -272,7 +274,7 @@ int jt_momento(const void* gacc, const void* ge, void* Mm, void* ME, long long n
 int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* RE, int k_lr, int ef, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(Wm, WE, Mm, ME, Rm, RE)) return (int)hipErrorInvalidValue;
-#define C(BL) (k_peso<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((int8_t*)Wm, (int8_t*)WE, (const int8_t*)Mm, (const int8_t*)ME, (int8_t*)Rm, \
+#define C(BL) (k_peso<BL><<<grade_u(nblocos), 256, 0, g_stream>>>((int8_t*)Wm, (int8_t*)WE, (const int8_t*)Mm, (const int8_t*)ME, (int8_t*)Rm, \
                                                                       (int8_t*)RE, k_lr, ef, nblocos, kid), 0)
     POR_BLK(C);
 #undef C

@@ -170,6 +170,53 @@ __device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (
     return zero ? E_ZERO : E;
 }
 
+// x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^30; s < 0 is a left shift the
+// caller knows to be exact): the parameters are computed once, then each value costs a shift, a bit extract, an
+// add and a shift, with no branch. s >= 31 gives 0, as rnd does for s > 30.
+struct Desl {
+    int shl, sr, bias, w1;
+    __device__ __forceinline__ explicit Desl(int s) {
+        shl = min(max(-s, 0), 31);
+        sr = min(max(s, 0), 31);
+        bias = sr ? (1 << (sr - 1)) - 1 : 0;
+        w1 = sr ? 1 : 0;
+    }
+    __device__ __forceinline__ int operator()(int x) const {
+        const int t = (int)((unsigned)x << shl);
+        return (t + bias + (int)__builtin_amdgcn_ubfe((unsigned)t, (unsigned)sr, (unsigned)w1)) >> sr;
+    }
+};
+
+// quant8 for a block whose values all share exponent e and satisfy |v| < 2^30 (the element-wise ops whose
+// inputs are block tensors): the spec's rules (ops.py:58-72) with the per-element work reduced by two facts.
+// topo = e + bitlen(max |v|), because bitlen is monotone in |v|; and half-to-even rounding is monotone and odd,
+// so max |q| = rnd(max |v|, E - e) and the overflow test (any |q| > 127 -> E + 1) is decided on the block
+// maximum before any value is rounded. Each value is then rounded once, and no |q| exceeds 127 (so the
+// saturation clamp of the spec never acts). Returns E (E_ZERO for a zero block; those mantissas are 0).
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
+    int mx = v[0], mn = v[0];
+#pragma unroll
+    for (int i = 1; i < VPL; i++) { mx = max(mx, v[i]); mn = min(mn, v[i]); }
+    const int amax = g_max<LPB>(max(mx, -mn));
+    if (amax >= LIM) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++)
+            if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e);
+    }
+    const int bl = bitlen(amax);
+    const int s = bl - 7 + (int)(bl > 7 && rnd_d(amax, bl - 7) > 127);
+    const int E = e + s;
+    const bool zero = bl == 0 || E < -126;
+    const Desl d(s);
+    // every value is rounded, then masked: a select per value here makes the compiler branch around the rounding
+    const int manter = zero ? 0 : -1;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) q[i] = d(v[i]) & manter;
+    if (!zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
+    return zero ? E_ZERO : E;
+}
+
 // ---------------------------------------------------------------------------------------------- vector I/O
 template <int N>
 __device__ __forceinline__ void le_i8(const int8_t* p, int (&v)[N]) {
@@ -201,6 +248,18 @@ __device__ __forceinline__ void grava_i8(int8_t* p, const int8_t (&m)[N]) {
     if constexpr (N == 4) *reinterpret_cast<int*>(p) = ws[0];
     else if constexpr (N == 8) *reinterpret_cast<int2*>(p) = make_int2(ws[0], ws[1]);
     else *reinterpret_cast<int4*>(p) = make_int4(ws[0], ws[1], ws[2], ws[3]);
+}
+// store N int mantissas known to lie in [-127, 127] as int8
+template <int N>
+__device__ __forceinline__ void grava_q8(int8_t* p, const int (&q)[N]) {
+    static_assert(N == 8 || N == 16, "");
+    unsigned ws[N / 4];
+#pragma unroll
+    for (int j = 0; j < N / 4; j++)
+        ws[j] = ((unsigned)q[4 * j] & 255u) | (((unsigned)q[4 * j + 1] & 255u) << 8) | (((unsigned)q[4 * j + 2] & 255u) << 16) |
+                ((unsigned)q[4 * j + 3] << 24);
+    if constexpr (N == 8) *reinterpret_cast<uint2*>(p) = make_uint2(ws[0], ws[1]);
+    else *reinterpret_cast<uint4*>(p) = make_uint4(ws[0], ws[1], ws[2], ws[3]);
 }
 template <int N>
 __device__ __forceinline__ void le_i32(const int* p, int (&v)[N]) {

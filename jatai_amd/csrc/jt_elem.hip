@@ -27,38 +27,49 @@ __global__ void __launch_bounds__(256) k_quant(const int* __restrict__ acc, cons
     if ((threadIdx.x & (LPB - 1)) == 0) E[w] = (int8_t)Eo;
 }
 
-// z = x + y: ec = max(xE, yE) - 21 (ops.py:128-132)
+// The ops below give every value of a block one exponent (their inputs are block tensors), so they quantize with
+// quant8_u and 16 values per lane (16-byte vectors; a block is LPU = BLK/16 lanes): a few VALU operations per
+// value instead of the generic quant8's per-value exponent work. One 16-value chunk per lane measured fastest on
+// MI355X: several chunks per lane, with all loads issued first or with the next chunk's loads issued before the
+// current chunk is computed, cost more in occupancy than they gained.
+#define VPU 16
+#define ELEM_PROLOGO_U                                                 \
+    constexpr int LPU = BLK / VPU;                                     \
+    const long long o = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * VPU; \
+    const long long w = o / BLK;                                       \
+    if (w >= nblocos) return;
+
+// z = x + y: ec = max(xE, yE) - 21 (ops.py:128-132). Both alignments are exact left shifts or roundings with
+// |x| <= 2^28, so no shift check is needed.
 template <int BLK>
 __global__ void __launch_bounds__(256) k_soma(const int8_t* __restrict__ xm, const int8_t* __restrict__ xE, const int8_t* __restrict__ ym,
                                               const int8_t* __restrict__ yE, int8_t* __restrict__ zm, int8_t* __restrict__ zE,
                                               long long nblocos, int kid) {
-    ELEM_PROLOGO
-    int a[VPL], b[VPL], v[VPL], ee[VPL];
+    ELEM_PROLOGO_U
+    int a[VPU], b[VPU], v[VPU], q[VPU];
     le_i8(xm + o, a);
     le_i8(ym + o, b);
     const int ex = xE[w], ey = yE[w], ec = max(ex, ey) - 21;
+    const Desl da(ec - ex), db(ec - ey);
 #pragma unroll
-    for (int i = 0; i < VPL; i++) { v[i] = rnd(a[i], ec - ex, kid, o + i) + rnd(b[i], ec - ey, kid, o + i); ee[i] = ec; }
-    int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
-    grava_i8(zm + o, q);
-    if ((threadIdx.x & (LPB - 1)) == 0) zE[w] = (int8_t)Eo;
+    for (int i = 0; i < VPU; i++) v[i] = da(a[i]) + db(b[i]);
+    const int Eo = quant8_u<VPU, LPU>(v, ec, q, kid, o);
+    grava_q8(zm + o, q);
+    if ((threadIdx.x & (LPU - 1)) == 0) zE[w] = (int8_t)Eo;
 }
 
 // a = max(h, 0)^2 with exponent 2E (ops.py:134-137)
 template <int BLK>
 __global__ void __launch_bounds__(256) k_relu2(const int8_t* __restrict__ hm, const int8_t* __restrict__ hE, int8_t* __restrict__ am,
                                                int8_t* __restrict__ aE, long long nblocos, int kid) {
-    ELEM_PROLOGO
-    int h[VPL], v[VPL], ee[VPL];
+    ELEM_PROLOGO_U
+    int h[VPU], v[VPU], q[VPU];
     le_i8(hm + o, h);
-    const int e2 = 2 * hE[w];
 #pragma unroll
-    for (int i = 0; i < VPL; i++) { const int r = max(h[i], 0); v[i] = r * r; ee[i] = e2; }
-    int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
-    grava_i8(am + o, q);
-    if ((threadIdx.x & (LPB - 1)) == 0) aE[w] = (int8_t)Eo;
+    for (int i = 0; i < VPU; i++) { const int r = max(h[i], 0); v[i] = r * r; }
+    const int Eo = quant8_u<VPU, LPU>(v, 2 * hE[w], q, kid, o);
+    grava_q8(am + o, q);
+    if ((threadIdx.x & (LPU - 1)) == 0) aE[w] = (int8_t)Eo;
 }
 
 // gh = g * 2 max(h, 0) with exponent gE + hE (ops.py:139-141)
@@ -66,17 +77,15 @@ template <int BLK>
 __global__ void __launch_bounds__(256) k_relu2_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ hm,
                                                     const int8_t* __restrict__ hE, int8_t* __restrict__ om, int8_t* __restrict__ oE,
                                                     long long nblocos, int kid) {
-    ELEM_PROLOGO
-    int g[VPL], h[VPL], v[VPL], ee[VPL];
+    ELEM_PROLOGO_U
+    int g[VPU], h[VPU], v[VPU], q[VPU];
     le_i8(gm + o, g);
     le_i8(hm + o, h);
-    const int es = gE[w] + hE[w];
 #pragma unroll
-    for (int i = 0; i < VPL; i++) { v[i] = g[i] * max(h[i], 0) * 2; ee[i] = es; }
-    int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
-    grava_i8(om + o, q);
-    if ((threadIdx.x & (LPB - 1)) == 0) oE[w] = (int8_t)Eo;
+    for (int i = 0; i < VPU; i++) v[i] = g[i] * max(h[i], 0) * 2;
+    const int Eo = quant8_u<VPU, LPU>(v, gE[w] + hE[w], q, kid, o);
+    grava_q8(om + o, q);
+    if ((threadIdx.x & (LPU - 1)) == 0) oE[w] = (int8_t)Eo;
 }
 
 // momentum, in place: m <- 7/8 m + g with g raw (ops.py:273-278)
@@ -102,38 +111,37 @@ __global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, c
     if ((threadIdx.x & (LPB - 1)) == 0) ME[w] = (int8_t)Eo;
 }
 
-// weight update, in place: W <- W - 2^-k m (+ error-feedback residual R) (ops.py:280-290)
+// weight update, in place: W <- W - 2^-k m (+ error-feedback residual R) (ops.py:280-290). ec is at least
+// (largest exponent + 7) - 27, so each alignment shifts left by at most 20 (|x| < 2^27) or rounds.
 template <int BLK>
 __global__ void __launch_bounds__(256) k_peso(int8_t* __restrict__ Wm, int8_t* __restrict__ WE, const int8_t* __restrict__ Mm,
                                               const int8_t* __restrict__ ME, int8_t* __restrict__ Rm, int8_t* __restrict__ RE, int k_lr,
                                               int ef, long long nblocos, int kid) {
-    ELEM_PROLOGO
-    int wv[VPL], mv[VPL], rv[VPL], alvo[VPL], ee[VPL];
+    ELEM_PROLOGO_U
+    int wv[VPU], mv[VPU], rv[VPU], alvo[VPU], q[VPU];
     le_i8(Wm + o, wv);
     le_i8(Mm + o, mv);
     if (ef) le_i8(Rm + o, rv);
     else
 #pragma unroll
-        for (int i = 0; i < VPL; i++) rv[i] = 0;
+        for (int i = 0; i < VPU; i++) rv[i] = 0;
     const int ew = WE[w], em = ME[w] - k_lr, er = ef ? (int)RE[w] : E_ZERO;
     const int ec = max(max(ew + 7, em + 7), er + 7) - 27;
+    const Desl dw(ec - ew), dm(ec - em), dr(ec - er);
 #pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        alvo[i] = rnd(wv[i], ec - ew, kid, o + i) - rnd(mv[i], ec - em, kid, o + i) + (ef ? rnd(rv[i], ec - er, kid, o + i) : 0);
-        ee[i] = ec;
-    }
-    int8_t q[VPL];
-    const int Ew = quant8<VPL, LPB>(alvo, ee, q, kid, o);
-    grava_i8(Wm + o, q);
-    const bool lider = (threadIdx.x & (LPB - 1)) == 0;
+    for (int i = 0; i < VPU; i++) alvo[i] = dw(wv[i]) - dm(mv[i]) + dr(rv[i]);
+    const int Ew = quant8_u<VPU, LPU>(alvo, ec, q, kid, o);
+    grava_q8(Wm + o, q);
+    const bool lider = (threadIdx.x & (LPU - 1)) == 0;
     if (lider) WE[w] = (int8_t)Ew;
     if (!ef) return;
-    int dif[VPL];
+    // the residual: what the new weight lost, alvo - q 2^(Ew - ec) (a zero mantissa contributes 0)
+    const Desl dq(ec - Ew);
+    int dif[VPU], r[VPU];
 #pragma unroll
-    for (int i = 0; i < VPL; i++) dif[i] = alvo[i] - (q[i] == 0 ? 0 : rnd(q[i], ec - Ew, kid, o + i));
-    int8_t r[VPL];
-    const int Er = quant8<VPL, LPB>(dif, ee, r, kid, o);
-    grava_i8(Rm + o, r);
+    for (int i = 0; i < VPU; i++) dif[i] = alvo[i] - dq(q[i]);
+    const int Er = quant8_u<VPU, LPU>(dif, ec, r, kid, o);
+    grava_q8(Rm + o, r);
     if (lider) RE[w] = (int8_t)Er;
 }
 
