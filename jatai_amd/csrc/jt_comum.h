@@ -71,11 +71,25 @@ __device__ __forceinline__ int exp_int(int d) {
 // exp(-(mx - u)/256) with the difference clamped before subtracting (mx - u may exceed 2^31)
 __device__ __forceinline__ int exp_dif(int mx, int u) { return exp_int(u <= mx - 6000 ? 6000 : mx - u); }
 
-__device__ __forceinline__ int isqrt_i(int n) {     // ops.py:84-89
-    n = max(n, 0);
-    int x = 1 << ((bitlen(n) + 1) / 2);
-    for (int i = 0; i < 10; i++) x = min(x, (x + n / max(x, 1)) >> 1);
-    return max(x, 1);
+// The spec's isqrt (ops.py:84-89: 10 Newton steps from 2^ceil(bitlen(n)/2)) is floor(sqrt(n)) for every
+// 1 <= n < 2^31 (checked over all of them) and 1 for n <= 0. Here: a float square root, within 0.01 of sqrt(n) for
+// these n, whose floor is off by at most one and is corrected by one exact integer step either way.
+__device__ __forceinline__ int isqrt_i(int n) {
+    if (n <= 0) return 1;
+    unsigned r = (unsigned)__builtin_sqrtf((float)n);
+    r -= (unsigned)(r * r > (unsigned)n);
+    r += (unsigned)((r + 1) * (r + 1) <= (unsigned)n);
+    return (int)r;
+}
+
+// floor(a / b) for 0 <= a < 2^30, b >= 1 and a quotient below 2^20: a float estimate (relative error a few
+// 2^-24, so within 1 of the quotient) corrected by one exact integer step either way -- in place of a 32-bit
+// integer division, which costs about 40 VALU instructions.
+__device__ __forceinline__ int div_exata(int a, int b) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+    q -= (int)(q * b > a);
+    q += (int)((q + 1) * b <= a);
+    return q;
 }
 
 __host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2_c(n >> 1); }
@@ -252,13 +266,14 @@ __device__ __forceinline__ void grava_i8(int8_t* p, const int8_t (&m)[N]) {
 // store N int mantissas known to lie in [-127, 127] as int8
 template <int N>
 __device__ __forceinline__ void grava_q8(int8_t* p, const int (&q)[N]) {
-    static_assert(N == 8 || N == 16, "");
+    static_assert(N == 4 || N == 8 || N == 16, "");
     unsigned ws[N / 4];
 #pragma unroll
     for (int j = 0; j < N / 4; j++)
         ws[j] = ((unsigned)q[4 * j] & 255u) | (((unsigned)q[4 * j + 1] & 255u) << 8) | (((unsigned)q[4 * j + 2] & 255u) << 16) |
                 ((unsigned)q[4 * j + 3] << 24);
-    if constexpr (N == 8) *reinterpret_cast<uint2*>(p) = make_uint2(ws[0], ws[1]);
+    if constexpr (N == 4) *reinterpret_cast<unsigned*>(p) = ws[0];
+    else if constexpr (N == 8) *reinterpret_cast<uint2*>(p) = make_uint2(ws[0], ws[1]);
     else *reinterpret_cast<uint4*>(p) = make_uint4(ws[0], ws[1], ws[2], ws[3]);
 }
 template <int N>

@@ -24,13 +24,13 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
     const bool lider = (lr & (LPB - 1)) == 0;
     const int ss = g_sum<LPR>(lider ? rnd(sq << G, 2 * (emax - eb), kid, (long long)row * D) : 0);
     if (ss >= LIM && lr == 0) reporta(E_ACUM, kid, (long long)row * D, ss, -1);
-    const int r = isqrt_i(ss >> log2D), k = bitlen(r) + 10, inv = (1 << k) / r;
-    int v[VPR], ee[VPR];
+    // inv = 2^k / r lies in (2^10, 2^11]: the quotient bound of div_exata holds
+    const int r = isqrt_i(ss >> log2D), k = bitlen(r) + 10, inv = div_exata(1 << k, r);
+    int v[VPR], q[VPR];
 #pragma unroll
-    for (int i = 0; i < VPR; i++) { v[i] = x[i] * inv; ee[i] = eb - k - emax + G / 2; }
-    int8_t q[VPR];
-    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
-    grava_i8(Ym + o, q);
+    for (int i = 0; i < VPR; i++) v[i] = x[i] * inv;            // |v| < 2^18, one exponent per block
+    const int Eo = quant8_u<VPR, LPB>(v, eb - k - emax + G / 2, q, kid, o);
+    grava_q8(Ym + o, q);
     if (lider) YE[(long long)row * nb + b] = (int8_t)Eo;
     if (lr == 0) { cr[row] = r; cemax[row] = emax; }
 }
@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
     const int sh = max(bitlen(S) - 15, 0);
     S = rnd(S, sh, kid, (long long)row * D);
     eS += sh;
-    const int r = cr[row], k = bitlen(r) + 10, inv = (1 << k) / r, emax = cemax[row];
+    const int r = cr[row], k = bitlen(r) + 10, inv = div_exata(1 << k, r), emax = cemax[row];
     const int ec = max(eg + 7, ey + eS + 22) - 28;
     int v[VPR], ee[VPR];
 #pragma unroll
