@@ -41,7 +41,7 @@ static bool alinhado(const void* p) { return ((uintptr_t)p & 15) == 0; }
 template <typename... P>
 static bool alinhados(P... p) { return (alinhado(p) && ...); }
 static unsigned grade_elem(long long nblocos) { return (unsigned)((nblocos * g_blk + 2047) / 2048); }
-// kernels with 16 values per lane (soma, relu2, relu2_back, peso)
+// kernels with 16 values per lane (soma, relu2, relu2_back, peso, otimizador)
 static unsigned grade_u(long long nblocos) { return (unsigned)((nblocos * g_blk + 4095) / 4096); }
 static int ilog2(long long n) { int l = 0; while ((2LL << l) <= n) l++; return l; }
 
@@ -285,7 +285,7 @@ int jt_peso(void* Wm, void* WE, const void* Mm, const void* ME, void* Rm, void* 
 int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid) {
     if (nblocos <= 0 || ntab <= 0 || ntab > 256) return nblocos == 0 ? 0 : (int)hipErrorInvalidValue;
     if (!alinhados(tabela)) return (int)hipErrorInvalidValue;
-#define C(BL) (k_otimizador<BL><<<grade_elem(nblocos), 256, 0, g_stream>>>((const TabOtim*)tabela, ntab, nblocos, k_lr, ef, kid), 0)
+#define C(BL) (k_otimizador<BL><<<grade_u(nblocos), 256, 0, g_stream>>>((const TabOtim*)tabela, ntab, nblocos, k_lr, ef, kid), 0)
     POR_BLK(C);
 #undef C
     return fim();

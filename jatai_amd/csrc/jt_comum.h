@@ -115,46 +115,53 @@ __device__ __forceinline__ int g_or(int v) {
     return v;
 }
 
+// x * 2^-s rounded half to even for a per-value s of either sign (|x| < 2^30; s < 0 a left shift the caller knows
+// to be exact): desloca without a branch -- the same shift, bit extract, add and shift as Desl, with the
+// parameters computed per value.
+__device__ __forceinline__ int desl_var(int x, int s) {
+    const int esq = min(max(-s, 0), 31), sr = min(max(s, 0), 31);
+    const int t = (int)((unsigned)x << esq);
+    const int bias = (int)(((1u << sr) >> 1) - (unsigned)(sr != 0));       // 2^(sr-1) - 1, or 0 at sr = 0
+    return (t + bias + (int)__builtin_amdgcn_ubfe((unsigned)t, (unsigned)sr, (unsigned)min(sr, 1))) >> sr;
+}
+
 // Quantize one block (LPB lanes x VPL values, per-element exponent e) into mantissas of MBITS bits plus one
 // exponent (ops.py:58-72; 16-bit variant jatai_cuda.cu:451-483): topo = max(e + bitlen(v)) over nonzeros,
 // E = topo - MBITS, q = rnd(v, E - e), E += 1 if any |q| > LIMQ, all-zero or E < -126 -> zero block.
 // Returns E (E_ZERO for a zero block). idx0 is the flat index of this lane's first value (for sentinels).
+// Written without per-value branches: e + bitlen(v) <= topo for every nonzero v bounds |v 2^(e - E)| below
+// 2^MBITS, so after the +1 no |q| exceeds LIMQ and the spec's saturation check and clamp never act; a value out
+// of range (|v| >= 2^30) is found from the block's largest |v| and reported, value by value, off the hot path.
 template <int VPL, int LPB, typename MT, int MBITS, int LIMQ>
 __device__ __forceinline__ int quant_grupo(const int (&v)[VPL], const int (&e)[VPL], MT (&m)[VPL], int kid, long long idx0) {
     int topo = SEM_TOPO;
+    unsigned amax = 0;
 #pragma unroll
     for (int i = 0; i < VPL; i++) {
-        if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e[i]);
-        if (v[i] != 0) topo = max(topo, e[i] + bitlen(v[i]));
+        const unsigned a = (unsigned)(v[i] < 0 ? -v[i] : v[i]);
+        amax = max(amax, a);
+        topo = max(topo, a ? e[i] + 32 - (int)__clz((int)a) : SEM_TOPO);
+    }
+    if (amax >= (unsigned)LIM) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++)
+            if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e[i]);
     }
     topo = g_max<LPB>(topo);
-    if (topo == SEM_TOPO) {
+    int E = topo - MBITS, q[VPL], qmax = 0;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) m[i] = 0;
-        return E_ZERO;
-    }
-    // E - e >= bitlen(v) - MBITS for every nonzero v, so a left shift here keeps |q| < 2^MBITS: no bit is lost and
-    // the shift needs no check (zeros shift to zero)
-    int E = topo - MBITS, q[VPL], est = 0;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) { q[i] = desloca(v[i], E - e[i]); est |= q[i] > LIMQ || q[i] < -LIMQ; }
-    if (g_or<LPB>(est)) {
+    for (int i = 0; i < VPL; i++) { q[i] = desl_var(v[i], E - e[i]); qmax = max(qmax, q[i] < 0 ? -q[i] : q[i]); }
+    if (g_max<LPB>(qmax) > LIMQ) {
         E += 1;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) q[i] = desloca(v[i], E - e[i]);
+        for (int i = 0; i < VPL; i++) q[i] = desl_var(v[i], E - e[i]);
     }
-    if (E < -126) {
+    const bool zero = topo == SEM_TOPO || E < -126;
+    const int manter = zero ? 0 : -1;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) m[i] = 0;
-        return E_ZERO;
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        if (q[i] > LIMQ || q[i] < -LIMQ) reporta(E_SAT, kid, idx0 + i, q[i], E);
-        m[i] = (MT)max(-LIMQ, min(LIMQ, q[i]));
-    }
-    if (E > 126) reporta(E_EXP, kid, idx0, E, topo);
-    return E;
+    for (int i = 0; i < VPL; i++) m[i] = (MT)(q[i] & manter);
+    if (!zero && E > 126) reporta(E_EXP, kid, idx0, E, topo);
+    return zero ? E_ZERO : E;
 }
 template <int VPL, int LPB>
 __device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], int8_t (&m)[VPL], int kid, long long idx0) {

@@ -98,12 +98,19 @@ __global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, c
     le_i32(gacc + o, g);
     le_i16(ge + o, eg);
     const int em = ME[w] - 3;
+    unsigned gmax = 0;
 #pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
-        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
-        v[i] = rnd(mm[i] * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
+    for (int i = 0; i < VPL; i++) {                // shifts keep |x| < 2^28 (see otim_valores): no check can fire
+        const unsigned a = (unsigned)(g[i] < 0 ? -g[i] : g[i]);
+        gmax = max(gmax, a);
+        const int ec = max(em + 10, eg[i] + 32 - (int)__clz((int)a)) - 28;
+        v[i] = desl_var(mm[i] * 7, ec - em) + desl_var(g[i], ec - eg[i]);
         ee[i] = ec;
+    }
+    if (gmax >= (unsigned)LIM) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++)
+            if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[VPL];
     const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
@@ -298,60 +305,73 @@ __device__ __forceinline__ OtimEnt<NV> otim_le(const Otim& d, long long o, long 
     x.re = ef ? (int)d.RE[w] : E_ZERO;
     return x;
 }
+// Every shift below keeps |x| < 2^28 (the momentum terms by ec >= bitlen - 28 per value, the weight terms by
+// ec >= largest exponent + 7 - 27), so none of the spec's left-shift checks can fire and the shifts run without
+// branches (desl_var per value, Desl per block); a gradient value out of range is still reported.
 template <int NV, int NL>
 __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)[NV], const OtimEnt<NV>& x, const Otim& d, long long o, long long w,
                                              bool lider, int k_lr, int ef, int kid) {
     int v[NV], ee[NV];
     const int em = x.me - 3;
+    unsigned gmax = 0;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
-        const int ec = max(em + 10, eg[i] + bitlen(g[i])) - 28;
-        v[i] = rnd(x.m(i) * 7, ec - em, kid, o + i) + rnd(g[i], ec - eg[i], kid, o + i);
+        const unsigned a = (unsigned)(g[i] < 0 ? -g[i] : g[i]);
+        gmax = max(gmax, a);
+        const int ec = max(em + 10, eg[i] + 32 - (int)__clz((int)a)) - 28;          // eg + bitlen(g)
+        v[i] = desl_var(x.m(i) * 7, ec - em) + desl_var(g[i], ec - eg[i]);
         ee[i] = ec;
+    }
+    if (gmax >= (unsigned)LIM) {
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[NV];
     const int Em = quant8<NV, NL>(v, ee, q, kid, o);
     grava_i8(d.Mm + o, q);
     if (lider) d.ME[w] = (int8_t)Em;
-    // peso with the new momentum
-    int alvo[NV];
+    // peso with the new momentum: one exponent per block from here on
     const int ew = x.we, emk = Em - k_lr, er = x.re;
     const int ec = max(max(ew + 7, emk + 7), er + 7) - 27;
+    const Desl dw(ec - ew), dm(ec - emk), dr(ec - er);
+    int alvo[NV], qw[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        alvo[i] = rnd(x.w(i), ec - ew, kid, o + i) - rnd(q[i], ec - emk, kid, o + i) + (ef ? rnd(x.r(i), ec - er, kid, o + i) : 0);
-        ee[i] = ec;
-    }
-    int8_t qw[NV];
-    const int Ew = quant8<NV, NL>(alvo, ee, qw, kid, o);
-    grava_i8(d.Wm + o, qw);
+    for (int i = 0; i < NV; i++) alvo[i] = dw(x.w(i)) - dm(q[i]) + dr(x.r(i));
+    const int Ew = quant8_u<NV, NL>(alvo, ec, qw, kid, o);
+    grava_q8(d.Wm + o, qw);
     if (lider) d.WE[w] = (int8_t)Ew;
     if (!ef) return;
-    int dif[NV];
+    // the residual: what the new weight lost, alvo - qw 2^(Ew - ec) (a zero mantissa contributes 0)
+    const Desl dq(ec - Ew);
+    int dif[NV], r[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++) dif[i] = alvo[i] - (qw[i] == 0 ? 0 : rnd(qw[i], ec - Ew, kid, o + i));
-    int8_t r[NV];
-    const int Er = quant8<NV, NL>(dif, ee, r, kid, o);
-    grava_i8(d.Rm + o, r);
+    for (int i = 0; i < NV; i++) dif[i] = alvo[i] - dq(qw[i]);
+    const int Er = quant8_u<NV, NL>(dif, ec, r, kid, o);
+    grava_q8(d.Rm + o, r);
     if (lider) d.RE[w] = (int8_t)Er;
 }
 
+// 16 values per lane; each workgroup finds the table entry of each lane's block by a binary search over the
+// entries' first blocks staged in LDS (the table is at most 256 entries)
 template <int BLK>
 __global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ tab, int ntab, long long nblocos, int k_lr, int ef, int kid) {
-    constexpr int LPB = BLK / VPL;
-    const long long og = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * VPL;
+    constexpr int NVO = 16, LPB = BLK / NVO;
+    __shared__ long long ini[256];
+    for (int i = threadIdx.x; i < ntab; i += blockDim.x) ini[i] = tab[i].inicio;
+    __syncthreads();
+    const long long og = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * NVO;
     const long long wg = og / BLK;
     if (wg >= nblocos) return;
     int t = 0;                                                      // table entry holding global block wg (entries sorted)
     for (int s = 128; s; s >>= 1)
-        if (t + s < ntab && tab[t + s].inicio <= wg) t += s;
+        if (t + s < ntab && ini[t + s] <= wg) t += s;
     const TabOtim d = tab[t];
     const long long w = wg - d.inicio, o = w * BLK + (og % BLK);
     const Otim ot{d.Mm, d.ME, d.Wm, d.WE, d.Rm, d.RE};
-    const OtimEnt<VPL> x = otim_le<VPL>(ot, o, w, ef);
-    int g[VPL], eg[VPL];
+    const OtimEnt<NVO> x = otim_le<NVO>(ot, o, w, ef);
+    int g[NVO], eg[NVO];
     le_i32(d.gacc + o, g);
     le_i16(d.ge + o, eg);
-    otim_valores<VPL, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid);
+    otim_valores<NVO, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid);
 }

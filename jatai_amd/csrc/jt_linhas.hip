@@ -37,6 +37,9 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
 
 // RMSNorm backward: dx = (g - y * mean(g y)) / rms in the spec's integer steps (ops.py:167-184). SOMA: the output
 // is soma(x, dx) instead (ops.py:128-132, x given by xm, xE), as the backward's residual update uses it.
+// The block-uniform alignments run through Desl: |g y| << GB < 2^21 shifts right, g shifts left by at most 21
+// (ec >= eg + 7 - 28) and y S by at most 6 (|S| <= 2^15, ec >= ey + eS + 22 - 28), so every value stays below 2^28
+// and the spec's left-shift checks cannot fire. Every load (x included) is issued before the first reduction.
 template <int VPR, int LPR, int BLK, bool SOMA = false>
 __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ ym,
                                                   const int8_t* __restrict__ yE, const int* __restrict__ cr, const int* __restrict__ cemax,
@@ -46,41 +49,51 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
     if (row >= M) return;
     const long long o = (long long)row * D + lr * VPR;
-    int g[VPR], y[VPR];
+    const int b = lr / LPB;
+    int g[VPR], y[VPR], a[VPR];
     le_i8(gm + o, g);
     le_i8(ym + o, y);
-    const int b = lr / LPB, eg = gE[(long long)row * nb + b], ey = yE[(long long)row * nb + b];
+    const int eg = gE[(long long)row * nb + b], ey = yE[(long long)row * nb + b];
+    const int r = cr[row], emax = cemax[row];
+    int ex = 0;
+    if constexpr (SOMA) {
+        le_i8(xm + o, a);
+        ex = xE[(long long)row * nb + b];
+    }
     const int smax = g_max<LPR>(eg + ey);
+    const Desl d1(smax - (eg + ey));
     int S = 0;
 #pragma unroll
-    for (int i = 0; i < VPR; i++) S += rnd((g[i] * y[i]) << GB, smax - (eg + ey), kid, (long long)row * D);
+    for (int i = 0; i < VPR; i++) S += d1((g[i] * y[i]) << GB);
     S = g_sum<LPR>(S);
     if ((S >= LIM || S <= -LIM) && lr == 0) reporta(E_ACUM, kid, (long long)row * D, S, -2);
     int eS = smax - GB - log2D;
     const int sh = max(bitlen(S) - 15, 0);
-    S = rnd(S, sh, kid, (long long)row * D);
+    S = rnd_d(S, sh);
     eS += sh;
-    const int r = cr[row], k = bitlen(r) + 10, inv = div_exata(1 << k, r), emax = cemax[row];
+    const int k = bitlen(r) + 10, inv = div_exata(1 << k, r);          // 2^k / r in (2^10, 2^11]
     const int ec = max(eg + 7, ey + eS + 22) - 28;
+    const Desl dg(ec - eg), dy(ec - (ey + eS));
     int v[VPR], ee[VPR];
 #pragma unroll
     for (int i = 0; i < VPR; i++) {
-        int dentro = rnd(g[i], ec - eg, kid, o + i) - rnd(y[i] * S, ec - (ey + eS), kid, o + i);
-        const int sh2 = max(bitlen(dentro) - 18, 0);
-        dentro = rnd(dentro, sh2, kid, o + i);
+        int dentro = dg(g[i]) - dy(y[i] * S);
+        const unsigned ad = (unsigned)(dentro < 0 ? -dentro : dentro);
+        const int sh2 = max(32 - (int)__clz((int)ad) - 18, 0);     // bitlen(dentro) - 18
+        dentro = desl_var(dentro, sh2);
         v[i] = dentro * inv;
         ee[i] = ec + sh2 - k - (emax - G / 2);
     }
     int8_t q[VPR];
     const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
     if constexpr (SOMA) {                                            // z = soma(x, dx): ec = max(xE, E) - 21
-        int a[VPR], zs[VPR];
-        le_i8(xm + o, a);
-        const int ex = xE[(long long)row * nb + b], ec = max(ex, Eo) - 21;
+        const int ec2 = max(ex, Eo) - 21;
+        const Desl da(ec2 - ex), dq(ec2 - Eo);
+        int zs[VPR], qz[VPR];
 #pragma unroll
-        for (int i = 0; i < VPR; i++) { zs[i] = rnd(a[i], ec - ex, kid2, o + i) + rnd((int)q[i], ec - Eo, kid2, o + i); ee[i] = ec; }
-        const int Ez = quant8<VPR, LPB>(zs, ee, q, kid2, o);
-        grava_i8(om + o, q);
+        for (int i = 0; i < VPR; i++) zs[i] = da(a[i]) + dq((int)q[i]);
+        const int Ez = quant8_u<VPR, LPB>(zs, ec2, qz, kid2, o);
+        grava_q8(om + o, qz);
         if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Ez;
         return;
     }
