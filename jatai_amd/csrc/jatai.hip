@@ -69,6 +69,10 @@ static void lds_max(K* k, size_t lds) {
 // hide LDS and MFMA latency under the VALU rounding work, as long as the grid does not already fill the chip
 // (1024 = 256 CUs x 4 SIMDs). (Each K-split holds three stage buffers in LDS -- 10 KiB each at BLK=32, 21 KiB at
 // BLK=128, 160 KiB per workgroup -- and the fused epilogues of modes 2-4 would spill at 1024 threads.)
+// K up to 65536; past 4096 (one chunk of shift tables) the exponent rows are read with 16-byte loads, so the
+// number of K-blocks must be a multiple of 16
+static bool k_ok(int K) { return K <= 4096 || (K <= 65536 && (K / g_blk) % 16 == 0); }
+
 static int gemm_divisoes(int M, int N, int K, int modo) {
     const long long tiles = (long long)(M / gemm::BM) * (N / gemm::BN);
     const int nb = K / g_blk, ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
@@ -113,7 +117,7 @@ int jt_gemm_divisoes(int M, int N, int K, int modo) { return gemm_divisoes(M, N,
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
               const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
     using namespace gemm;
-    if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || K > 4096 || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || !k_ok(K) || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk;
     // mode 4 with Om2: the transposed copy needs a single K-split (BLK = 32 only)
@@ -162,7 +166,7 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
         long long tot = 0;
         for (int i = 0; i < L.n; i++) {
             const EntradaG& x = e[base + i];
-            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || x.K > 4096 || x.K <= 0) return (int)hipErrorInvalidValue;
+            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || !k_ok(x.K) || x.K <= 0) return (int)hipErrorInvalidValue;
             if (!alinhados(x.A, x.EA, x.B, x.EB, x.C32, x.Ce)) return (int)hipErrorInvalidValue;
             L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
             L.C32[i] = (int*)x.C32; L.Ce[i] = (int16_t*)x.Ce; L.M[i] = x.M; L.N[i] = x.N; L.ini[i] = (int)tot;
@@ -203,7 +207,7 @@ int jt_gemm_otim_lote(const void* entradas, int n, int k_lr, int ef, int kid) {
         long long tot = 0;
         for (int i = 0; i < L.n; i++) {
             const EntradaGO& x = e[base + i];
-            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || x.K > 4096 || x.K <= 0) return (int)hipErrorInvalidValue;
+            if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || !k_ok(x.K) || x.K <= 0) return (int)hipErrorInvalidValue;
             if (!alinhados(x.A, x.EA, x.B, x.EB, x.Mm, x.ME, x.Wm, x.WE) || !alinhados(x.Rm, x.RE)) return (int)hipErrorInvalidValue;
             L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
             L.ot[i] = Otim{(int8_t*)x.Mm, (int8_t*)x.ME, (int8_t*)x.Wm, (int8_t*)x.WE, (int8_t*)x.Rm, (int8_t*)x.RE};

@@ -92,6 +92,11 @@ __device__ __forceinline__ int div_exata(int a, int b) {
     return q;
 }
 
+// largest of the four signed bytes of w
+__device__ __forceinline__ int max_i8x4(int w) {
+    return max(max((int)(int8_t)w, (int)(int8_t)(w >> 8)), max((int)(int8_t)(w >> 16), w >> 24));
+}
+
 __host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2_c(n >> 1); }
 
 // ---------------------------------------------------------------------------------------------- lane groups

@@ -55,16 +55,20 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     const int nb = K / BLK, ns = (K + SK - 1) / SK;
     constexpr int BPS = SK / BLK;                                   // blocks per stage
     constexpr int KST = BLK / 32;                                   // MFMA k-steps per block
+    // The shift tables hold at most NBC K-blocks (4096 values of K); a longer K runs in chunks of NBC blocks,
+    // each with its own tables (the row maxima RA, RB are over all of K).
+    constexpr int NBC = 4096 / BLK;
+    const int nbt = min(nb, NBC), nch = (nb + NBC - 1) / NBC;
     // LDS: RA [BM], RB [BN] int32 (live to the end); shift terms na[b][i] = ea_ib + 4 - RA_i (int32) and
-    // nb[b][j] = eb_jb - RB_j (int8), clamped at -100 (n = na + nb <= -22 scales |p| < 2^21 below 1/2, i.e. to
-    // 0, as rnd(., s >= 26) does); then the stage buffers [KS][2][STAGE], which first hold the raw exponent
-    // bytes and at the end the KS accumulator tiles.
+    // nb[b][j] = eb_jb - RB_j (int8) of the chunk's blocks, clamped at -100 (n = na + nb <= -22 scales |p| < 2^21
+    // below 1/2, i.e. to 0, as rnd(., s >= 26) does); then the stage buffers [KS][2][STAGE], which first hold the
+    // chunk's raw exponent bytes and at the end the KS accumulator tiles.
     int* ra_s = reinterpret_cast<int*>(smem);
     int* rb_s = ra_s + BM;
     int* na_s = rb_s + BN;
-    int8_t* nb_s = reinterpret_cast<int8_t*>(na_s + (size_t)nb * BM);
-    char* buf = reinterpret_cast<char*>(nb_s) + (((size_t)nb * BN + 15) & ~(size_t)15);
-    int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nb], EB rows [BN][nb]
+    int8_t* nb_s = reinterpret_cast<int8_t*>(na_s + (size_t)nbt * BM);
+    char* buf = reinterpret_cast<char*>(nb_s) + (((size_t)nbt * BN + 15) & ~(size_t)15);
+    int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nbc], EB rows [BN][nbc]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
     const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
@@ -105,57 +109,81 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             }
         }
     };
-    if (g < ns) busca(g, reg);                                      // first stage in flight during the exponent staging
-    if (g + KS < ns) busca(g + KS, reg2);                           // and the second
-
     // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
     const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
     const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
     const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
-    // exponents of the tile's 32 rows of A and 128 rows of B: two contiguous spans (32 nb and 128 nb bytes,
-    // multiples of 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span
-    // re-read its last vector and store it to a junk slot after the span, so neither side branches
-    {
-        const int nva = 2 * nb, nvt = 10 * nb;
-        const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
-        const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
-        for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
-            int4 t[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int v = min(v0 + k * 256 * KS, nvt - 1);
-                t[k] = v < nva ? ga[v] : gb[v - nva];
+    // Several chunks: RA and RB first, by one pass over the exponent rows in global memory (rows of nb bytes, nb a
+    // multiple of 16 there: 16-byte loads). One chunk: from the staged exponents, below.
+    if (nch > 1) {
+        const int8_t* er = tid < BM ? EA + (size_t)(row0 + tid) * nb
+                                    : (tid >= 64 && tid < 64 + BN) ? EB + (size_t)(col0 + tid - 64) * nb : nullptr;
+        if (er) {
+            int m = -128;
+            for (int v = 0; v < nb / 16; v++) {
+                const int4 t = reinterpret_cast<const int4*>(er)[v];
+                m = max(m, max(max(max_i8x4(t.x), max_i8x4(t.y)), max(max_i8x4(t.z), max_i8x4(t.w))));
             }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int v = min(v0 + k * 256 * KS, nvt);
-                *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
-            }
+            if (tid < BM) ra_s[tid] = m;
+            else rb_s[tid - 64] = m;
         }
     }
-    __syncthreads();
-    if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
-    else if (tid >= 64 && tid < 64 + BN) {
-        const int c = tid - 64;
-        int m = -128;
-        for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
-        rb_s[c] = m;
-    }
-    __syncthreads();
-    for (int i = tid; i < BM * nb; i += 256 * KS) {                 // i = b * BM + r
-        const int r = i & (BM - 1), b = i >> 5;
-        na_s[i] = max((int)st_s[r * nb + b] + 4 - ra_s[r], -100);
-    }
-    for (int i = tid; i < BN * nb; i += 256 * KS) {                 // i = b * BN + c
-        const int c = i & (BN - 1), b = i >> 7;
-        nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nb + b] - rb_s[c], -100);
-    }
-    __syncthreads();                                                // staging bytes consumed: buffers are free
-    if (g < ns) guarda(0, reg);
-    __syncthreads();
+    // one chunk's exponents and shift tables (blocks b0 .. b0 + nbc - 1); the stage buffers must be free
+    auto tabelas = [&](int b0, int nbc) {
+        if (nch == 1) {
+            // the tile's 32 rows of A and 128 rows of B: two contiguous spans (32 nb and 128 nb bytes, multiples of
+            // 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span re-read its last
+            // vector and store it to a junk slot after the span, so neither side branches
+            const int nva = 2 * nb, nvt = 10 * nb;
+            const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
+            const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
+            for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
+                int4 t[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int v = min(v0 + k * 256 * KS, nvt - 1);
+                    t[k] = v < nva ? ga[v] : gb[v - nva];
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int v = min(v0 + k * 256 * KS, nvt);
+                    *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
+                }
+            }
+        } else {
+            // 160 row segments of nbc bytes (a multiple of 16) at column b0 of rows of nb bytes
+            const int vpr = nbc / 16;
+            for (int v = tid; v < (BM + BN) * vpr; v += 256 * KS) {
+                const int r = v / vpr, k = v - r * vpr;
+                const int8_t* e = r < BM ? EA + (size_t)(row0 + r) * nb : EB + (size_t)(col0 + r - BM) * nb;
+                *reinterpret_cast<int4*>(st_s + (size_t)r * nbc + 16 * k) = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
+            }
+        }
+        __syncthreads();
+        if (nch == 1) {
+            if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
+            else if (tid >= 64 && tid < 64 + BN) {
+                const int c = tid - 64;
+                int m = -128;
+                for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
+                rb_s[c] = m;
+            }
+            __syncthreads();
+        }
+        for (int i = tid; i < BM * nbc; i += 256 * KS) {            // i = b * BM + r
+            const int r = i & (BM - 1), b = i >> 5;
+            na_s[i] = max((int)st_s[r * nbc + b] + 4 - ra_s[r], -100);
+        }
+        for (int i = tid; i < BN * nbc; i += 256 * KS) {            // i = b * BN + c
+            const int c = i & (BN - 1), b = i >> 7;
+            nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nbc + b] - rb_s[c], -100);
+        }
+        __syncthreads();                                            // staging bytes consumed: buffers are free
+    };
+    int b0 = 0;                                                     // first K-block of the current chunk
 
     int acc[2][2][4] = {};
-    // stage k of this group (k = 0, 1, ...) is stage g + k KS, held in buffer k % 3. In iteration k the loads of
+    // stage k of this group in a chunk (k = 0, 1, ...) is stage gs + k KS, held in buffer k % 3. In iteration k the loads of
     // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored.
     // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
     // LDS latency of block bl + 1 runs under the VALU work of block bl. Modes 3 and 4 (larger epilogues) go block
@@ -182,9 +210,10 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
     };
     auto arredonda = [&](int b, const v4i (&p)[2][2]) {
-        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
-        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
-        const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
+        const int bt = b - b0;                                      // block index in the chunk's tables
+        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 4 * lg);
+        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 16 + 4 * lg);
+        const int nb0 = nb_s[bt * BN + wc + lr], nb1 = nb_s[bt * BN + wc + 16 + lr];
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
 #pragma unroll
@@ -198,12 +227,13 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // BLK=32, two blocks in the stage: the two rounded products are added in fp32 before the conversion; each is
     // an integer below 2^23 in magnitude (|p| <= 32 * 128 * 128 = 2^19, scale <= 2^4), so the sum is exact
     auto arredonda2 = [&](int b, const v4i (&p)[2][2], const v4i (&q)[2][2]) {
-        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + b * BM + 4 * lg);
-        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + b * BM + 16 + 4 * lg);
-        const int nb0 = nb_s[b * BN + wc + lr], nb1 = nb_s[b * BN + wc + 16 + lr];
-        const v4i ma0 = *reinterpret_cast<const v4i*>(na_s + (b + 1) * BM + 4 * lg);
-        const v4i ma1 = *reinterpret_cast<const v4i*>(na_s + (b + 1) * BM + 16 + 4 * lg);
-        const int mb0 = nb_s[(b + 1) * BN + wc + lr], mb1 = nb_s[(b + 1) * BN + wc + 16 + lr];
+        const int bt = b - b0;                                      // block index in the chunk's tables
+        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 4 * lg);
+        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 16 + 4 * lg);
+        const int nb0 = nb_s[bt * BN + wc + lr], nb1 = nb_s[bt * BN + wc + 16 + lr];
+        const v4i ma0 = *reinterpret_cast<const v4i*>(na_s + (bt + 1) * BM + 4 * lg);
+        const v4i ma1 = *reinterpret_cast<const v4i*>(na_s + (bt + 1) * BM + 16 + 4 * lg);
+        const int mb0 = nb_s[(bt + 1) * BN + wc + lr], mb1 = nb_s[(bt + 1) * BN + wc + 16 + lr];
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
 #pragma unroll
@@ -241,22 +271,47 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             }
         }
     };
-    const int nk = g < ns ? (ns - g + KS - 1) / KS : 0;            // stages of this group
-    for (int k = 0; k < nk; k += 2) {
-        // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
-        if (k + 2 < nk) busca(g + (k + 2) * KS, reg);
-        calcula(meu + (k % 3) * STAGE, g + k * KS);
-        if (k + 1 < nk) guarda((k + 1) % 3, reg2);
+    for (int c = 0; c < nch; c++) {
+        b0 = c * NBC;
+        const int nbc = min(NBC, nb - b0);
+        const int s0 = b0 / BPS, s1 = min(ns, (b0 + nbc + BPS - 1) / BPS);   // the chunk's stages
+        const int gs = s0 + g;                                      // this group's first stage
+        if (gs < s1) busca(gs, reg);                                // first stage in flight during the exponent staging
+        if (gs + KS < s1) busca(gs + KS, reg2);                     // and the second
+        tabelas(b0, nbc);
+        if (gs < s1) guarda(0, reg);
         __syncthreads();
-        if (k + 1 >= nk) break;
-        // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
-        if (k + 3 < nk) busca(g + (k + 3) * KS, reg2);
-        calcula(meu + ((k + 1) % 3) * STAGE, g + (k + 1) * KS);
-        if (k + 2 < nk) guarda((k + 2) % 3, reg);
-        __syncthreads();
+        const int nk = gs < s1 ? (s1 - gs + KS - 1) / KS : 0;       // stages of this group in the chunk
+        for (int k = 0; k < nk; k += 2) {
+            // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
+            if (k + 2 < nk) busca(gs + (k + 2) * KS, reg);
+            calcula(meu + (k % 3) * STAGE, gs + k * KS);
+            if (k + 1 < nk) guarda((k + 1) % 3, reg2);
+            __syncthreads();
+            if (k + 1 >= nk) break;
+            // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
+            if (k + 3 < nk) busca(gs + (k + 3) * KS, reg2);
+            calcula(meu + ((k + 1) % 3) * STAGE, gs + (k + 1) * KS);
+            if (k + 2 < nk) guarda((k + 2) % 3, reg);
+            __syncthreads();
+        }
+        // groups with fewer stages still take part in every barrier of the loop above
+        for (int k = nk; k < (s1 - s0 + KS - 1) / KS; k++) __syncthreads();
+        // Past 4096 values of K the int32 accumulator has no a-priori bound: each chunk adds less than 2^30
+        // (NBC blocks of |rnd(p << 4, s)| < 2^23), so a partial sum kept below 2^30 / KS at every chunk end can
+        // neither wrap inside the chunk nor in the sum of the KS partials; one that is not is reported.
+        if (nch > 1) {
+            constexpr int T = LIM / KS;
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (acc[ti][tj][i] >= T || acc[ti][tj][i] <= -T)
+                            reporta(E_ACUM, kid, (long long)(row0 + 16 * ti + 4 * lg + i) * N + col0 + wc + 16 * tj + lr, acc[ti][tj][i], -3);
+        }
     }
-    // groups with fewer stages still take part in every barrier of the loop above
-    for (int k = nk; k < (ns + KS - 1) / KS; k++) __syncthreads();
 
     // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout. The X operand
     // of modes 2 and 4 is read here, not before the K loop, so its 16 registers do not cost a resident wave.
@@ -447,6 +502,7 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
 // dynamic LDS bytes for nb K-blocks and KS K-splits
 static inline size_t gemm_lds(int nb, int ks, int blk) {
     using namespace gemm;
+    nb = std::min(nb, 4096 / blk);                                  // the shift tables hold one chunk of K
     const size_t fixo = (size_t)(BM + BN) * 4 + (size_t)nb * BM * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
     size_t area = (size_t)ks * 3 * (blk == 32 ? Est<32>::STAGE : Est<128>::STAGE);
     const size_t exp_bruto = (size_t)nb * (BM + BN) + 16;

@@ -224,3 +224,45 @@ def test_tabela_otimizador_mantem_tensores():
     assert len(tab[3]) == 8
     mom2, w2, res2 = tab[3][2:4], tab[3][4:6], tab[3][6:8]
     assert [R.sha(host(t)) for t in (*w2, *mom2, *res2)] == esperado
+
+
+def _gemm_modos(ops, A, B, X):
+    return [ops.gemm(A, B), ops.gemm(A, B, cru=True), ops.gemm_soma(A, B, X), ops.gemm_relu2(A, B), ops.gemm_relu2_back(A, B, X)]
+
+
+@pytest.mark.parametrize("blk,K", [(32, 4608), (32, 8192), (128, 8192), (32, 16384)])
+def test_gemm_k_longo_vs_oraculo(blk, K):
+    """K beyond 4096 (up to 65536; the reference stops at 4096, ops.py:336-337): the kernel walks K in chunks of
+    4096 with the row maxima RA, RB over all of K; every mode equals the CPU oracle, at the default K-split and
+    with K-splits forced on (split target 4096), K = 4608 leaving a short last chunk."""
+    gpu, cpu = GPU(blk), CPU(blk)
+    M, N = 64, 256
+    s = lambda t: R.substream(77, f"{t} {blk} {K}")
+    A = R.bloco(s("A"), M, K, blk, espalha=5, e0=-8)
+    B = R.bloco(s("B"), N, K, blk, espalha=5, e0=-12)
+    X = R.bloco(s("X"), M, N, blk, espalha=3, e0=2)
+    ref = [CS.plano(t) for t in _gemm_modos(cpu.ops, *[tuple(cpu.dev(v) for v in T) for T in (A, B, X)])]
+    for alvo in (1024, 4096):
+        gpu.ops.lib.jt_gemm_split(alvo)
+        try:
+            out = [CS.plano(t) for t in _gemm_modos(gpu.ops, *[tuple(gpu.dev(v) for v in T) for T in (A, B, X)])]
+        finally:
+            gpu.ops.lib.jt_gemm_split(1024)
+        gpu.reg.confere_device()
+        for modo, (a, b) in enumerate(zip(out, ref)):
+            for x, y in zip(a, b):
+                assert np.array_equal(host(x), host(y)), f"mode {modo}, split target {alvo}: {primeira_diferenca(host(x), host(y))}"
+
+
+def test_gemm_k_longo_acumulador_fora_do_formato():
+    """K = 16384 with every mantissa 127 and one exponent: each K-block adds 16 * 32 * 127^2 (about 2^23) and the
+    raw sum passes 2^30 -- past the int32 range the format allows. It is reported as a device sentinel (an
+    accumulator out of range) instead of wrapping silently."""
+    from jatai_amd.registro import ErroJatai
+    blk, M, N, K = 32, 32, 128, 16384
+    gpu = GPU(blk)
+    A = (torch.full((M, K), 127, dtype=torch.int8, device="cuda"), torch.zeros(M, K // blk, dtype=torch.int8, device="cuda"))
+    B = (torch.full((N, K), 127, dtype=torch.int8, device="cuda"), torch.zeros(N, K // blk, dtype=torch.int8, device="cuda"))
+    gpu.ops.gemm(A, B, cru=True)
+    with pytest.raises(ErroJatai, match="gemm"):
+        gpu.reg.confere_device()
