@@ -11,8 +11,10 @@ Workloads (--config):
       BLK=32
   r   reference-native shape: 12 layers, D=256, 64 heads x 4, FF=1024, T=128, Bt=16 (2048 tokens), BLK=128 --
       the configuration of the reference's published 34,248 tokens/s (GTX 1650, README.md:87)
+  c5  BASELINE config 5: 24 layers at the config-4 widths, Bt=64 (16384 tokens), 16-bit residual stream; with
+      the default b4 run its step is also timed (10 replays) and reported under "config5"
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config b4|r] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config b4|r|c5] [--no-cpu] [--sem-c5]
 Prints one JSON line.
 """
 import argparse
@@ -34,6 +36,9 @@ CONFIGS = {
                nome="BASELINE config 4: 12L D512 H8x64 FF2048 V256 T256 Bt8 BLK32", publicado=None),
     "r": dict(V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=16, BLK=128, r16=False,
               nome="reference-native 12L D256 H64x4 FF1024 T128 Bt16 BLK128", publicado=34248.0),
+    "c5": dict(V=256, D=512, H=8, FF=2048, L=24, T=256, Bt=64, BLK=32, r16=True,
+               nome="BASELINE config 5: 24L D512 H8x64 FF2048 V256 T256 Bt64 (16384 tokens) BLK32, 16-bit residual",
+               publicado=None),
 }
 
 
@@ -47,6 +52,7 @@ def args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--so-passo", action="store_true", help="time the step only (no GEMM sweep, no CPU baseline): for profiling")
     ap.add_argument("--so-ops", action="store_true", help="the config-2 op sweep only (one JSON line)")
+    ap.add_argument("--sem-c5", action="store_true", help="skip the config-5 step measured beside config 4")
     ap.add_argument("--trafego", action="store_true",
                     help="for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB device copy (the counters' calibration), "
                          "then each GEMM shape of the step twice in its mode; prints the dispatch order")
@@ -430,27 +436,12 @@ def cpu_baseline_fp32(c, segundos):
                        f"{cpu_modelo()}, {dt:.1f} s; last loss {ultima:.4f}")
 
 
-def main():
-    a = args()
-    if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the multi-GPU path is a design "
-              f"(DESIGN.md), not a measured configuration.", file=sys.stderr)
-        sys.exit(2)
+def mede_passo(ops, reg, c, steps, warmup):
+    """Tokens/s of the training step of workload c replayed from one hipGraph: W untimed replays, then K timed
+    ones bracketed by device synchronizations (batches resident on the device). Returns (tokens/s, seconds of the
+    timed replays, last loss, graph launches)."""
     import torch
-    from jatai_amd import ops as O
     from jatai_amd.modelo import Modelo, PassoGravado
-    from jatai_amd.registro import Registro
-
-    c = CONFIGS[a.config]
-    O.BLK = c["BLK"]
-    reg = Registro("/tmp/jatai_bench", "bench", eco=False)
-    ops = O.OpsHip(reg)
-    if a.trafego:
-        trafego_despacha(O, ops, c)
-        return
-    if a.so_ops:
-        print(json.dumps({"config": c["nome"], "ops_config2": mede_ops(O, ops, c, reg)}), flush=True)
-        return
     dev = "cuda"
     m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, dev, ops, reg, r16=c["r16"])
     g = torch.Generator().manual_seed(1)
@@ -470,17 +461,38 @@ def main():
         perda = pg(*lotes[i % nlotes])
         reg.fim_passo()
         return perda
-    for i in range(a.warmup):
+    for i in range(warmup):
         passo(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(a.steps):
+    for i in range(steps):
         perda = passo(i)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    perda = float(perda)
+    return c["Bt"] * c["T"] * steps / dt, dt, float(perda), nlanc
+
+
+def main():
+    a = args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the multi-GPU path is a design "
+              f"(DESIGN.md), not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+    from jatai_amd import ops as O
+    from jatai_amd.registro import Registro
+
+    c = CONFIGS[a.config]
+    O.BLK = c["BLK"]
+    reg = Registro("/tmp/jatai_bench", "bench", eco=False)
+    ops = O.OpsHip(reg)
+    if a.trafego:
+        trafego_despacha(O, ops, c)
+        return
+    if a.so_ops:
+        print(json.dumps({"config": c["nome"], "ops_config2": mede_ops(O, ops, c, reg)}), flush=True)
+        return
+    tps, dt, perda, nlanc = mede_passo(ops, reg, c, a.steps, a.warmup)
     tokens = c["Bt"] * c["T"]
-    tps = tokens * a.steps / dt
 
     if a.so_passo:
         print(json.dumps({"metric": METRIC, "value": tps, "unit": "tokens/s", "ms_per_step": dt / a.steps * 1e3,
@@ -509,6 +521,13 @@ def main():
                                "per_step": v["por_passo"], "kernel": v["kernel"]} for k, v in gem.items()},
            "gemm_ms_per_step_eager_sum": tot_gemm_ms,
            "ops_config2": mede_ops(O, ops, c, reg)}
+    if a.config == "b4" and not a.sem_c5:
+        # BASELINE config 5 beside it: the 24-layer, 16384-token step with the 16-bit residual stream
+        c5 = CONFIGS["c5"]
+        print(f"bench: {c5['nome']}", file=sys.stderr, flush=True)
+        t5, dt5, p5, n5 = mede_passo(ops, reg, c5, 10, 2)
+        res["config5"] = {"workload": c5["nome"], "value": t5, "unit": "tokens/s", "ms_per_step": dt5 / 10 * 1e3, "steps": 10,
+                          "warmup": 2, "tokens_per_step": c5["Bt"] * c5["T"], "graph_launches": n5, "loss_last_step": p5}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, a.cpu_seconds)
         res["speedup_vs_cpu_baseline"] = tps / res["cpu_baseline"]["value"]

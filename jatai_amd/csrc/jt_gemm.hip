@@ -128,48 +128,9 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             else rb_s[tid - 64] = m;
         }
     }
-    // one chunk's exponents and shift tables (blocks b0 .. b0 + nbc - 1); the stage buffers must be free
-    auto tabelas = [&](int b0, int nbc) {
-        if (nch == 1) {
-            // the tile's 32 rows of A and 128 rows of B: two contiguous spans (32 nb and 128 nb bytes, multiples of
-            // 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span re-read its last
-            // vector and store it to a junk slot after the span, so neither side branches
-            const int nva = 2 * nb, nvt = 10 * nb;
-            const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
-            const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
-            for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
-                int4 t[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int v = min(v0 + k * 256 * KS, nvt - 1);
-                    t[k] = v < nva ? ga[v] : gb[v - nva];
-                }
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int v = min(v0 + k * 256 * KS, nvt);
-                    *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
-                }
-            }
-        } else {
-            // 160 row segments of nbc bytes (a multiple of 16) at column b0 of rows of nb bytes
-            const int vpr = nbc / 16;
-            for (int v = tid; v < (BM + BN) * vpr; v += 256 * KS) {
-                const int r = v / vpr, k = v - r * vpr;
-                const int8_t* e = r < BM ? EA + (size_t)(row0 + r) * nb : EB + (size_t)(col0 + r - BM) * nb;
-                *reinterpret_cast<int4*>(st_s + (size_t)r * nbc + 16 * k) = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
-            }
-        }
-        __syncthreads();
-        if (nch == 1) {
-            if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
-            else if (tid >= 64 && tid < 64 + BN) {
-                const int c = tid - 64;
-                int m = -128;
-                for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
-                rb_s[c] = m;
-            }
-            __syncthreads();
-        }
+    // shift tables of K-blocks b0 .. b0 + nbc - 1 from the staged exponent bytes (rows of nbc bytes); then the
+    // stage buffers are free again
+    auto desloca_tab = [&](int nbc) {
         for (int i = tid; i < BM * nbc; i += 256 * KS) {            // i = b * BM + r
             const int r = i & (BM - 1), b = i >> 5;
             na_s[i] = max((int)st_s[r * nbc + b] + 4 - ra_s[r], -100);
@@ -178,11 +139,63 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             const int c = i & (BN - 1), b = i >> 7;
             nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nbc + b] - rb_s[c], -100);
         }
-        __syncthreads();                                            // staging bytes consumed: buffers are free
+        __syncthreads();
+    };
+    // one chunk (K <= 4096): the tile's 32 rows of A and 128 rows of B are two contiguous spans (32 nb and 128 nb
+    // bytes, multiples of 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span
+    // re-read its last vector and store it to a junk slot after the span, so neither side branches. RA and RB
+    // come from the staged bytes.
+    auto tabelas_unica = [&]() {
+        const int nva = 2 * nb, nvt = 10 * nb;
+        const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
+        const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
+        for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
+            int4 t[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = min(v0 + k * 256 * KS, nvt - 1);
+                t[k] = v < nva ? ga[v] : gb[v - nva];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = min(v0 + k * 256 * KS, nvt);
+                *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
+            }
+        }
+        __syncthreads();
+        if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
+        else if (tid >= 64 && tid < 64 + BN) {
+            const int c = tid - 64;
+            int m = -128;
+            for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
+            rb_s[c] = m;
+        }
+        __syncthreads();
+        desloca_tab(nb);
+    };
+    // several chunks: 160 row segments of nbc bytes (a multiple of 16) at column b0 of rows of nb bytes, one
+    // 16-byte vector at a time (this runs between chunks, with the accumulators live)
+    auto tabelas_parte = [&](int b0, int nbc) {
+        const int vpr = nbc / 16;
+        for (int v = tid; v < (BM + BN) * vpr; v += 256 * KS) {
+            const int r = v / vpr, k = v - r * vpr;
+            const int8_t* e = r < BM ? EA + (size_t)(row0 + r) * nb : EB + (size_t)(col0 + r - BM) * nb;
+            *reinterpret_cast<int4*>(st_s + (size_t)r * nbc + 16 * k) = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
+        }
+        __syncthreads();
+        desloca_tab(nbc);
     };
     int b0 = 0;                                                     // first K-block of the current chunk
+    // chunk 0, before the accumulators are live: its first two stages in flight during the exponent staging
+    if (g < min(ns, NBC / BPS)) busca(g, reg);
+    if (g + KS < min(ns, NBC / BPS)) busca(g + KS, reg2);
+    if (nch == 1) tabelas_unica();
+    else tabelas_parte(0, NBC);
+    if (g < min(ns, NBC / BPS)) guarda(0, reg);
+    __syncthreads();
 
     int acc[2][2][4] = {};
+    int fora = 0;                                                   // bit 8 ti + 4 tj + i: acc[ti][tj][i] out of range
     // stage k of this group in a chunk (k = 0, 1, ...) is stage gs + k KS, held in buffer k % 3. In iteration k the loads of
     // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored.
     // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
@@ -276,11 +289,13 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         const int nbc = min(NBC, nb - b0);
         const int s0 = b0 / BPS, s1 = min(ns, (b0 + nbc + BPS - 1) / BPS);   // the chunk's stages
         const int gs = s0 + g;                                      // this group's first stage
-        if (gs < s1) busca(gs, reg);                                // first stage in flight during the exponent staging
-        if (gs + KS < s1) busca(gs + KS, reg2);                     // and the second
-        tabelas(b0, nbc);
-        if (gs < s1) guarda(0, reg);
-        __syncthreads();
+        if (c > 0) {                                                // chunk 0 was staged above
+            if (gs < s1) busca(gs, reg);
+            if (gs + KS < s1) busca(gs + KS, reg2);
+            tabelas_parte(b0, nbc);
+            if (gs < s1) guarda(0, reg);
+            __syncthreads();
+        }
         const int nk = gs < s1 ? (s1 - gs + KS - 1) / KS : 0;       // stages of this group in the chunk
         for (int k = 0; k < nk; k += 2) {
             // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
@@ -300,6 +315,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         // Past 4096 values of K the int32 accumulator has no a-priori bound: each chunk adds less than 2^30
         // (NBC blocks of |rnd(p << 4, s)| < 2^23), so a partial sum kept below 2^30 / KS at every chunk end can
         // neither wrap inside the chunk nor in the sum of the KS partials; one that is not is reported.
+        // (the violations are collected as bits and reported after the loop: a call here, with the accumulators
+        // and both stage register sets live, would make the compiler keep registers in scratch)
         if (nch > 1) {
             constexpr int T = LIM / KS;
 #pragma unroll
@@ -308,8 +325,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                 for (int tj = 0; tj < 2; tj++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        if (acc[ti][tj][i] >= T || acc[ti][tj][i] <= -T)
-                            reporta(E_ACUM, kid, (long long)(row0 + 16 * ti + 4 * lg + i) * N + col0 + wc + 16 * tj + lr, acc[ti][tj][i], -3);
+                        fora |= (int)(acc[ti][tj][i] >= T || acc[ti][tj][i] <= -T) << (8 * ti + 4 * tj + i);
         }
     }
 
@@ -333,6 +349,11 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         for (int tj = 0; tj < 2; tj++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
+    if (fora) {                                                     // K > 4096 only: an accumulator out of range
+        const int e = __builtin_ctz(fora), ti = e >> 3, tj = (e >> 2) & 1, i = e & 3;
+        reporta(E_ACUM, kid, (long long)(row0 + 16 * ti + 4 * lg + i) * N + col0 + wc + 16 * tj + lr,
+                acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr], -3);
+    }
     OtimEnt<16> otx;                                               // mode 5: the optimizer's inputs, in flight during the LDS round trip
     if constexpr (MODO == 5) {
         if (tid < 256) otx = otim_le<16>(ot, (long long)o, (long long)(o / BLK), ef);
