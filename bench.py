@@ -30,6 +30,13 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 train tokens/s (12L, 2048 tok); block-32 GEMM TOPS & % i8 MFMA peak"
 PEAK_I8 = 5.0e15          # MI355X dense int8 MFMA, ops/s
 PEAK_HBM = 8.0e12         # bytes/s
+# The format's bound: every output needs, per K-block, the exact rounding of that block's product. k_gemm spends
+# 5.5 VALU lane-operations per output and K-block on it (cvt, add of the two shift terms, ldexp, rndne; then per
+# pair of blocks an fp32 add, a cvt and an int add), and MI355X issues 64 VALU lane-ops per clock per CU
+# (4 SIMD16, wave64) on 256 CUs at 2.4 GHz. A GEMM of 2 M N K ops can therefore not beat
+# 2 BLK / 5.5 x 39.3e12 ops/s however the MFMA is fed: 457 TOP/s at BLK = 32, 9.1% of the i8 MFMA peak.
+VALU_LANE_OPS = 256 * 64 * 2.4e9
+VALU_POR_BLOCO = 5.5
 
 CONFIGS = {
     "b4": dict(V=256, D=512, H=8, FF=2048, L=12, T=256, Bt=8, BLK=32, r16=False,
@@ -506,7 +513,10 @@ def main():
             "frac": achieved / PEAK_I8, "traffic": trafego(dom_nome),
             "kernel": f"{dom['kernel']['symbol']} ({dom_nome} M={dom['M']} N={dom['N']} K={dom['K']}, "
                       f"{dom['kernel']['workgroups']} workgroups x {dom['kernel']['threads']} threads)",
-            "avg_ms": dom["ms"]}
+            "avg_ms": dom["ms"],
+            "format_bound": {"bound": "valu", "peak": 2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS / 1e12, "unit": "TOP/s",
+                             "frac": achieved / (2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS),
+                             "valu_lane_ops_per_output_block": VALU_POR_BLOCO, "valu_lane_ops_per_s": VALU_LANE_OPS}}
     res = {"metric": METRIC, "value": tps, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
            "ms_per_step": dt / a.steps * 1e3, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": tps / c["publicado"] if c.get("publicado") else None, "dtype": "int8",
