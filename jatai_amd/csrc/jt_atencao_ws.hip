@@ -13,6 +13,8 @@
 // 4096 waves at config 4 (4 per SIMD) instead of 1024, each with a quarter of the serial score/softmax chain.
 #include "jt_comum.h"
 
+constexpr size_t cmax_(size_t a, size_t b) { return a > b ? a : b; }
+
 namespace atw {
 // workspace parts, each 256-byte aligned: km8 int8 [BH][T][64]; kl int8 [BH][T][2]; vt f16 [BH][64][T];
 // mx int [BH][4] (emq, emk, emv)
@@ -565,8 +567,11 @@ template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge, int T,
                                               int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
-    __shared__ __align__(16) short dw[4][16][LP];
-    __shared__ long long parc[4][16][64];
+    // dS tiles, then (after a barrier) the waves' int64 partial sums in the same LDS: 32 KiB per workgroup, so
+    // every workgroup of the launch is resident at once
+    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP, sizeof(long long) * 4 * 16 * 64)];
+    auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
+    auto& parc = *reinterpret_cast<long long (*)[4][16][64]>(lds);
     ATB_TILE_Q
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
     const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
@@ -617,6 +622,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
 #pragma unroll
         for (int v = 0; v < 4; v++) mine[dt][v] = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
     const int ld = 3 * D;
+    __syncthreads();                                                 // every wave is done with dw: parc reuses it
     if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
         soma_ondas_bloco(parc, mine, wv, lr, lg, gq);
         const int r = tid >> 4, c = 4 * (tid & 15);
@@ -644,9 +650,12 @@ template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
                                                int T, int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
-    __shared__ __align__(16) short dw[4][16][LP];
-    __shared__ __align__(16) uint8_t pw[4][16][LP];
-    __shared__ long long parc[4][16][64];
+    // dS and P tiles, then (after a barrier) the waves' int64 partial sums in the same LDS: 32 KiB per workgroup,
+    // so every workgroup of the launch is resident at once
+    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP + 4 * 16 * LP, sizeof(long long) * 4 * 16 * 64)];
+    auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
+    auto pw = reinterpret_cast<uint8_t (*)[16][LP]>(lds + sizeof(short) * 4 * 16 * LP);
+    auto& parc = *reinterpret_cast<long long (*)[4][16][64]>(lds);
     // key tile kt pairs with the query tiles kt .. nqt - 1: decreasing work is increasing kt
     const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, kt = (int)(blockIdx.x / BH);
     const int b = bh / H, h = bh % H, b0 = b * T;
@@ -715,6 +724,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
 #pragma unroll
         for (int v = 0; v < 4; v++) mine[dt][v] = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
     const int ld = 3 * D;
+    __syncthreads();                                                 // every wave is done with dw, pw: parc reuses them
     if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
         soma_ondas_bloco(parc, mine, wv, lr, lg, gk);
 #pragma unroll
