@@ -68,17 +68,20 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
     __shared__ int red[3][4];
     const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, nbl = ld / blk, tid = threadIdx.x;
+    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t; its k and v values are loaded before the head
+    // maxima's barrier, so their latency overlaps it
+    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
+    const size_t base = (size_t)(b0 + t) * ld, tt = (size_t)bh * T + t;
+    const int colk = D + h * HD + 16 * c4, colv = 2 * D + h * HD + 16 * c4;
+    const int4 rk = ld16(qm + base + colk), rv = ld16(qm + base + colv);
+    const int ekt = qE[(size_t)(b0 + t) * nbl + colk / blk], evt = qE[(size_t)(b0 + t) * nbl + colv / blk];
     int emq, emk, emv;
     emx3(qE, ld, h * HD, D + h * HD, 2 * D + h * HD, blk, b0, T, red, emq, emk, emv);
     if (part == 0 && tid == 0) { w.mx[bh * 4] = emq; w.mx[bh * 4 + 1] = emk; w.mx[bh * 4 + 2] = emv; }
-    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t
-    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
-    const size_t base = (size_t)(b0 + t) * ld, tt = (size_t)bh * T + t;
     {
-        const int col = D + h * HD + 16 * c4;
         int v[16];
-        le_i8(qm + base + col, v);
-        const int sh = emk - (int)qE[(size_t)(b0 + t) * nbl + col / blk];
+        abre_i8(rk, v);
+        const int sh = emk - ekt;
         int8_t m8[16];
         int L = 0;
 #pragma unroll
@@ -87,10 +90,9 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         if ((c4 & 1) == 0) w.kl[tt * 2 + half] = (int8_t)L;
     }
     {
-        const int col = 2 * D + h * HD + 16 * c4;
         int v[16];
-        le_i8(qm + base + col, v);
-        const int sv = emv - (int)qE[(size_t)(b0 + t) * nbl + col / blk];
+        abre_i8(rv, v);
+        const int sv = emv - evt;
 #pragma unroll
         for (int k = 0; k < 16; k++) w.vt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), sv);
     }
@@ -357,32 +359,51 @@ template <int LIMITE>
 __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
                                                   const int8_t* __restrict__ qE, atw::WsB w, int T, int H, int D, int blk, int GA) {
     constexpr int HD = 64;
-    __shared__ int red[3][4];
+    __shared__ int red[4][4];
     __shared__ int red1[4];
     const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
-    const int ld = 3 * D, b0 = b * T, tid = threadIdx.x;
-    int emq, emk, emv;
-    emx3(qE, ld, h * HD, D + h * HD, 2 * D + h * HD, blk, b0, T, red, emq, emk, emv);
-    int emg;
+    const int ld = 3 * D, b0 = b * T, tid = threadIdx.x, nbl = ld / blk, nbg = D / blk;
+    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t. Every value it converts is loaded first, so the
+    // loads overlap the head maxima's reduction below.
+    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
+    const size_t tt = (size_t)bh * T + t, lq = (size_t)(b0 + t) * ld;
+    const int colg = h * HD + 16 * c4;
+    const int4 rg = ld16(gom + (size_t)(b0 + t) * D + colg), rv = ld16(qm + lq + 2 * D + colg);
+    const int4 rq = ld16(qm + lq + colg), rk = ld16(qm + lq + D + colg);
+    const int egt = goE[(size_t)(b0 + t) * nbg + colg / blk], evt = qE[(size_t)(b0 + t) * nbl + (2 * D + colg) / blk];
+    const int eqt = qE[(size_t)(b0 + t) * nbl + colg / blk], ekt = qE[(size_t)(b0 + t) * nbl + (D + colg) / blk];
+    // head maxima of the q, k, v and dO exponents in one reduction
+    int emq, emk, emv, emg;
     {
-        const int r = tid & 3, nbl = D / blk, cb = (h * HD + 16 * r) / blk;
-        int m = SEM_TOPO;
+        const int r = tid & 3, ba = (h * HD + 16 * r) / blk, bb = (D + h * HD + 16 * r) / blk, bc = (2 * D + h * HD + 16 * r) / blk;
+        const int bg = (h * HD + 16 * r) / blk;
+        int m[4] = {SEM_TOPO, SEM_TOPO, SEM_TOPO, SEM_TOPO};
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int t = (tid >> 2) + 64 * k;
-            if (t < T) m = max(m, (int)goE[(size_t)(b0 + t) * nbl + cb]);
+        for (int k = 0; k < 8; k++) {                                // T <= 512: all loads issued together
+            const int tk = (tid >> 2) + 64 * k;
+            if (tk < T) {
+                const int8_t* e = qE + (size_t)(b0 + tk) * nbl;
+                m[0] = max(m[0], (int)e[ba]); m[1] = max(m[1], (int)e[bb]); m[2] = max(m[2], (int)e[bc]);
+                m[3] = max(m[3], (int)goE[(size_t)(b0 + tk) * nbg + bg]);
+            }
         }
-        emg = wg_max4(m - SEM_TOPO, red1) + SEM_TOPO;                // wg_max4 takes non-negative values
+#pragma unroll
+        for (int x = 0; x < 4; x++) m[x] = g_max<64>(m[x]);
+        if ((tid & 63) == 0)
+#pragma unroll
+            for (int x = 0; x < 4; x++) red[x][tid >> 6] = m[x];
+        __syncthreads();
+        emq = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+        emk = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+        emv = max(max(red[2][0], red[2][1]), max(red[2][2], red[2][3]));
+        emg = max(max(red[3][0], red[3][1]), max(red[3][2], red[3][3]));
     }
     if (part == 0 && tid == 0) { w.mx[bh * 4] = emg - GA; w.mx[bh * 4 + 1] = emq - GA; w.mx[bh * 4 + 2] = emk - GA; w.mx[bh * 4 + 3] = emv - GA; }
-    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
-    const size_t tt = (size_t)bh * T + t;
     int amax = 0, v1 = 0;
     {   // dO: m8 << L fragments and aligned f16
-        const int col = h * HD + 16 * c4;
         int v[16];
-        le_i8(gom + (size_t)(b0 + t) * D + col, v);
-        const int s = emg - (int)goE[(size_t)(b0 + t) * (D / blk) + col / blk];
+        abre_i8(rg, v);
+        const int s = emg - egt;
         int8_t m8[16];
         int L = 0;
 #pragma unroll
@@ -396,10 +417,9 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
     }
     {   // v: m8 << L fragments (and ||v||_1 for LIMITE)
-        const int col = 2 * D + h * HD + 16 * c4;
         int v[16];
-        le_i8(qm + (size_t)(b0 + t) * ld + col, v);
-        const int s = emv - (int)qE[(size_t)(b0 + t) * (ld / blk) + col / blk];
+        abre_i8(rv, v);
+        const int s = emv - evt;
         int8_t m8[16];
         int L = 0;
 #pragma unroll
@@ -412,10 +432,9 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     }
 #pragma unroll
     for (int x = 0; x < 2; x++) {   // q (x = 0), k (x = 1): aligned f16, transposed
-        const int col = x * D + h * HD + 16 * c4;
         int v[16];
-        le_i8(qm + (size_t)(b0 + t) * ld + col, v);
-        const int s = (x ? emk : emq) - (int)qE[(size_t)(b0 + t) * (ld / blk) + col / blk];
+        abre_i8(x ? rk : rq, v);
+        const int s = (x ? emk : emq) - (x ? ekt : eqt);
         _Float16* dst = x ? w.kt : w.qt;
 #pragma unroll
         for (int k = 0; k < 16; k++) dst[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), s);

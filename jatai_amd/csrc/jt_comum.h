@@ -275,6 +275,16 @@ __device__ __forceinline__ void grava_i8(int8_t* p, const int8_t (&m)[N]) {
     else if constexpr (N == 8) *reinterpret_cast<int2*>(p) = make_int2(ws[0], ws[1]);
     else *reinterpret_cast<int4*>(p) = make_int4(ws[0], ws[1], ws[2], ws[3]);
 }
+// 16 int8 values: one 16-byte load, and its unpacking to ints (split so that loads can be issued early)
+__device__ __forceinline__ int4 ld16(const int8_t* p) { return *reinterpret_cast<const int4*>(p); }
+__device__ __forceinline__ void abre_i8(const int4 x, int (&v)[16]) {
+    const int ws[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[4 * j + i] = (int)(int8_t)(ws[j] >> (8 * i));
+}
+
 // store N int mantissas known to lie in [-127, 127] as int8
 template <int N>
 __device__ __forceinline__ void grava_q8(int8_t* p, const int (&q)[N]) {
