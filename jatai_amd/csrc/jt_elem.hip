@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, c
         const unsigned a = (unsigned)(g[i] < 0 ? -g[i] : g[i]);
         gmax = max(gmax, a);
         const int ec = max(em + 10, eg[i] + 32 - (int)__clz((int)a)) - 28;
-        v[i] = desl_var(mm[i] * 7, ec - em) + desl_var(g[i], ec - eg[i]);
+        v[i] = desl_f(mm[i] * 7, ec - em) + desl_f(g[i], ec - eg[i]);
         ee[i] = ec;
     }
     if (gmax >= (unsigned)LIM) {
@@ -307,7 +307,7 @@ __device__ __forceinline__ OtimEnt<NV> otim_le(const Otim& d, long long o, long 
 }
 // Every shift below keeps |x| < 2^28 (the momentum terms by ec >= bitlen - 28 per value, the weight terms by
 // ec >= largest exponent + 7 - 27), so none of the spec's left-shift checks can fire and the shifts run without
-// branches (desl_var per value, Desl per block); a gradient value out of range is still reported.
+// branches (desl_f per value, Desl per block); a gradient value out of range is still reported.
 template <int NV, int NL>
 __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)[NV], const OtimEnt<NV>& x, const Otim& d, long long o, long long w,
                                              bool lider, int k_lr, int ef, int kid) {
@@ -319,7 +319,7 @@ __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)
         const unsigned a = (unsigned)(g[i] < 0 ? -g[i] : g[i]);
         gmax = max(gmax, a);
         const int ec = max(em + 10, eg[i] + 32 - (int)__clz((int)a)) - 28;          // eg + bitlen(g)
-        v[i] = desl_var(x.m(i) * 7, ec - em) + desl_var(g[i], ec - eg[i]);
+        v[i] = desl_f(x.m(i) * 7, ec - em) + desl_f(g[i], ec - eg[i]);
         ee[i] = ec;
     }
     if (gmax >= (unsigned)LIM) {

@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
         int dentro = dg(g[i]) - dy(y[i] * S);
         const unsigned ad = (unsigned)(dentro < 0 ? -dentro : dentro);
         const int sh2 = max(32 - (int)__clz((int)ad) - 18, 0);     // bitlen(dentro) - 18
-        dentro = desl_var(dentro, sh2);
+        dentro = desl_f(dentro, sh2);
         v[i] = dentro * inv;
         ee[i] = ec + sh2 - k - (emax - G / 2);
     }
