@@ -172,28 +172,6 @@ __device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], 
     return quant_grupo<VPL, LPB, int8_t, 7, 127>(v, e, m, kid, idx0);
 }
 
-// Quantize a block whose values all share exponent e, where the caller knows every left shift is exact
-// (values built from int8 mantissas): same rules as quant_grupo, without per-element checks (the fused
-// GEMM epilogues use this, as jatai_cuda.cu:161-188 does).
-template <int VPL, int LPB>
-__device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
-    int bl = 0;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) bl = max(bl, bitlen(v[i]));
-    bl = g_max<LPB>(bl);
-    int E = e + bl - 7, q[VPL], est = 0;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) { q[i] = desloca(v[i], bl - 7); est |= q[i] > 127 || q[i] < -127; }
-    if (g_or<LPB>(est)) {
-        E += 1;
-#pragma unroll
-        for (int i = 0; i < VPL; i++) q[i] = desloca(v[i], bl - 6);
-    }
-    const bool zero = bl == 0 || E < -126;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) m[i] = zero ? 0 : (int8_t)q[i];
-    return zero ? E_ZERO : E;
-}
 
 // x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^30; s < 0 is a left shift the
 // caller knows to be exact): the parameters are computed once, then each value costs a shift, a bit extract, an
@@ -218,13 +196,13 @@ struct Desl {
 // so max |q| = rnd(max |v|, E - e) and the overflow test (any |q| > 127 -> E + 1) is decided on the block
 // maximum before any value is rounded. Each value is then rounded once, and no |q| exceeds 127 (so the
 // saturation clamp of the spec never acts). Returns E (E_ZERO for a zero block; those mantissas are 0).
-template <int VPL, int LPB>
+template <int VPL, int LPB, bool REPORTA = true>
 __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
     int mx = v[0], mn = v[0];
 #pragma unroll
     for (int i = 1; i < VPL; i++) { mx = max(mx, v[i]); mn = min(mn, v[i]); }
     const int amax = g_max<LPB>(max(mx, -mn));
-    if (amax >= LIM) {
+    if (REPORTA && amax >= LIM) {
 #pragma unroll
         for (int i = 0; i < VPL; i++)
             if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e);
@@ -238,8 +216,20 @@ __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL
     const int manter = zero ? 0 : -1;
 #pragma unroll
     for (int i = 0; i < VPL; i++) q[i] = d(v[i]) & manter;
-    if (!zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
+    if (REPORTA && !zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
     return zero ? E_ZERO : E;
+}
+
+// Quantize a block whose values all share exponent e and are built from int8 mantissas (|v| far below 2^30): the
+// fused GEMM epilogues, as jatai_cuda.cu:161-188 does; quant8_u without its sentinel reports (the callers report
+// an out-of-range exponent themselves, naming their epilogue).
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
+    int q[VPL];
+    const int E = quant8_u<VPL, LPB, false>(v, e, q, 0, 0);
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = (int8_t)q[i];
+    return E;
 }
 
 // ---------------------------------------------------------------------------------------------- vector I/O

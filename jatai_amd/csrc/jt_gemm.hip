@@ -414,8 +414,9 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         if constexpr (MODO == 2) {                                 // z = soma(X, C): ec = max(xE, E) - 21
             int s[16];
             const int ec = max(exin, E) - 21;
+            const Desl dx(ec - exin), dm(ec - E);                  // exact left shifts or roundings, |s| <= 2^28
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = desloca(xin[j], ec - exin) + desloca((int)m[j], ec - E);
+            for (int j = 0; j < 16; j++) s[j] = dx(xin[j]) + dm((int)m[j]);
             int8_t q[16];
             const int Ez = quant8_comum<16, LPB>(s, ec, q);
             if (Ez > 126 && lider) reporta(E_EXP, kid, (long long)o, Ez, -6);
