@@ -101,23 +101,29 @@ __host__ __device__ constexpr int ilog2_c(int n) { return n <= 1 ? 0 : 1 + ilog2
 
 // ---------------------------------------------------------------------------------------------- lane groups
 // A block of BLK values is held by LPB consecutive lanes (a power of two <= 64), VPL values each.
+// Reductions over the group run on DPP lane permutations (quad permutes, then the half-row and row mirrors: each
+// an involution that pairs the two halves of the next larger group, so every lane ends with the group's result),
+// a lane swap across rows for 32, and the whole-wave reduction of the device library for 64 -- no LDS
+// round trip, except the one ds_bpermute of the 32-lane step. Every lane of a group is active where these run.
+template <int LPB, class OP>
+__device__ __forceinline__ int g_red(int v, OP op) {
+    static_assert(LPB >= 1 && LPB <= 32 && (LPB & (LPB - 1)) == 0, "");
+    if constexpr (LPB >= 2) v = op(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (LPB >= 4) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (LPB >= 8) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    if constexpr (LPB >= 16) v = op(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));  // row_mirror
+    if constexpr (LPB >= 32) v = op(v, __shfl_xor(v, 16));
+    return v;
+}
 template <int LPB>
 __device__ __forceinline__ int g_max(int v) {
-#pragma unroll
-    for (int o = 1; o < LPB; o <<= 1) v = max(v, __shfl_xor(v, o));
-    return v;
+    if constexpr (LPB == 64) return __ockl_wfred_max_i32(v);
+    else return g_red<LPB>(v, [](int a, int b) { return max(a, b); });
 }
 template <int LPB>
 __device__ __forceinline__ int g_sum(int v) {
-#pragma unroll
-    for (int o = 1; o < LPB; o <<= 1) v += __shfl_xor(v, o);
-    return v;
-}
-template <int LPB>
-__device__ __forceinline__ int g_or(int v) {
-#pragma unroll
-    for (int o = 1; o < LPB; o <<= 1) v |= __shfl_xor(v, o);
-    return v;
+    if constexpr (LPB == 64) return __ockl_wfred_add_i32(v);
+    else return g_red<LPB>(v, [](int a, int b) { return a + b; });
 }
 
 // x * 2^-s rounded half to even for any int32 x and any s, in double precision: the conversion and the

@@ -163,12 +163,20 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             }
         }
         __syncthreads();
-        if (tid < BM) { int m = -128; for (int b = 0; b < nb; b++) m = max(m, (int)st_s[tid * nb + b]); ra_s[tid] = m; }
-        else if (tid >= 64 && tid < 64 + BN) {
-            const int c = tid - 64;
+        // RA, RB: 16 exponent bytes per LDS read when the rows are 16-byte aligned (nb a multiple of 16)
+        const int8_t* er = tid < BM ? st_s + tid * nb : (tid >= 64 && tid < 64 + BN) ? st_s + (BM + tid - 64) * nb : nullptr;
+        if (er) {
             int m = -128;
-            for (int b = 0; b < nb; b++) m = max(m, (int)st_s[(BM + c) * nb + b]);
-            rb_s[c] = m;
+            if (nb % 16 == 0) {
+                for (int b = 0; b < nb; b += 16) {
+                    const int4 t = *reinterpret_cast<const int4*>(er + b);
+                    m = max(m, max(max(max_i8x4(t.x), max_i8x4(t.y)), max(max_i8x4(t.z), max_i8x4(t.w))));
+                }
+            } else {
+                for (int b = 0; b < nb; b++) m = max(m, (int)er[b]);
+            }
+            if (tid < BM) ra_s[tid] = m;
+            else rb_s[tid - 64] = m;
         }
         __syncthreads();
         desloca_tab(nb);
