@@ -67,7 +67,7 @@ static void lds_max(K* k, size_t lds) {
 // K-splits inside a workgroup: doubled (up to 4) while tiles x splits stays within g_alvo_wg and each split
 // keeps at least four K-blocks. A split adds a group of 4 waves to the workgroup: more resident waves per SIMD to
 // hide LDS and MFMA latency under the VALU rounding work, as long as the grid does not already fill the chip
-// (1024 = 256 CUs x 4 SIMDs). (Each K-split holds three stage buffers in LDS -- 10 KiB each at BLK=32, 21 KiB at
+// (1024 = 256 CUs x 4 SIMDs). (Each K-split holds two stage buffers in LDS -- 10 KiB each at BLK=32, 21 KiB at
 // BLK=128, 160 KiB per workgroup -- and the fused epilogues of modes 2-4 would spill at 1024 threads.)
 // K up to 65536; past 4096 (one chunk of shift tables) the exponent rows are read with 16-byte loads, so the
 // number of K-blocks must be a multiple of 16

@@ -72,7 +72,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
     const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
-    char* meu = buf + (size_t)g * 3 * STAGE;                        // this group's three stage buffers
+    char* meu = buf + (size_t)g * 2 * STAGE;                        // this group's two stage buffers
 
     // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
     // (row 0..31 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
@@ -204,8 +204,9 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 
     int acc[2][2][4] = {};
     int fora = 0;                                                   // bit 8 ti + 4 tj + i: acc[ti][tj][i] out of range
-    // stage k of this group in a chunk (k = 0, 1, ...) is stage gs + k KS, held in buffer k % 3. In iteration k the loads of
-    // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored.
+    // stage k of this group in a chunk (k = 0, 1, ...) is stage gs + k KS, held in buffer k % 2. In iteration k the loads of
+    // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored -- into
+    // the buffer of stage k - 1, which every wave finished reading before the barrier that ended iteration k - 1.
     // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
     // LDS latency of block bl + 1 runs under the VALU work of block bl. Modes 3 and 4 (larger epilogues) go block
     // by block: holding both blocks' products would cost a resident wave per SIMD.
@@ -308,14 +309,14 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         for (int k = 0; k < nk; k += 2) {
             // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
             if (k + 2 < nk) busca(gs + (k + 2) * KS, reg);
-            calcula(meu + (k % 3) * STAGE, gs + k * KS);
-            if (k + 1 < nk) guarda((k + 1) % 3, reg2);
+            calcula(meu + (k % 2) * STAGE, gs + k * KS);
+            if (k + 1 < nk) guarda((k + 1) % 2, reg2);
             __syncthreads();
             if (k + 1 >= nk) break;
             // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
             if (k + 3 < nk) busca(gs + (k + 3) * KS, reg2);
-            calcula(meu + ((k + 1) % 3) * STAGE, gs + (k + 1) * KS);
-            if (k + 2 < nk) guarda((k + 2) % 3, reg);
+            calcula(meu + ((k + 1) % 2) * STAGE, gs + (k + 1) * KS);
+            if (k + 2 < nk) guarda((k + 2) % 2, reg);
             __syncthreads();
         }
         // groups with fewer stages still take part in every barrier of the loop above
@@ -534,7 +535,7 @@ static inline size_t gemm_lds(int nb, int ks, int blk) {
     using namespace gemm;
     nb = std::min(nb, 4096 / blk);                                  // the shift tables hold one chunk of K
     const size_t fixo = (size_t)(BM + BN) * 4 + (size_t)nb * BM * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
-    size_t area = (size_t)ks * 3 * (blk == 32 ? Est<32>::STAGE : Est<128>::STAGE);
+    size_t area = (size_t)ks * 2 * (blk == 32 ? Est<32>::STAGE : Est<128>::STAGE);
     const size_t exp_bruto = (size_t)nb * (BM + BN) + 16;
     const size_t acc = (size_t)ks * BM * (BN + PAD) * 4;
     if (exp_bruto > area) area = exp_bruto;
