@@ -217,7 +217,8 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     for (int v = 0; v < 4; v++) {
         int s = sred[0][4 * lg + v] + sred[1][4 * lg + v] + sred[2][4 * lg + v] + sred[3][4 * lg + v];
         if (s <= 0) { if (lr == 0 && wv == 0) reporta(E_DIV, kid, idx + (long long)v * D, s, mx[v]); s = 1; }
-        inv[v] = (1 << 28) / s;
+        // s >= 4095 (the row maximum contributes exp(0) >> 3), so 2^28 / s < 2^20: div_exata's bound
+        inv[v] = s > 256 ? div_exata(1 << 28, s) : (1 << 28) / s;
     }
     uint8_t* Pb = P + (size_t)bh * T * T;
 #pragma unroll

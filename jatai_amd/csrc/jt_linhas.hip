@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
     for (int i = 0; i < VPR; i++) { ex[i] = exp_dif(umax, u[i]) >> 3; s += ex[i]; }
     s = g_sum<LPR>(s);
     if (s <= 0) { if (lr == 0) reporta(E_DIV, kid, (long long)row * V, s, umax); s = 1; }
-    const int inv = (1 << 28) / s;
+    const int inv = s > 256 ? div_exata(1 << 28, s) : (1 << 28) / s;   // s >= 4095 (exp(0) >> 3 of the row maximum): 2^28 / s < 2^20
     int v[VPR], ee[VPR];
 #pragma unroll
     for (int i = 0; i < VPR; i++) {
