@@ -28,7 +28,7 @@ void jt_stream(void* stream);          /* every later launch goes to this hipStr
 void jt_gemm_split(int alvo_wg);       /* split-K target workgroup count for raw GEMM outputs */
 void jt_gemm_bm(int bm);               /* accepted; the MFMA GEMM has a single tile shape */
 void jt_atencao_linhas(int n);         /* accepted; attention runs one query row per thread */
-int jt_res_estocastico(int ligado);    /* 0 ok when off; stochastic residual rounding returns hipErrorNotSupported */
+int jt_res_estocastico(int ligado);    /* jatai_cuda.cu:1087: 1 = gemm_soma's residual add rounds stochastically (0 = off, the default) */
 
 /* ---- no reference counterpart: attention kernel family at head width 64, matrix cores (1, default) or dot2 (0) */
 void jt_atencao_mfma(int ligado);

@@ -238,6 +238,46 @@ __device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (
     return E;
 }
 
+// ---------------------------------------------------------------------------------------------- stochastic rounding
+// The residual add of gemm_soma under jt_res_estocastico (no spec; restated from the reference kernel text,
+// jatai_cuda.cu:146-159 and :375): x * 2^-s rounded up with probability equal to the discarded fraction, the
+// coin being a 32-bit integer hash of a per-value seed mixed with the value itself.
+__device__ __forceinline__ uint32_t hash32(uint32_t x) {
+    x ^= x >> 16; x *= 0x7feb352dU;
+    x ^= x >> 15; x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return x;
+}
+__device__ __forceinline__ int desloca_est(int x, int s, uint32_t h) {
+    if (s <= 0) return (int)((unsigned)x << min(-s, 31));
+    s = min(s, 31);
+    const long long piso = (long long)x >> s, resto = (long long)x - (piso << s);     // 0 <= resto < 2^s
+    const long long u = (long long)(hash32(h ^ (uint32_t)x * 0x9E3779B1u) & (uint32_t)((1ull << s) - 1));
+    return (int)(piso + (u < resto ? 1 : 0));
+}
+// quant8 of a block with one exponent e, every value rounded by desloca_est with its seed h[i] (the reference's
+// quant_grupo16<true>: bl = bitlen of the largest |v|, E = e + bl - 7, again one up if a mantissa passes 127,
+// zero block below 2^-126)
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_est(const int (&v)[VPL], int e, int8_t (&m)[VPL], const uint32_t (&h)[VPL]) {
+    int bl = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) bl = max(bl, bitlen(v[i]));
+    bl = g_max<LPB>(bl);
+    int E = e + bl - 7, q[VPL], qmax = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) { q[i] = desloca_est(v[i], bl - 7, h[i]); qmax = max(qmax, q[i] < 0 ? -q[i] : q[i]); }
+    if (g_max<LPB>(qmax) > 127) {
+        E += 1;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) q[i] = desloca_est(v[i], bl - 6, h[i]);
+    }
+    const bool zero = bl == 0 || E < -126;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = zero ? 0 : (int8_t)q[i];
+    return zero ? E_ZERO : E;
+}
+
 // ---------------------------------------------------------------------------------------------- vector I/O
 template <int N>
 __device__ __forceinline__ void le_i8(const int8_t* p, int (&v)[N]) {

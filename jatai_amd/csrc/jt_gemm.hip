@@ -48,7 +48,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                            const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
                                            int K, int kid, const int row0, const int col0, const Otim ot = Otim{}, int k_lr = 0,
-                                           int ef = 0) {
+                                           int ef = 0, int est = 0) {
     using namespace gemm;
     constexpr int SK = Est<BLK>::SK, LD = Est<BLK>::LD, STAGE = Est<BLK>::STAGE, VB = Est<BLK>::VB;
     extern __shared__ __align__(16) char smem[];
@@ -427,7 +427,20 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 #pragma unroll
             for (int j = 0; j < 16; j++) s[j] = dx(xin[j]) + dm((int)m[j]);
             int8_t q[16];
-            const int Ez = quant8_comum<16, LPB>(s, ec, q);
+            int Ez;
+            if (est) {                                             // stochastic rounding (jt_res_estocastico)
+                // seeds as the reference's epilogue lays out a 128-column tile: the value at tile column c has seed
+                // 8 (flat index of column c & 60 of its row) + (c & 3) + 4 (c >= 64), in 32-bit arithmetic
+                uint32_t h[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int c = oc + j;
+                    h[j] = (uint32_t)((size_t)(row0 + orow) * N + col0 + (c & 60)) * 8u + (uint32_t)((c & 3) + 4 * ((c >> 6) & 1));
+                }
+                Ez = quant8_est<16, LPB>(s, ec, q, h);
+            } else {
+                Ez = quant8_comum<16, LPB>(s, ec, q);
+            }
             if (Ez > 126 && lider) reporta(E_EXP, kid, (long long)o, Ez, -6);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Ez;
@@ -476,8 +489,9 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
                                                    const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                                    int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
-                                                   int N, int K, int kid) {
-    gemm_corpo<BLK, MODO, KS>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * gemm::BM, blockIdx.x * gemm::BN);
+                                                   int N, int K, int kid, int est) {
+    gemm_corpo<BLK, MODO, KS>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * gemm::BM, blockIdx.x * gemm::BN,
+                              Otim{}, 0, 0, est);
 }
 
 // Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels

@@ -70,10 +70,10 @@ class OpsHip:
         reg.lib = self.lib
         if self.lib.jt_erro_limpa() != 0:
             raise RuntimeError("libjatai: could not clear the device error record (no usable GPU?)")
-        if os.environ.get("JATAI_RES_EST") == "1":      # stochastic residual rounding (ops.py:308-309)
+        if os.environ.get("JATAI_RES_EST") == "1":      # stochastic residual rounding in gemm_soma (ops.py:308-309)
             rc = self.lib.jt_res_estocastico(1)
             if rc != 0:
-                raise RuntimeError("JATAI_RES_EST=1: stochastic residual rounding is not implemented in libjatai for MI355X")
+                raise RuntimeError(f"JATAI_RES_EST=1: jt_res_estocastico failed ({rc})")
         self._blk = None
         OpsHip.lib_global = self.lib
 

@@ -248,6 +248,48 @@ void or_soma(const int8_t* xm, const int8_t* xE, const int8_t* ym, const int8_t*
     quant_linhas<int8_t>(v.data(), e.data(), R, C, blk, zm, zE);
 }
 
+// soma with the stochastic residual rounding of gemm_soma under jt_res_estocastico: no spec; restated from the
+// kernel text, jatai_cuda.cu:146-159 (hash32, desloca_est, quant_grupo16<true>) and :375 (the seed of each value:
+// 8 x the flat index of its lane's first value in the epilogue's 128-column tile, plus its slot in the lane).
+static inline uint32_t hash32(uint32_t x) {
+    x ^= x >> 16; x *= 0x7feb352dU; x ^= x >> 15; x *= 0x846ca68bU; x ^= x >> 16;
+    return x;
+}
+static inline i64 desloca_est(i64 x, i64 s, uint32_t h) {
+    if (s <= 0) return shl(x, std::min<i64>(-s, 31));
+    s = std::min<i64>(s, 31);
+    const i64 piso = x >> s, resto = x - shl(piso, s);
+    const i64 u = (i64)(hash32(h ^ (uint32_t)x * 0x9E3779B1u) & (uint32_t)((1ull << s) - 1));
+    return piso + (u < resto ? 1 : 0);
+}
+void or_soma_est(const int8_t* xm, const int8_t* xE, const int8_t* ym, const int8_t* yE, i64 R, int C, int blk, int8_t* zm, int8_t* zE) {
+    const int nb = C / blk;
+#pragma omp parallel for schedule(static)
+    for (i64 r = 0; r < R; r++) {
+        std::vector<i64> v(blk);
+        std::vector<uint32_t> h(blk);
+        for (int b = 0; b < nb; b++) {
+            const i64 w = r * nb + b, ex = xE[w], ey = yE[w], ec = std::max(ex, ey) - 21;
+            i64 bl = 0;
+            for (int k = 0; k < blk; k++) {
+                const i64 x = r * C + b * blk + k;
+                v[k] = rnd(xm[x], ec - ex) + rnd(ym[x], ec - ey);
+                bl = std::max(bl, bitlen(v[k]));
+                const i64 c = b * blk + k, col0 = c & ~(i64)127, cc = c & 127;
+                h[k] = (uint32_t)(r * C + col0 + (cc & 60)) * 8u + (uint32_t)((cc & 3) + 4 * ((cc >> 6) & 1));
+            }
+            i64 E = ec + bl - 7;
+            bool big = false;
+            for (int k = 0; k < blk; k++) { const i64 q = desloca_est(v[k], bl - 7, h[k]); big |= q > 127 || q < -127; }
+            const i64 s = big ? bl - 6 : bl - 7;
+            if (big) E += 1;
+            const bool zero = bl == 0 || E < -126;
+            for (int k = 0; k < blk; k++) zm[r * C + b * blk + k] = zero ? 0 : (int8_t)desloca_est(v[k], s, h[k]);
+            zE[w] = (int8_t)(zero ? E_ZERO : E);
+        }
+    }
+}
+
 // relu2: quant(max(m,0)^2, 2E) (ops.py:134-137)
 void or_relu2(const int8_t* hm, const int8_t* hE, i64 R, int C, int blk, int8_t* am, int8_t* aE) {
     const int nb = C / blk;

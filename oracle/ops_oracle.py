@@ -59,8 +59,9 @@ def g_rms(D, blk):
 class OpsOraculo:
     nome = "oraculo"
 
-    def __init__(self, blk=128, limite=False):
-        self.blk, self.limite = blk, limite
+    def __init__(self, blk=128, limite=False, estocastico=False):
+        # estocastico: gemm_soma's residual add rounds stochastically, as OpsCuda with jt_res_estocastico(1)
+        self.blk, self.limite, self.estocastico = blk, limite, estocastico
 
     def _bloco(self, R, C, dt=torch.int8):
         return torch.empty(R, C, dtype=dt), torch.empty(R, C // self.blk, dtype=torch.int8)
@@ -88,7 +89,16 @@ class OpsOraculo:
         return C
 
     def gemm_soma(self, A, B, X):
-        return self.soma(X, self.gemm(A, B))
+        return (self.soma_est if self.estocastico else self.soma)(X, self.gemm(A, B))
+
+    def soma_est(self, X, Y):
+        """soma(X, Y) with gemm_soma's stochastic residual rounding (jatai_cuda.cu:146-159, :375); the seeds follow
+        the positions of Y's values in its [R, C] matrix."""
+        (xm, xE), (ym, yE) = [tuple(_cpu(t) for t in T) for T in (X, Y)]
+        R, C = xm.shape
+        Z = self._bloco(R, C)
+        lib().or_soma_est(_p(xm), _p(xE), _p(ym), _p(yE), _ll(R), _i(C), _i(self.blk), _p(Z[0]), _p(Z[1]))
+        return Z
 
     def gemm_relu2(self, A, B):
         h = self.gemm(A, B)

@@ -266,3 +266,34 @@ def test_gemm_k_longo_acumulador_fora_do_formato():
     gpu.ops.gemm(A, B, cru=True)
     with pytest.raises(ErroJatai, match="gemm"):
         gpu.reg.confere_device()
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_gemm_soma_estocastica(blk):
+    """gemm_soma with stochastic residual rounding switched on (jt_res_estocastico(1); ops.py:308-309,
+    jatai_cuda.cu:146-159 and :375): every bit equals the CPU oracle's restatement, whose seeds follow each value's
+    position in the output; with the switch off again the output is the deterministic one. Spread exponents make
+    the residual add drop bits in most blocks, so the hashed rounding decides many values."""
+    gpu, cpu = GPU(blk), CPU(blk)
+    from oracle.ops_oracle import OpsOraculo
+    M, N, K = 96, 384, 512
+    s = lambda t: R.substream(91, f"{t} {blk}")
+    A = R.bloco(s("A"), M, K, blk, espalha=5, e0=-8)
+    B = R.bloco(s("B"), N, K, blk, espalha=5, e0=-12)
+    X = R.bloco(s("X"), M, N, blk, espalha=4, e0=3)
+    c = [tuple(cpu.dev(v) for v in T) for T in (A, B, X)]
+    g = [tuple(gpu.dev(v) for v in T) for T in (A, B, X)]
+    ref_est = OpsOraculo(blk, estocastico=True).gemm_soma(*c)
+    ref_det = cpu.ops.gemm_soma(*c)
+    assert sum(int((host(a) != host(b)).sum()) for a, b in zip(ref_est, ref_det)) > 100
+    assert gpu.ops.lib.jt_res_estocastico(1) == 0
+    try:
+        out = gpu.ops.gemm_soma(*g)
+    finally:
+        gpu.ops.lib.jt_res_estocastico(0)
+    det = gpu.ops.gemm_soma(*g)
+    gpu.reg.confere_device()
+    for x, y in zip(out, ref_est):
+        assert np.array_equal(host(x), host(y)), primeira_diferenca(host(x), host(y))
+    for x, y in zip(det, ref_det):
+        assert np.array_equal(host(x), host(y)), primeira_diferenca(host(x), host(y))

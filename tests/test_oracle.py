@@ -198,3 +198,28 @@ def test_r16_round_trip_and_sum():
     e16 = np.linalg.norm(deq(*ops.soma16(ops.para16(x), y)) - exato)
     e8 = np.linalg.norm(deq(*ops.soma(x, y)) - exato)
     assert e16 < e8 / 8          # 15-bit vs 7-bit mantissas; measured ratio ~16 at a 2^-12 addend
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_soma_estocastica(blk):
+    """gemm_soma's stochastic residual rounding (jt_res_estocastico; no spec, restated from jatai_cuda.cu:146-159
+    and :375). Where no bit is dropped it equals the deterministic soma. Over many rows holding the same values
+    (each row other seeds) the mean of x + y approaches the exact sum, where half-to-even rounding keeps a fixed
+    bias: 100 + 3/256 rounds to 100 every time, and stochastically up with probability 3/256."""
+    ops = OpsOraculo(blk)
+    NL, C = 4096, 256
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    # no bit dropped: equal exponents and |x + y| <= 127
+    x = R.uniform_int(61, (NL, C), -60, 60).astype(np.int8)
+    y = R.uniform_int(62, (NL, C), -60, 60).astype(np.int8)
+    e = R.uniform_int(63, (NL, C // blk), -20, 5).astype(np.int8)
+    X, Y = (t(x), t(e)), (t(y), t(e.copy()))
+    assert all(np.array_equal(host(a), host(b)) for a, b in zip(ops.soma_est(X, Y), ops.soma(X, Y)))
+    # unbiased where half-to-even is not
+    X = (t(np.full((NL, C), 100, np.int8)), t(np.zeros((NL, C // blk), np.int8)))
+    Y = (t(np.full((NL, C), 3, np.int8)), t(np.full((NL, C // blk), -8, np.int8)))
+    deq = lambda Z: host(Z[0]).astype(np.float64) * np.repeat(2.0 ** host(Z[1]).astype(np.float64), blk, axis=1)
+    exato = 100 + 3 / 256
+    assert np.all(deq(ops.soma(X, Y)) == 100.0)
+    media = deq(ops.soma_est(X, Y)).mean()
+    assert abs(media - exato) < 0.002, media
