@@ -33,7 +33,6 @@ static int g_blk = 128;                 // block size of every tensor: 32 or 128
 static int g_alvo_wg = 1024;            // GEMM K-split target: tiles x K-splits per launch
 static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
 static int g_atencao_mfma = 1;          // head width 64: matrix-core attention (1) or the dot2 kernels (0)
-static int g_res_est = 0;               // stochastic rounding of gemm_soma's residual add (jt_res_estocastico)
 
 static int fim() { return (int)hipGetLastError(); }
 // Every kernel moves 8- or 16-byte vectors: operands must be 16-byte aligned (torch allocations are 256-byte
@@ -103,9 +102,12 @@ void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one til
 void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
 // No reference counterpart: selects the matrix-core (1, default) or dot2 (0) attention kernels at head width 64.
 void jt_atencao_mfma(int ligado) { g_atencao_mfma = ligado ? 1 : 0; }
-// jatai_cuda.cu:1087: stochastic rounding of gemm_soma's residual add. Read when a GEMM is launched (a captured
-// graph keeps the value it was captured with).
-int jt_res_estocastico(int ligado) { g_res_est = ligado ? 1 : 0; return 0; }
+// jatai_cuda.cu:1087: stochastic rounding of gemm_soma's residual add. A synchronous copy into the device global
+// g_res_est of the current device; gemm_soma kernels read it when they run.
+int jt_res_estocastico(int ligado) {
+    const int v = ligado ? 1 : 0;
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_res_est), &v, sizeof(int));
+}
 // No reference counterpart: the reference fixes BLK = 128 (jatai_cuda.cu:16).
 int jt_bloco(int blk) {
     if (blk != 32 && blk != 128) return (int)hipErrorInvalidValue;
@@ -129,7 +131,7 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
     const dim3 grade(N / BN, M / BM);
     const size_t lds = gemm_lds(nb, ks, g_blk);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
-             (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kid, g_res_est
+             (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kid
 #define L(BL, MD, S) (lds_max(k_gemm<BL, MD, S>, lds), k_gemm<BL, MD, S><<<grade, 256 * S, lds, g_stream>>>(ARGS))
 #define LS2(BL, MD) (ks == 1 ? L(BL, MD, 1) : L(BL, MD, 2))
 #define LS4(BL, MD) (ks == 1 ? L(BL, MD, 1) : ks == 2 ? L(BL, MD, 2) : L(BL, MD, 4))

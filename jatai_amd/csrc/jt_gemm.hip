@@ -484,14 +484,18 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     }
 }
 
+// jt_res_estocastico's switch, as in the reference a device global (jatai_cuda.cu:146) read when a mode-2 kernel
+// runs, so a captured graph follows the value set before each replay.
+__device__ int g_res_est = 0;
+
 template <int BLK, int MODO, int KS>
 __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                                    const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                                    int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
-                                                   int N, int K, int kid, int est) {
+                                                   int N, int K, int kid) {
     gemm_corpo<BLK, MODO, KS>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * gemm::BM, blockIdx.x * gemm::BN,
-                              Otim{}, 0, 0, est);
+                              Otim{}, 0, 0, MODO == 2 ? g_res_est : 0);
 }
 
 // Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels

@@ -1,8 +1,7 @@
 """The training step with stochastic residual rounding switched on (jt_res_estocastico(1), the JATAI_RES_EST=1
 switch of ops.py:308-309; kernel text jatai_cuda.cu:146-159, :375), at the BASELINE config-4 widths with 2 layers
 and 2 sequences: the fused HIP step, two steps eagerly and a third replayed from a captured hipGraph, leaves the
-same losses, weights, momenta and residuals as the CPU oracle's op-by-op step with the same switch. The switch is
-read when a kernel is launched or captured, so the graph is captured with it on."""
+same losses, weights, momenta and residuals as the CPU oracle's op-by-op step with the same switch."""
 import pytest
 import torch
 

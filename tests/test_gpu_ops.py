@@ -273,7 +273,8 @@ def test_gemm_soma_estocastica(blk):
     """gemm_soma with stochastic residual rounding switched on (jt_res_estocastico(1); ops.py:308-309,
     jatai_cuda.cu:146-159 and :375): every bit equals the CPU oracle's restatement, whose seeds follow each value's
     position in the output; with the switch off again the output is the deterministic one. Spread exponents make
-    the residual add drop bits in most blocks, so the hashed rounding decides many values."""
+    the residual add drop bits in most blocks, so the hashed rounding decides many values. A captured graph follows
+    the switch's value at each replay."""
     gpu, cpu = GPU(blk), CPU(blk)
     from oracle.ops_oracle import OpsOraculo
     M, N, K = 96, 384, 512
@@ -297,3 +298,22 @@ def test_gemm_soma_estocastica(blk):
         assert np.array_equal(host(x), host(y)), primeira_diferenca(host(x), host(y))
     for x, y in zip(det, ref_det):
         assert np.array_equal(host(x), host(y)), primeira_diferenca(host(x), host(y))
+    # as in the reference, the switch is a device global read when the kernel runs: a graph captured with it off
+    # rounds stochastically on the replays made with it on
+    grafo = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    try:
+        with torch.cuda.graph(grafo):
+            gpu.ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+            gout = gpu.ops.gemm_soma(*g)
+    finally:
+        gpu.ops.lib.jt_stream(None)
+    for ligado, ref in ((1, ref_est), (0, ref_det), (1, ref_est)):
+        assert gpu.ops.lib.jt_res_estocastico(ligado) == 0
+        try:
+            grafo.replay()
+            torch.cuda.synchronize()
+        finally:
+            gpu.ops.lib.jt_res_estocastico(0)
+        for x, y in zip(gout, ref):
+            assert np.array_equal(host(x), host(y)), (ligado, primeira_diferenca(host(x), host(y)))
