@@ -31,12 +31,12 @@ METRIC = "INT8 train tokens/s (12L, 2048 tok); block-32 GEMM TOPS & % i8 MFMA pe
 PEAK_I8 = 5.0e15          # MI355X dense int8 MFMA, ops/s
 PEAK_HBM = 8.0e12         # bytes/s
 # The format's bound: every output needs, per K-block, the exact rounding of that block's product. k_gemm spends
-# 5.5 VALU lane-operations per output and K-block on it (cvt, add of the two shift terms, ldexp, rndne; then per
-# pair of blocks an fp32 add, a cvt and an int add), and MI355X issues 64 VALU lane-ops per clock per CU
-# (4 SIMD16, wave64) on 256 CUs at 2.4 GHz. A GEMM of 2 M N K ops can therefore not beat
-# 2 BLK / 5.5 x 39.3e12 ops/s however the MFMA is fed: 457 TOP/s at BLK = 32, 9.1% of the i8 MFMA peak.
+# 4 VALU lane-operations per output and K-block on it (fp64 cvt, ldexp by the row shift, fma by the column scale
+# plus the rounding constant, int add), and MI355X issues 64 VALU lane-ops per clock per CU (4 SIMD16, wave64)
+# on 256 CUs at 2.4 GHz. A GEMM of 2 M N K ops can therefore not beat 2 BLK / 4 x 39.3e12 ops/s however the MFMA
+# is fed: 629 TOP/s at BLK = 32, 12.6% of the i8 MFMA peak.
 VALU_LANE_OPS = 256 * 64 * 2.4e9
-VALU_POR_BLOCO = 5.5
+VALU_POR_BLOCO = 4.0
 
 CONFIGS = {
     "b4": dict(V=256, D=512, H=8, FF=2048, L=12, T=256, Bt=8, BLK=32, r16=False,

@@ -4,11 +4,14 @@
 // p_ijb = sum_{k in b} a_ik b_jk (one MFMA per 32 values of K), then acc_ij += rnd(p_ijb << 4, sa + sb) with
 // sa = RA_i - ea_ib, sb = RB_j - eb_jb, round half to even; base_ij = RA_i + RB_j - 4.
 //
-// The rounding runs in fp32, where it is exact: |p| < 2^21, so p, p * 2^(4 - s) (a power-of-two scale) and
-// its nearest-even integer (v_rndne_f32) are all representable, and for s >= 26 the scaled value is below 1/2
-// and rounds to 0 exactly as rnd(., s) does. The shift n = 4 - sa - sb is one add of two precomputed terms, so
-// per output and K-block the epilogue is add, cvt, ldexp, rndne, cvt, add: six VALU ops (~9 in integer form).
-// This per-block VALU epilogue, not the MFMA, bounds the kernel.
+// The rounding runs in fp64 with the round-to-nearest-even of the FMA itself:
+//   g = fma(ldexp(double(p), 4 - sa), 2^-sb, 1.5 * 2^52).
+// ldexp and the product by a power of two are exact, and |p * 2^(4 - sa - sb)| < 2^26 (|p| <= 128 * 128 * BLK),
+// so the exact sum lies in [2^52, 2^53), where the spacing of doubles is 1: the FMA's one rounding is
+// rnd(p << 4, sa + sb), and the low 32 bits of g are that integer in two's complement (1.5 * 2^52 has zero low
+// bits). The row term is a 32-bit ldexp operand and the column term one double per column and block, so per
+// output and K-block the work is cvt, ldexp, fma and add: 4 VALU ops, against 9 in integer form. This per-block
+// VALU work, not the MFMA, bounds the kernel.
 //
 // Tiling: a workgroup of 4 x KS waves owns a 32 x 128 output tile (one 128-column block at BLK=128, four at
 // BLK=32). K is walked in stages of 128 bytes per row (4 blocks at BLK=32, 1 at BLK=128): wave group g
@@ -76,22 +79,26 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 
     // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
     // (row 0..31 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
+    // Addresses: a workgroup-uniform base per 32-row band (A's rows, then B's in four bands) plus one 32-bit lane
+    // offset vr K + vc shared by the five loads (< 128 * 65536 = 2^23), so the loads take a scalar base.
     const int vr = tg >> 3, vc = (tg & 7) * VB;
     const int8_t* src[5];
-    src[0] = A + (size_t)(row0 + vr) * K + vc;
+    src[0] = A + (size_t)row0 * K;
 #pragma unroll
-    for (int i = 1; i < 5; i++) src[i] = B + (size_t)(col0 + vr + 32 * (i - 1)) * K + vc;
+    for (int i = 1; i < 5; i++) src[i] = B + (size_t)(col0 + 32 * (i - 1)) * K;
+    const unsigned vofs = (unsigned)(vr * K + vc);
     int4 reg[5], reg2[5];                                           // two register sets: loads run two stages ahead
     // The last stage may extend past K (nb not a multiple of the blocks per stage): its vectors past K re-read the
     // row's last vector instead (a uniform test; those bytes land in blocks >= nb, which are never computed).
     auto busca = [&](int st, int4 (&r)[5]) {
         int o = st * SK;
         if (o + SK > K) o = min(o + vc, K - VB) - vc;
+        const unsigned d = vofs + (unsigned)o;
 #pragma unroll
         for (int i = 0; i < 5; i++) {
-            if constexpr (VB == 16) r[i] = *reinterpret_cast<const int4*>(src[i] + o);
+            if constexpr (VB == 16) r[i] = *reinterpret_cast<const int4*>(src[i] + d);
             else {
-                const int2 t = *reinterpret_cast<const int2*>(src[i] + o);
+                const int2 t = *reinterpret_cast<const int2*>(src[i] + d);
                 r[i] = make_int4(t.x, t.y, 0, 0);
             }
         }
@@ -111,8 +118,6 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     };
     // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
     const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
-    const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
-    const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
     // Several chunks: RA and RB first, by one pass over the exponent rows in global memory (rows of nb bytes, nb a
     // multiple of 16 there: 16-byte loads). One chunk: from the staged exponents, below.
     if (nch > 1) {
@@ -207,10 +212,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // stage k of this group in a chunk (k = 0, 1, ...) is stage gs + k KS, held in buffer k % 2. In iteration k the loads of
     // stage k + 2 are issued, stage k is computed, and stage k + 1 (loaded during iteration k - 1) is stored -- into
     // the buffer of stage k - 1, which every wave finished reading before the barrier that ended iteration k - 1.
-    // Modes 0-2: all fragment reads and MFMAs of a stage first, then the rounding of each block, so the MFMA and
-    // LDS latency of block bl + 1 runs under the VALU work of block bl. Modes 3 and 4 (larger epilogues) go block
-    // by block: holding both blocks' products would cost a resident wave per SIMD.
-    constexpr bool ADIANTA = true;
+    // Each block's MFMAs are followed by its rounding: the MFMA latency runs under the other resident waves' VALU
+    // work, and only one block's products are live (the fp64 rounding's temporaries need the registers).
     auto produtos = [&](const char* tile, int bl, v4i (&p)[2][2]) {
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
@@ -231,66 +234,28 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                 for (int tj = 0; tj < 2; tj++) p[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], p[ti][tj], 0, 0, 0);
         }
     };
+    // rnd(p << 4, sa + sb) from the row term n = 4 - sa and the column scale c = 2^-sb (see the head of this file)
+    auto rnd_fma = [](int p, int n, double c) { return __double2loint(__builtin_fma(ldexp((double)p, n), c, 0x1.8p52)); };
+    auto escala = [](int nbv) { return __hiloint2double((1023 + nbv) << 20, 0); };
     auto arredonda = [&](int b, const v4i (&p)[2][2]) {
         const int bt = b - b0;                                      // block index in the chunk's tables
         const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 4 * lg);
         const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 16 + 4 * lg);
-        const int nb0 = nb_s[bt * BN + wc + lr], nb1 = nb_s[bt * BN + wc + 16 + lr];
+        const double cb0 = escala(nb_s[bt * BN + wc + lr]), cb1 = escala(nb_s[bt * BN + wc + 16 + lr]);
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
 #pragma unroll
             for (int tj = 0; tj < 2; tj++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);                     // 4 - sa - sb
-                    acc[ti][tj][i] += (int)rintf(ldexpf((float)p[ti][tj][i], n));
-                }
-    };
-    // BLK=32, two blocks in the stage: the two rounded products are added in fp32 before the conversion; each is
-    // an integer below 2^23 in magnitude (|p| <= 32 * 128 * 128 = 2^19, scale <= 2^4), so the sum is exact
-    auto arredonda2 = [&](int b, const v4i (&p)[2][2], const v4i (&q)[2][2]) {
-        const int bt = b - b0;                                      // block index in the chunk's tables
-        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 4 * lg);
-        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 16 + 4 * lg);
-        const int nb0 = nb_s[bt * BN + wc + lr], nb1 = nb_s[bt * BN + wc + 16 + lr];
-        const v4i ma0 = *reinterpret_cast<const v4i*>(na_s + (bt + 1) * BM + 4 * lg);
-        const v4i ma1 = *reinterpret_cast<const v4i*>(na_s + (bt + 1) * BM + 16 + 4 * lg);
-        const int mb0 = nb_s[(bt + 1) * BN + wc + lr], mb1 = nb_s[(bt + 1) * BN + wc + 16 + lr];
-#pragma unroll
-        for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-            for (int tj = 0; tj < 2; tj++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = (ti ? na1[i] : na0[i]) + (tj ? nb1 : nb0);
-                    const int m = (ti ? ma1[i] : ma0[i]) + (tj ? mb1 : mb0);
-                    acc[ti][tj][i] += (int)(rintf(ldexpf((float)p[ti][tj][i], n)) + rintf(ldexpf((float)q[ti][tj][i], m)));
-                }
+                for (int i = 0; i < 4; i++) acc[ti][tj][i] += rnd_fma(p[ti][tj][i], ti ? na1[i] : na0[i], tj ? cb1 : cb0);
     };
     auto calcula = [&](const char* tile, int st) {
-        if constexpr (ADIANTA && BPS == 2) {
-            v4i p[BPS][2][2];
 #pragma unroll
-            for (int bl = 0; bl < BPS; bl++)
-                if (st * BPS + bl < nb) produtos(tile, bl, p[bl]);
-            if (st * BPS + 1 < nb) arredonda2(st * BPS, p[0], p[1]);
-            else arredonda(st * BPS, p[0]);
-        } else if constexpr (ADIANTA) {
-            v4i p[BPS][2][2];
-#pragma unroll
-            for (int bl = 0; bl < BPS; bl++)
-                if (st * BPS + bl < nb) produtos(tile, bl, p[bl]);
-#pragma unroll
-            for (int bl = 0; bl < BPS; bl++)
-                if (st * BPS + bl < nb) arredonda(st * BPS + bl, p[bl]);
-        } else {
-#pragma unroll
-            for (int bl = 0; bl < BPS; bl++) {
-                if (st * BPS + bl >= nb) break;
-                v4i p[2][2];
-                produtos(tile, bl, p);
-                arredonda(st * BPS + bl, p);
-            }
+        for (int bl = 0; bl < BPS; bl++) {
+            if (st * BPS + bl >= nb) break;
+            v4i p[2][2];
+            produtos(tile, bl, p);
+            arredonda(st * BPS + bl, p);
         }
     };
     for (int c = 0; c < nch; c++) {
@@ -340,6 +305,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 
     // ---- output stage: KS partial tiles to LDS, summed while read back in the row-block layout. The X operand
     // of modes 2 and 4 is read here, not before the K loop, so its 16 registers do not cost a resident wave.
+    const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
+    const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
     int xin[16], exin = 0;
     if constexpr (MODO == 2 || MODO == 4) {
         if (tid < 256) { le_i8(Xm + o, xin); exin = XE[oe]; }
