@@ -178,6 +178,42 @@ __device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], 
     return quant_grupo<VPL, LPB, int8_t, 7, 127>(v, e, m, kid, idx0);
 }
 
+// quant8 of values whose per-value exponents satisfy |e| <= 900 (the GEMM epilogue: e = RA + RB - 4), through
+// d = v 2^e in double precision, exact and normal for every nonzero int32 v. bitlen(|v|) + e is the binary
+// exponent of d, so topo is read from the exponent field of the block's largest |d|. q = rnd(d 2^-E) is the low
+// word of fma(d, 2^-E, 1.5 * 2^52) (the sum lies where doubles are spaced by 1, so the FMA's rounding is the
+// half-to-even rounding), and that rounding is monotone: max |q| = rnd(max |d| 2^-E), so the bump test takes one
+// FMA per lane instead of a pass over the values. Same results and sentinels as quant8.
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_d(const int (&v)[VPL], const int (&e)[VPL], int8_t (&m)[VPL], int kid, long long idx0) {
+    double d[VPL], dmax = 0.0;
+    unsigned fora = 0;                                              // max of v + LIM - 1 as unsigned: >= 2 LIM - 1 iff |v| >= LIM
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        d[i] = __builtin_ldexp((double)v[i], e[i]);
+        dmax = __builtin_fmax(dmax, __builtin_fabs(d[i]));
+        fora = max(fora, (unsigned)v[i] + (unsigned)(LIM - 1));
+    }
+    if (fora >= 2u * LIM - 1) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++)
+            if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e[i]);
+    }
+    // exponent field - 1022 = floor(log2 dmax) + 1; a lane of zeros gives -1022, below every real topo
+    const int topo = g_max<LPB>((__double2hiint(dmax) >> 20) - 1022);
+    const int E0 = topo - 7;
+    const double k0 = __hiloint2double((1023 - E0) << 20, 0);
+    const int bump = g_max<LPB>(__double2loint(__builtin_fma(dmax, k0, 0x1.8p52))) > 127;
+    const int E = E0 + bump;
+    const double k = bump ? k0 * 0.5 : k0;                          // 2^-E
+    const bool zero = E < -126;                                     // also the all-zero block (topo = -1022)
+    const int manter = zero ? 0 : -1;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = (int8_t)(__double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter);
+    if (!zero && E > 126) reporta(E_EXP, kid, idx0, E, topo);
+    return zero ? E_ZERO : E;
+}
+
 
 // x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^30; s < 0 is a left shift the
 // caller knows to be exact): the parameters are computed once, then each value costs a shift, a bit extract, an
@@ -227,15 +263,30 @@ __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL
 }
 
 // Quantize a block whose values all share exponent e and are built from int8 mantissas (|v| far below 2^30): the
-// fused GEMM epilogues, as jatai_cuda.cu:161-188 does; quant8_u without its sentinel reports (the callers report
-// an out-of-range exponent themselves, naming their epilogue).
+// fused GEMM epilogues, as jatai_cuda.cu:161-188 does. quant8_u's rules (no sentinel reports: the callers report
+// an out-of-range exponent themselves, naming their epilogue), in double precision as quant8_d: bitlen of the
+// block's largest |v| from the exponent field of max |(double)v|, and each value rounded by one FMA with
+// 1.5 * 2^52 (exact left shifts for s <= 0, half-to-even roundings otherwise); the bump test is the rounding of
+// the largest |v| (rounding is monotone). Four VALU ops per value against seven in integer form.
 template <int VPL, int LPB>
 __device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
-    int q[VPL];
-    const int E = quant8_u<VPL, LPB, false>(v, e, q, 0, 0);
+    double d[VPL], dmax = 0.0;
 #pragma unroll
-    for (int i = 0; i < VPL; i++) m[i] = (int8_t)q[i];
-    return E;
+    for (int i = 0; i < VPL; i++) {
+        d[i] = (double)v[i];
+        dmax = __builtin_fmax(dmax, __builtin_fabs(d[i]));
+    }
+    const int bl = g_max<LPB>((__double2hiint(dmax) >> 20) - 1022);      // bitlen(max |v|); -1022 for all zeros
+    const int s0 = bl - 7;
+    const double k0 = __hiloint2double((1023 - s0) << 20, 0);            // 2^-s0
+    const int bump = g_max<LPB>(__double2loint(__builtin_fma(dmax, k0, 0x1.8p52))) > 127;
+    const int E = e + s0 + bump;
+    const double k = bump ? k0 * 0.5 : k0;
+    const bool zero = bl <= 0 || E < -126;
+    const int manter = zero ? 0 : -1;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = (int8_t)(__double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter);
+    return zero ? E_ZERO : E;
 }
 
 // ---------------------------------------------------------------------------------------------- stochastic rounding

@@ -372,7 +372,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             return;
         }
         int8_t m[16];
-        const int E = quant8<16, LPB>(v, base, m, kid, o);
+        const int E = quant8_d<16, LPB>(v, base, m, kid, o);        // |base| <= 260
         if constexpr (MODO == 0 || MODO == 3) {
             grava_i8(Cm + o, m);
             if (lider) CE[oe] = (int8_t)E;
@@ -442,7 +442,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                     }
                     int8_t t8[16];
                     const long long ot = (long long)(col0 + c) * M + row0 + 16 * hf;
-                    const int Et = quant8<16, 2>(tv, te, t8, kid, ot);
+                    const int Et = quant8_d<16, 2>(tv, te, t8, kid, ot);   // int8 exponents
                     grava_i8(Om2 + ot, t8);
                     if (hf == 0) OE2[(size_t)(col0 + c) * (M / 32) + row0 / 32] = (int8_t)Et;
                 }
