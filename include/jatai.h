@@ -19,8 +19,8 @@ extern "C" {
 #endif
 
 /* ---- device error record and stream (jatai_cuda.cu:1062-1073, 1088) */
-int jt_erro_le(long long* out);        /* out[6] = {n, code, kid, idx, value, aux}; returns n, or -hipError */
-int jt_erro_limpa(void);               /* clears the record */
+int jt_erro_le(long long* out);        /* jatai_cuda.cu:1062: out[6] = {n, code, kid, idx, value, aux}; returns n, or -hipError; synchronizes the device first */
+int jt_erro_limpa(void);               /* jatai_cuda.cu:1069: clears the record, ordered on the library's stream (no host wait) */
 int jt_sincroniza(void);               /* hipDeviceSynchronize */
 void jt_stream(void* stream);          /* every later launch goes to this hipStream_t (graph capture) */
 

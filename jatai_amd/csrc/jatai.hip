@@ -28,6 +28,10 @@ __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long lo
     }
 }
 
+__global__ void k_erro_limpa() {
+    if (threadIdx.x < sizeof(Erro) / sizeof(int)) reinterpret_cast<int*>(&g_erro)[threadIdx.x] = 0;
+}
+
 static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
 static int g_alvo_wg = 1024;            // GEMM K-split target: tiles x K-splits per launch
@@ -84,16 +88,20 @@ static int gemm_divisoes(int M, int N, int K, int modo) {
 extern "C" {
 
 // ---------------------------------------------------------------------------------------------- state
+// jatai_cuda.cu:1062: reads the record after every launch so far, on any stream, has finished.
 int jt_erro_le(long long* out) {
+    hipError_t c = hipDeviceSynchronize();
     Erro e;
-    hipError_t c = hipMemcpyFromSymbol(&e, HIP_SYMBOL(g_erro), sizeof(Erro), 0, hipMemcpyDeviceToHost);
+    if (c == hipSuccess) c = hipMemcpyFromSymbol(&e, HIP_SYMBOL(g_erro), sizeof(Erro), 0, hipMemcpyDeviceToHost);
     if (c != hipSuccess) return -(int)c;
     out[0] = e.n; out[1] = e.codigo; out[2] = e.kid; out[3] = e.idx; out[4] = e.valor; out[5] = e.aux;
     return e.n;
 }
+// jatai_cuda.cu:1069: clears the record. A kernel on the library's stream rather than a synchronous copy: the
+// launches before it cannot write into the cleared record, and the host does not wait for the GPU to drain.
 int jt_erro_limpa() {
-    Erro e = {};
-    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_erro), &e, sizeof(Erro), 0, hipMemcpyHostToDevice);
+    k_erro_limpa<<<1, 64, 0, g_stream>>>();
+    return fim();
 }
 int jt_sincroniza() { return (int)hipDeviceSynchronize(); }
 void jt_stream(void* st) { g_stream = (hipStream_t)st; }

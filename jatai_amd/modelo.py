@@ -238,7 +238,8 @@ class PassoGravado:
 
     Capture runs nothing (weights do not change while recording). Inputs go to fixed buffers with copy_ before
     each replay. The launch list of the capture (kid -> op, scope, inputs) is kept, so a device sentinel raised
-    in a replay names the same op and scope as in eager mode. Format checks run once, at capture.
+    in a replay names the same op and scope as in eager mode. Format checks run once, at capture. The loss is
+    computed inside the graph too: a call returns the graph's loss tensor, which the next replay overwrites.
     """
 
     def __init__(self, modelo, Bt, T, k_lr):
@@ -257,6 +258,7 @@ class PassoGravado:
             with torch.cuda.graph(self.grafo):
                 lib.jt_stream(torch.cuda.current_stream().cuda_stream)
                 self.d_alvo, self.soma = modelo.passo(self.tok, self.alvo, k_lr=k_lr)
+                self.perda = perda_de(self.d_alvo, self.soma)     # in the graph, as modelo.py:170 captures passo's loss
         finally:
             lib.jt_stream(None)
             modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = est, vig, pi
@@ -268,4 +270,4 @@ class PassoGravado:
         self.alvo.copy_(alvo)
         self.reg.lancamentos = self.lancamentos
         self.grafo.replay()
-        return perda_de(self.d_alvo, self.soma)
+        return self.perda
