@@ -660,6 +660,13 @@ __device__ __forceinline__ void tile_xyt(long xa0, long xa1, long yb0, long yb1,
     for (int v = 0; v < 4; v++) out[v] = shl(p0[v], lx[v][0] + ly0) + shl(p1[v], lx[v][1] + ly1);
 }
 
+// The exact fp32 piece sums (integers below 2^23) back to an integer: a 256 + b 16 + c and a 16 + b. (int) of an
+// integral float is one conversion; (long long) of a float would be a ten-instruction sequence per value.
+__device__ __forceinline__ long long junta3(float a, float b, float c) {
+    return (long long)(int)a * 256 + (long long)((int)b * 16 + (int)c);
+}
+__device__ __forceinline__ long long junta2(float a, float b) { return (long long)((int)a * 16 + (int)b); }
+
 // f16 pieces of 8 int16 dS values: dS = a 256 + b 16 + c
 __device__ __forceinline__ void pedacos_ds(const s8_t& d, h8_t& a, h8_t& b, h8_t& c) {
 #pragma unroll
@@ -836,7 +843,7 @@ __global__ void __launch_bounds__(256) k_atb_mf_gq(const int8_t* __restrict__ go
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const long long gq = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
+            const long long gq = junta3(acc[dt][0][v], acc[dt][1][v], acc[dt][2][v]);
             const size_t o = (size_t)(b0 + i0 + v) * ld + h * HD + 16 * dt + lr;
             if (gq >= LIM || gq <= -LIM) reporta(E_ACUM, kid, o, gq, -5);
             Gacc[o] = (int)gq;
@@ -929,8 +936,8 @@ __global__ void __launch_bounds__(256) k_atb_mf_gkv(const int8_t* __restrict__ g
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const long long gk = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
-            const long long gvv = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+            const long long gk = junta3(ak[dt][0][v], ak[dt][1][v], ak[dt][2][v]);
+            const long long gvv = junta2(av[dt][0][v], av[dt][1][v]);
             const size_t o = (size_t)(b0 + jr + v) * ld + h * HD + 16 * dt + lr;
             if (gk >= LIM || gk <= -LIM) reporta(E_ACUM, kid, o + D, gk, -5);
             if (gvv >= LIM || gvv <= -LIM) reporta(E_ACUM, kid, o + 2 * D, gvv, -5);

@@ -640,7 +640,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)acc[dt][0][v] * 256 + (long long)acc[dt][1][v] * 16 + (long long)acc[dt][2][v];
+        for (int v = 0; v < 4; v++) mine[dt][v] = junta3(acc[dt][0][v], acc[dt][1][v], acc[dt][2][v]);
     const int ld = 3 * D;
     __syncthreads();                                                 // every wave is done with dw: parc reuses it
     if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
@@ -742,7 +742,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)ak[dt][0][v] * 256 + (long long)ak[dt][1][v] * 16 + (long long)ak[dt][2][v];
+        for (int v = 0; v < 4; v++) mine[dt][v] = junta3(ak[dt][0][v], ak[dt][1][v], ak[dt][2][v]);
     const int ld = 3 * D;
     __syncthreads();                                                 // every wave is done with dw, pw: parc reuses them
     if constexpr (BLOCO) {                                           // Gacc, Ge: int8 mantissas and exponents
@@ -750,7 +750,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) mine[dt][v] = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+            for (int v = 0; v < 4; v++) mine[dt][v] = junta2(av[dt][0][v], av[dt][1][v]);
         soma_ondas_bloco(parc, mine, wv, lr, lg, gvv);
         const int r = tid >> 4, c = 4 * (tid & 15);
         const size_t x = (size_t)(b0 + 16 * kt + r) * ld + h * 64 + c, xe = (size_t)(b0 + 16 * kt + r) * (ld / 32) + (h * 64 + c) / 32;
@@ -770,7 +770,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) mine[dt][v] = (long long)av[dt][0][v] * 16 + (long long)av[dt][1][v];
+        for (int v = 0; v < 4; v++) mine[dt][v] = junta2(av[dt][0][v], av[dt][1][v]);
     soma_ondas(parc, mine, wv, lr, lg, gvv);
 #pragma unroll
     for (int v = 0; v < 4; v++) {
