@@ -661,11 +661,13 @@ __device__ __forceinline__ void tile_xyt(long xa0, long xa1, long yb0, long yb1,
 }
 
 // The exact fp32 piece sums (integers below 2^23) back to an integer: a 256 + b 16 + c and a 16 + b. (int) of an
-// integral float is one conversion; (long long) of a float would be a ten-instruction sequence per value.
-__device__ __forceinline__ long long junta3(float a, float b, float c) {
-    return (long long)(int)a * 256 + (long long)((int)b * 16 + (int)c);
+// integral float is one conversion; (long long) of a float would be a ten-instruction sequence per value. The
+// recombined value is a sum of at most 256 terms |dS| |k| <= 4096 * 2032 (or P |dO| <= 255 * 2032), below 2^31,
+// so the 32-bit arithmetic (modular: unsigned) gives it exactly.
+__device__ __forceinline__ int junta3(float a, float b, float c) {
+    return (int)((unsigned)(int)a * 256u + (unsigned)(int)b * 16u + (unsigned)(int)c);
 }
-__device__ __forceinline__ long long junta2(float a, float b) { return (long long)((int)a * 16 + (int)b); }
+__device__ __forceinline__ int junta2(float a, float b) { return (int)((unsigned)(int)a * 16u + (unsigned)(int)b); }
 
 // f16 pieces of 8 int16 dS values: dS = a 256 + b 16 + c
 __device__ __forceinline__ void pedacos_ds(const s8_t& d, h8_t& a, h8_t& b, h8_t& c) {

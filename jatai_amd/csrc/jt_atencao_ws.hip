@@ -290,7 +290,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 //   (3a) k_atbq: gq_i = sum_j dS_ij k_j and the exponents of the q columns;
 //   (3b) k_atbkv: gk_j = sum_i dS_ij q_i, gv_j = sum_i P_ij dO_i and the exponents of the k and v columns.
 // Partial maxima sit in per-tile slots (no atomics, no clearing); the consumers reduce over the slots. The four
-// waves' partial sums are exact integers and are added in int64 through LDS.
+// waves' partial sums are exact integers below 2^31 and are added in 32 bits through LDS.
 namespace atw {
 constexpr int SLOTS = 32;            // per head and kind: T / 16 <= 32 query tiles
 struct WsB {
@@ -553,9 +553,11 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
     }
 }
 
-// sums the four waves' int64 partials parc[w][16][64] (this lane: rows 4 lg + v, column 16 dt + lr of wave wv's
-// registers) -- written by every wave, then wave wv adds column group 16 wv .. 16 wv + 15 -- into out[v]
-__device__ __forceinline__ void soma_ondas(long long (&parc)[4][16][64], const long long (&mine)[4][4], int wv, int lr, int lg, long long (&out)[4]) {
+// sums the four waves' partials parc[w][16][64] (this lane: rows 4 lg + v, column 16 dt + lr of wave wv's
+// registers) -- written by every wave, then wave wv adds column group 16 wv .. 16 wv + 15 -- into out[v]. The sums
+// are the exact integer results of at most 256 products |dS| |k| <= 4096 * 2032 (or P |dO| <= 255 * 2032), below
+// 2^31: 32-bit adds (modular, unsigned) give them exactly, as the int64 sums of the arithmetic would.
+__device__ __forceinline__ void soma_ondas(int (&parc)[4][16][64], const int (&mine)[4][4], int wv, int lr, int lg, int (&out)[4]) {
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -564,14 +566,13 @@ __device__ __forceinline__ void soma_ondas(long long (&parc)[4][16][64], const l
 #pragma unroll
     for (int v = 0; v < 4; v++) {
         const int r = 4 * lg + v, c = 16 * wv + lr;
-        out[v] = parc[0][r][c] + parc[1][r][c] + parc[2][r][c] + parc[3][r][c];
+        out[v] = (int)((unsigned)parc[0][r][c] + (unsigned)parc[1][r][c] + (unsigned)parc[2][r][c] + (unsigned)parc[3][r][c]);
     }
     __syncthreads();
 }
 
 // as soma_ondas, read back in the block layout of grava_bloco4: out[k] = row tid / 16, column 4 (tid % 16) + k
-__device__ __forceinline__ void soma_ondas_bloco(long long (&parc)[4][16][64], const long long (&mine)[4][4], int wv, int lr, int lg,
-                                                 long long (&out)[4]) {
+__device__ __forceinline__ void soma_ondas_bloco(int (&parc)[4][16][64], const int (&mine)[4][4], int wv, int lr, int lg, int (&out)[4]) {
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -579,7 +580,8 @@ __device__ __forceinline__ void soma_ondas_bloco(long long (&parc)[4][16][64], c
     __syncthreads();
     const int r = threadIdx.x >> 4, c = 4 * (threadIdx.x & 15);
 #pragma unroll
-    for (int k = 0; k < 4; k++) out[k] = parc[0][r][c + k] + parc[1][r][c + k] + parc[2][r][c + k] + parc[3][r][c + k];
+    for (int k = 0; k < 4; k++)
+        out[k] = (int)((unsigned)parc[0][r][c + k] + (unsigned)parc[1][r][c + k] + (unsigned)parc[2][r][c + k] + (unsigned)parc[3][r][c + k]);
     __syncthreads();
 }
 
@@ -587,11 +589,11 @@ template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge, int T,
                                               int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
-    // dS tiles, then (after a barrier) the waves' int64 partial sums in the same LDS: 32 KiB per workgroup, so
+    // dS tiles, then (after a barrier) the waves' 32-bit partial sums in the same LDS: 16 KiB per workgroup, so
     // every workgroup of the launch is resident at once
-    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP, sizeof(long long) * 4 * 16 * 64)];
+    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP, sizeof(int) * 4 * 16 * 64)];
     auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
-    auto& parc = *reinterpret_cast<long long (*)[4][16][64]>(lds);
+    auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     ATB_TILE_Q
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
     const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
@@ -636,7 +638,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
             acc[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, kv, acc[dt][2], 0, 0, 0);
         }
     }
-    long long mine[4][4], gq[4];
+    int mine[4][4], gq[4];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -670,12 +672,12 @@ template <int NTW, int LIMITE, bool BLOCO = false>
 __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
                                                int T, int H, int D, int dsb, int kid) {
     constexpr int LP = 16 * (NTW + 1);
-    // dS and P tiles, then (after a barrier) the waves' int64 partial sums in the same LDS: 32 KiB per workgroup,
+    // dS and P tiles, then (after a barrier) the waves' 32-bit partial sums in the same LDS: 16 KiB per workgroup,
     // so every workgroup of the launch is resident at once
-    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP + 4 * 16 * LP, sizeof(long long) * 4 * 16 * 64)];
+    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP + 4 * 16 * LP, sizeof(int) * 4 * 16 * 64)];
     auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
     auto pw = reinterpret_cast<uint8_t (*)[16][LP]>(lds + sizeof(short) * 4 * 16 * LP);
-    auto& parc = *reinterpret_cast<long long (*)[4][16][64]>(lds);
+    auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     // key tile kt pairs with the query tiles kt .. nqt - 1: decreasing work is increasing kt
     const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, kt = (int)(blockIdx.x / BH);
     const int b = bh / H, h = bh % H, b0 = b * T;
@@ -738,7 +740,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
             av[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, gv, av[dt][1], 0, 0, 0);
         }
     }
-    long long mine[4][4], gk[4], gvv[4];
+    int mine[4][4], gk[4], gvv[4];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
