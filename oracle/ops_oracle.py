@@ -247,3 +247,71 @@ class OpsOraculo:
 
 def log2i(n):
     return int(math.log2(n))
+
+
+def _plano(x):
+    if torch.is_tensor(x):
+        return [x]
+    if isinstance(x, (tuple, list)):
+        return [t for y in x for t in _plano(y)]
+    return []
+
+
+def _copia(x):
+    if torch.is_tensor(x):
+        return x.detach().cpu().clone()
+    if isinstance(x, tuple):
+        return tuple(_copia(y) for y in x)
+    if isinstance(x, list):
+        return [_copia(y) for y in x]
+    return x
+
+
+class OpsConferido:
+    """The reference's checked wrapper (jatai_cuda/ops.py:519-560): every op runs on the backend under test
+    (default: OpsHip, the HIP path) and on this oracle with the same inputs, and must agree bit for bit; the
+    backend's outputs are returned. A mismatch fails through the Registro with the op, the output, the count of
+    differing values and the first one, as ops.py:519-529 does. The oracle's inputs are copied before the
+    backend runs (momento and peso update their arguments in place); block size and the attention variant follow
+    jatai_amd.ops.BLK and ATENCAO_LIMITE at each call. A debugging aid: test infrastructure, like this module."""
+    nome = "conferido"
+    NOMES = {"rms": ["mantissa", "expoente", "r", "emax"], "atencao": ["o acc", "o exp", "P"],
+             "softmax_ce": ["g mantissa", "g expoente", "d_alvo", "soma"], "peso": ["W", "W exp", "residuo", "residuo exp"],
+             "gemm_relu2": ["h mantissa", "h expoente", "a mantissa", "a expoente"]}
+
+    def __init__(self, reg, ops=None):
+        from jatai_amd import ops as O
+        self.O, self.reg = O, reg
+        self.c = ops if ops is not None else O.OpsHip(reg)
+        self.lib = getattr(self.c, "lib", None)
+        self.n = {}
+
+    def _compara(self, op, a, b, nome):
+        a, b = a.detach().cpu(), b.detach().cpu()
+        if tuple(a.shape) != tuple(b.shape):
+            self.reg.falha(f"conferencia '{op}' / {nome}: forma HIP {tuple(a.shape)} x oraculo {tuple(b.shape)}")
+        dif = a != b
+        if not bool(dif.any()):
+            return
+        n = int(dif.sum())
+        pos = dif.nonzero()[0].tolist()
+        self.reg.falha(f"conferencia '{op}' / {nome}: {n} de {a.numel()} valores diferentes do oraculo.\n"
+                       f"  primeiro em {pos}: HIP = {a[tuple(pos)].item()}, oraculo = {b[tuple(pos)].item()}", op=op, n_dif=n, pos=pos)
+
+    def __getattr__(self, op):
+        fc = getattr(self.c, op)
+        if not callable(fc) or op.startswith("_"):
+            return fc
+
+        def f(*args, **kw):
+            r = OpsOraculo(self.O.BLK, self.O.ATENCAO_LIMITE)
+            fr = getattr(r, op)
+            ra = _copia(args)
+            out_c = fc(*args, **kw)
+            out_r = fr(*ra, **{k: v for k, v in kw.items() if k == "cru"})
+            nomes = self.NOMES.get(op, ["mantissa/acc", "expoente"])
+            for i, (a, b) in enumerate(zip(_plano(out_c), _plano(out_r))):
+                self._compara(op, a, b, nomes[i] if i < len(nomes) else f"saida {i}")
+            self.n[op] = self.n.get(op, 0) + 1
+            return out_c
+        return f

@@ -317,3 +317,47 @@ def test_gemm_soma_estocastica(blk):
             gpu.ops.lib.jt_res_estocastico(0)
         for x, y in zip(gout, ref):
             assert np.array_equal(host(x), host(y)), (ligado, primeira_diferenca(host(x), host(y)))
+
+
+def test_ops_conferido_sobre_hip():
+    """OpsConferido (the reference's checked wrapper, ops.py:532-560) around OpsHip at BLK 32: GEMM modes, quant,
+    rms and rms_back, attention forward and backward at head width 64, softmax-CE, and the in-place momento and
+    peso (whose inputs the wrapper copies for the oracle before the HIP call) all agree bit for bit with the
+    oracle; a mismatch would raise."""
+    from jatai_amd import ops as O
+    from jatai_amd.registro import Registro
+    from oracle.ops_oracle import OpsConferido
+    from backends import LOGS
+    O.BLK = 32
+    try:
+        reg = Registro(LOGS, "conferido", eco=False)
+        ops = OpsConferido(reg)
+        s = lambda t: R.substream(93, t)
+        dev = lambda T: tuple(torch.from_numpy(np.ascontiguousarray(v)).cuda() for v in T)
+        A = dev(R.bloco(s("A"), 512, 512, 32, espalha=4, e0=-6))
+        W = dev(R.bloco(s("W"), 1536, 512, 32, espalha=3, e0=-8))
+        Wo = dev(R.bloco(s("Wo"), 512, 512, 32, espalha=3, e0=-8))
+        X = dev(R.bloco(s("X"), 512, 512, 32, espalha=3, e0=1))
+        n, c = ops.rms(X)
+        qkv = ops.gemm(n, W)
+        (oacc, oe), P = ops.atencao(qkv, 2, 256, 8)
+        om = ops.quant((oacc, oe))
+        x2 = ops.gemm_soma(om, Wo, X)
+        h, _ = ops.gemm_relu2(x2, W)
+        ops.gemm_relu2_back(x2, W, h)
+        go = ops.gemm(A, Wo)
+        ops.atencao_back(go, qkv, P, 2, 256, 8)
+        ops.rms_back(go, n, c)
+        mom = dev(R.bloco(s("M"), 512, 512, 32, espalha=2, e0=-4))
+        wt = dev(R.bloco(s("Wt"), 512, 512, 32, espalha=2, e0=-6))
+        res = dev(R.bloco(s("R"), 512, 512, 32, espalha=2, e0=-14))
+        mom = ops.momento(ops.gemm(A, A, cru=True), mom)
+        ops.peso(wt, mom, res, 4, True)
+        logits = ops.gemm(A, dev(R.bloco(s("V"), 256, 512, 32, espalha=2, e0=-8)), cru=True)
+        ops.softmax_ce(logits, torch.from_numpy(R.tokens(s("alvo"), 512, 256)).cuda())
+        reg.lib = ops.lib
+        reg.confere_device()
+        assert set(ops.n) == {"rms", "gemm", "atencao", "quant", "gemm_soma", "gemm_relu2", "gemm_relu2_back", "atencao_back",
+                              "rms_back", "momento", "peso", "softmax_ce"}
+    finally:
+        O.BLK = 128

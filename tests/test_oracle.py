@@ -223,3 +223,32 @@ def test_soma_estocastica(blk):
     assert np.all(deq(ops.soma(X, Y)) == 100.0)
     media = deq(ops.soma_est(X, Y)).mean()
     assert abs(media - exato) < 0.002, media
+
+
+def test_ops_conferido_aponta_divergencia(tmp_path):
+    """OpsConferido (the reference's checked wrapper, ops.py:519-560) over a CPU backend: agreement passes the
+    backend's outputs through; a backend whose soma is off by one in a single mantissa fails with the op, the
+    output and the first differing index. The planted mistake lives in this CPU stand-in, not in any GPU code."""
+    from jatai_amd import ops as O
+    from jatai_amd.registro import ErroJatai, Registro
+    from oracle.ops_oracle import OpsConferido
+    O.BLK = 32
+    try:
+        reg = Registro(str(tmp_path), "conferido", eco=False)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+        X = (t(R.uniform_int(71, (64, 128), -100, 100).astype(np.int8)), t(R.uniform_int(72, (64, 4), -10, 5).astype(np.int8)))
+        Y = (t(R.uniform_int(73, (64, 128), -100, 100).astype(np.int8)), t(R.uniform_int(74, (64, 4), -10, 5).astype(np.int8)))
+        ok = OpsConferido(reg, OpsOraculo(32))
+        Z = ok.soma(X, Y)
+        assert np.array_equal(host(Z[0]), host(OpsOraculo(32).soma(X, Y)[0])) and ok.n == {"soma": 1}
+
+        class Torto(OpsOraculo):
+            def soma(self, A, B):
+                m, e = super().soma(A, B)
+                m = m.clone()
+                m[3, 17] += 1 if m[3, 17] < 127 else -1
+                return m, e
+        with pytest.raises(ErroJatai, match=r"conferencia 'soma' / mantissa/acc: 1 de 8192 valores[\s\S]*primeiro em \[3, 17\]"):
+            OpsConferido(reg, Torto(32)).soma(X, Y)
+    finally:
+        O.BLK = 128
