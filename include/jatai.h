@@ -49,7 +49,7 @@ int jt_gemm_divisoes(int M, int N, int K, int modo);   /* no reference counterpa
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
             int M, int N, int K, int modo, int kid);
 
-/* ---- no reference counterpart: n raw-output GEMMs sharing K, in launches of up to 48. `entradas` is a HOST array of
+/* ---- no reference counterpart: n raw-output GEMMs sharing K, in launches of up to 64. `entradas` is a HOST array of
  * n entries {const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad;} (device pointers inside); entry i
  * equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i). For the weight gradients of a step. */
 int jt_gemm_lote(const void* entradas, int n, int kid);

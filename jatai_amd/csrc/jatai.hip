@@ -165,7 +165,7 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
     return jt_gemm_f(A, EA, B, EB, Cm, CE, C32, Ce, nullptr, nullptr, nullptr, nullptr, M, N, K, modo, kid);
 }
 
-// No reference counterpart: n raw-output GEMMs sharing K in launches of up to 48 (host array of EntradaG, device
+// No reference counterpart: n raw-output GEMMs sharing K in launches of up to 64 (host array of EntradaG, device
 // pointers inside); entry i equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i).
 struct EntradaG { const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad; };
 int jt_gemm_lote(const void* entradas, int n, int kid) {

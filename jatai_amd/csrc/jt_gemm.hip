@@ -468,7 +468,8 @@ __global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4
 // Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels
 // by value in the kernel arguments; GEMM i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over
 // its (M / 32) x (N / 128) tiles. Same tiles, same arithmetic as k_gemm<BLK, 1, KS>.
-constexpr int LOTE_G = 48;
+constexpr int LOTE_G = 64;                  // 3852 bytes of kernel arguments: every weight gradient of a step in one launch
+static_assert(sizeof(int8_t*) * 6 * LOTE_G + sizeof(int) * (3 * LOTE_G + 3) <= 4096, "kernel argument limit");
 struct LoteG {
     const int8_t* A[LOTE_G];
     const int8_t* EA[LOTE_G];

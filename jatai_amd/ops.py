@@ -129,7 +129,7 @@ class OpsHip:
             self._lanca("gemm", "jt_gemm", (a, ea, b, eb, C[0], C[1], None, None, M, N, K, 0), dict(A=a, EA=ea, B=b, EB=eb), (M, N))
         return C
 
-    # no reference counterpart: many raw GEMMs sharing K in one launch (48 per launch)
+    # no reference counterpart: many raw GEMMs sharing K in one launch (64 per launch)
     def gemm_cru_lote(self, pares):
         """[gemm(A, B, cru=True, saida=S) for (A, B, S) in pares]; S may be None. Launch ids are consecutive."""
         if not pares:

@@ -3,7 +3,7 @@
 * transpoe_lote over 70 tensors of mixed shapes (two launches: 64 tensors per launch) equals transpoe of each,
   at BLK 32 and 128, and each result equals the CPU oracle's transpose;
 * the model step with batched transposes leaves weights, momenta and residuals identical to one transpoe per use;
-* gemm_cru_lote over 50 GEMMs (two launches) equals one raw gemm each, at BLK 32 and 128, and a model step
+* gemm_cru_lote over 70 GEMMs (two launches) equals one raw gemm each, at BLK 32 and 128, and a model step
   with the deferred grouped weight-gradient GEMMs equals the step with one GEMM per gradient.
 """
 import numpy as np
@@ -59,7 +59,7 @@ def test_modelo_transpostas_em_lote():
 def test_gemm_cru_lote_igual_a_gemm(blk):
     gpu = GPU(blk, vigiar=True)
     K = 512
-    formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(50)]
+    formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(70)]
     pares, ref = [], []
     for i, (M, N) in enumerate(formas):
         A = tuple(gpu.dev(a) for a in R.bloco(R.substream(8, f"A {i}"), M, K, blk, espalha=4, e0=-6))
