@@ -126,13 +126,14 @@ __device__ __forceinline__ int g_sum(int v) {
     else return g_red<LPB>(v, [](int a, int b) { return a + b; });
 }
 
-// x * 2^-s rounded half to even for any int32 x and any s, in double precision: the conversion and the
-// power-of-two scaling are exact (53-bit significand), v_rndne_f64 rounds half to even, and a scale so small
-// that the value leaves the normal range leaves it below 1/2, where the rounding gives 0 as rnd does. Four VALU
-// instructions, against about twelve for the same rounding in integer form with a per-value shift; MI355X runs
-// vector FP64 at the unpacked FP32 rate.
+// x * 2^-s rounded half to even for any int32 x and any s >= -20, in double precision: the conversion and the
+// power-of-two scaling are exact (53-bit significand); adding 1.5 * 2^52 puts the value where doubles are spaced
+// by 1, so that addition's round-to-nearest-even is rnd's, and its low word is the result in two's complement. A
+// scale so small that the value leaves the normal range leaves it below 1/2, where the rounding gives 0 as rnd
+// does. Three VALU instructions, against about twelve for the same rounding in integer form with a per-value
+// shift; MI355X runs vector FP64 at the unpacked FP32 rate.
 __device__ __forceinline__ int desl_f(int x, int s) {
-    return (int)__builtin_rint(__builtin_ldexp((double)x, -s));
+    return __double2loint(__builtin_ldexp((double)x, -s) + 0x1.8p52);
 }
 
 // Quantize one block (LPB lanes x VPL values, per-element exponent e) into mantissas of MBITS bits plus one
@@ -178,8 +179,8 @@ __device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], 
     return quant_grupo<VPL, LPB, int8_t, 7, 127>(v, e, m, kid, idx0);
 }
 
-// quant8 of values whose per-value exponents satisfy |e| <= 900 (the GEMM epilogue: e = RA + RB - 4), through
-// d = v 2^e in double precision, exact and normal for every nonzero int32 v. bitlen(|v|) + e is the binary
+// quant8 of values whose per-value exponents satisfy |e| <= 990 (the GEMM epilogue: e = RA + RB - 4), through
+// d = v 2^e in double precision, exact, normal and finite for every nonzero int32 v. bitlen(|v|) + e is the binary
 // exponent of d, so topo is read from the exponent field of the block's largest |d|. q = rnd(d 2^-E) is the low
 // word of fma(d, 2^-E, 1.5 * 2^52) (the sum lies where doubles are spaced by 1, so the FMA's rounding is the
 // half-to-even rounding), and that rounding is monotone: max |q| = rnd(max |d| 2^-E), so the bump test takes one
@@ -215,21 +216,27 @@ __device__ __forceinline__ int quant8_d(const int (&v)[VPL], const int (&e)[VPL]
 }
 
 
-// x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^30; s < 0 is a left shift the
-// caller knows to be exact): the parameters are computed once, then each value costs a shift, a bit extract, an
-// add and a shift, with no branch. s >= 31 gives 0, as rnd does for s > 30.
+// The momentum's quantization (ops.py:273-278): its per-value exponents ec = max(em + 10, eg + bitlen(g)) - 28
+// lie in [-148, eg + 4], so quant8_d applies unless a raw gradient exponent eg exceeds 950 (never from a GEMM,
+// whose raw exponents are RA + RB - 4); a group holding one takes the generic quant8.
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_mom(const int (&v)[VPL], const int (&ee)[VPL], const int (&eg)[VPL], int8_t (&m)[VPL], int kid,
+                                          long long idx0) {
+    int mx = eg[0];
+#pragma unroll
+    for (int i = 1; i < VPL; i++) mx = max(mx, eg[i]);
+    if (g_max<LPB>(mx) > 950) return quant8<VPL, LPB>(v, ee, m, kid, idx0);
+    return quant8_d<VPL, LPB>(v, ee, m, kid, idx0);
+}
+
+// x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^31; s < 0 is a left shift the
+// caller knows to be exact): the scale 2^-s is built once, then each value is fma(x, 2^-s, 1.5 * 2^52), whose
+// low word is the rounded result (the rounding of desl_f): a conversion and an FMA, with no branch. A large s
+// gives 0, as rnd does for s > 30.
 struct Desl {
-    int shl, sr, bias, w1;
-    __device__ __forceinline__ explicit Desl(int s) {
-        shl = min(max(-s, 0), 31);
-        sr = min(max(s, 0), 31);
-        bias = sr ? (1 << (sr - 1)) - 1 : 0;
-        w1 = sr ? 1 : 0;
-    }
-    __device__ __forceinline__ int operator()(int x) const {
-        const int t = (int)((unsigned)x << shl);
-        return (t + bias + (int)__builtin_amdgcn_ubfe((unsigned)t, (unsigned)sr, (unsigned)w1)) >> sr;
-    }
+    double k;
+    __device__ __forceinline__ explicit Desl(int s) { k = __hiloint2double((1023 - min(max(s, -40), 1000)) << 20, 0); }
+    __device__ __forceinline__ int operator()(int x) const { return __double2loint(__builtin_fma((double)x, k, 0x1.8p52)); }
 };
 
 // quant8 for a block whose values all share exponent e and satisfy |v| < 2^30 (the element-wise ops whose
@@ -240,41 +247,19 @@ struct Desl {
 // saturation clamp of the spec never acts). Returns E (E_ZERO for a zero block; those mantissas are 0).
 template <int VPL, int LPB, bool REPORTA = true>
 __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
-    int mx = v[0], mn = v[0];
-#pragma unroll
-    for (int i = 1; i < VPL; i++) { mx = max(mx, v[i]); mn = min(mn, v[i]); }
-    const int amax = g_max<LPB>(max(mx, -mn));
-    if (REPORTA && amax >= LIM) {
-#pragma unroll
-        for (int i = 0; i < VPL; i++)
-            if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e);
-    }
-    const int bl = bitlen(amax);
-    const int s = bl - 7 + (int)(bl > 7 && rnd_d(amax, bl - 7) > 127);
-    const int E = e + s;
-    const bool zero = bl == 0 || E < -126;
-    const Desl d(s);
-    // every value is rounded, then masked: a select per value here makes the compiler branch around the rounding
-    const int manter = zero ? 0 : -1;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) q[i] = d(v[i]) & manter;
-    if (REPORTA && !zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
-    return zero ? E_ZERO : E;
-}
-
-// Quantize a block whose values all share exponent e and are built from int8 mantissas (|v| far below 2^30): the
-// fused GEMM epilogues, as jatai_cuda.cu:161-188 does. quant8_u's rules (no sentinel reports: the callers report
-// an out-of-range exponent themselves, naming their epilogue), in double precision as quant8_d: bitlen of the
-// block's largest |v| from the exponent field of max |(double)v|, and each value rounded by one FMA with
-// 1.5 * 2^52 (exact left shifts for s <= 0, half-to-even roundings otherwise); the bump test is the rounding of
-// the largest |v| (rounding is monotone). Four VALU ops per value against seven in integer form.
-template <int VPL, int LPB>
-__device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
+    // in double precision: bitlen(max |v|) is the exponent field of max |(double)v| (exact for int32), and each
+    // value is rounded by one FMA with 1.5 * 2^52 (exact left shifts for s <= 0); the bump test is the rounding
+    // of the largest |v|
     double d[VPL], dmax = 0.0;
 #pragma unroll
     for (int i = 0; i < VPL; i++) {
         d[i] = (double)v[i];
         dmax = __builtin_fmax(dmax, __builtin_fabs(d[i]));
+    }
+    if (REPORTA && dmax >= (double)LIM) {
+#pragma unroll
+        for (int i = 0; i < VPL; i++)
+            if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e);
     }
     const int bl = g_max<LPB>((__double2hiint(dmax) >> 20) - 1022);      // bitlen(max |v|); -1022 for all zeros
     const int s0 = bl - 7;
@@ -283,10 +268,24 @@ __device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (
     const int E = e + s0 + bump;
     const double k = bump ? k0 * 0.5 : k0;
     const bool zero = bl <= 0 || E < -126;
+    // every value is rounded, then masked: a select per value here makes the compiler branch around the rounding
     const int manter = zero ? 0 : -1;
 #pragma unroll
-    for (int i = 0; i < VPL; i++) m[i] = (int8_t)(__double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter);
+    for (int i = 0; i < VPL; i++) q[i] = __double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter;
+    if (REPORTA && !zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
     return zero ? E_ZERO : E;
+}
+
+// Quantize a block whose values all share exponent e and are built from int8 mantissas (|v| far below 2^30): the
+// fused GEMM epilogues, as jatai_cuda.cu:161-188 does; quant8_u without its sentinel reports (the callers report
+// an out-of-range exponent themselves, naming their epilogue).
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_comum(const int (&v)[VPL], int e, int8_t (&m)[VPL]) {
+    int q[VPL];
+    const int E = quant8_u<VPL, LPB, false>(v, e, q, 0, 0);
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = (int8_t)q[i];
+    return E;
 }
 
 // ---------------------------------------------------------------------------------------------- stochastic rounding

@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, c
             if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    const int Eo = quant8_mom<VPL, LPB>(v, ee, eg, q, kid, o);
     grava_i8(Mm + o, q);
     if ((threadIdx.x & (LPB - 1)) == 0) ME[w] = (int8_t)Eo;
 }
@@ -328,7 +328,7 @@ __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)
             if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[NV];
-    const int Em = quant8<NV, NL>(v, ee, q, kid, o);
+    const int Em = quant8_mom<NV, NL>(v, ee, eg, q, kid, o);
     grava_i8(d.Mm + o, q);
     if (lider) d.ME[w] = (int8_t)Em;
     // peso with the new momentum: one exponent per block from here on
