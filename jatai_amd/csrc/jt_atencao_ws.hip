@@ -104,9 +104,8 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
 // output (ops.py:125-126) with the block's common exponent e.
 __device__ __forceinline__ void grava_bloco4(const int (&v)[4], int e, int8_t* __restrict__ Mm, int8_t* __restrict__ ME, size_t x, size_t xe,
                                              int kid) {
-    int ee[4] = {e, e, e, e};
     int8_t q[4];
-    const int E = quant8<4, 8>(v, ee, q, kid, (long long)x);
+    const int E = quant8_u8<4, 8>(v, e, q, kid, (long long)x);
     grava_i8(Mm + x, q);
     if ((threadIdx.x & 7) == 0) ME[xe] = (int8_t)E;
 }

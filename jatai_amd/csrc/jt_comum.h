@@ -216,17 +216,15 @@ __device__ __forceinline__ int quant8_d(const int (&v)[VPL], const int (&e)[VPL]
 }
 
 
-// The momentum's quantization (ops.py:273-278): its per-value exponents ec = max(em + 10, eg + bitlen(g)) - 28
-// lie in [-148, eg + 4], so quant8_d applies unless a raw gradient exponent eg exceeds 950 (never from a GEMM,
-// whose raw exponents are RA + RB - 4); a group holding one takes the generic quant8.
+// quant8 through quant8_d when every exponent of the group lies in [-990, 990] (the momentum's, whose exponents
+// are at least -148; the raw inputs of quant, produced by GEMMs as RA + RB - 4), else through the generic quant8.
 template <int VPL, int LPB>
-__device__ __forceinline__ int quant8_mom(const int (&v)[VPL], const int (&ee)[VPL], const int (&eg)[VPL], int8_t (&m)[VPL], int kid,
-                                          long long idx0) {
-    int mx = eg[0];
+__device__ __forceinline__ int quant8_f(const int (&v)[VPL], const int (&e)[VPL], int8_t (&m)[VPL], int kid, long long idx0) {
+    unsigned fora = 0;                                              // e + 990 as unsigned: above 1980 iff |e| > 990
 #pragma unroll
-    for (int i = 1; i < VPL; i++) mx = max(mx, eg[i]);
-    if (g_max<LPB>(mx) > 950) return quant8<VPL, LPB>(v, ee, m, kid, idx0);
-    return quant8_d<VPL, LPB>(v, ee, m, kid, idx0);
+    for (int i = 0; i < VPL; i++) fora = max(fora, (unsigned)(e[i] + 990));
+    if (g_max<LPB>((int)(fora > 1980u)) != 0) return quant8<VPL, LPB>(v, e, m, kid, idx0);
+    return quant8_d<VPL, LPB>(v, e, m, kid, idx0);
 }
 
 // x * 2^-s rounded half to even for one s shared by a group of values (|x| < 2^31; s < 0 is a left shift the
@@ -274,6 +272,16 @@ __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL
     for (int i = 0; i < VPL; i++) q[i] = __double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter;
     if (REPORTA && !zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
     return zero ? E_ZERO : E;
+}
+
+// quant8_u with int8 mantissas out (sentinels reported)
+template <int VPL, int LPB>
+__device__ __forceinline__ int quant8_u8(const int (&v)[VPL], int e, int8_t (&m)[VPL], int kid, long long idx0) {
+    int q[VPL];
+    const int E = quant8_u<VPL, LPB>(v, e, q, kid, idx0);
+#pragma unroll
+    for (int i = 0; i < VPL; i++) m[i] = (int8_t)q[i];
+    return E;
 }
 
 // Quantize a block whose values all share exponent e and are built from int8 mantissas (|v| far below 2^30): the

@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(256) k_quant(const int* __restrict__ acc, cons
     le_i32(acc + o, v);
     le_i16(e + o, ee);
     int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    const int Eo = quant8_f<VPL, LPB>(v, ee, q, kid, o);
     grava_i8(m + o, q);
     if ((threadIdx.x & (LPB - 1)) == 0) E[w] = (int8_t)Eo;
 }
@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(256) k_momento(const int* __restrict__ gacc, c
             if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[VPL];
-    const int Eo = quant8_mom<VPL, LPB>(v, ee, eg, q, kid, o);
+    const int Eo = quant8_f<VPL, LPB>(v, ee, q, kid, o);
     grava_i8(Mm + o, q);
     if ((threadIdx.x & (LPB - 1)) == 0) ME[w] = (int8_t)Eo;
 }
@@ -172,13 +172,11 @@ template <int BLK>
 __global__ void __launch_bounds__(256) k_para8(const int16_t* __restrict__ xm, const int8_t* __restrict__ xE, int8_t* __restrict__ ym,
                                                int8_t* __restrict__ yE, long long nblocos, int kid) {
     ELEM_PROLOGO
-    int v[VPL], ee[VPL];
+    int v[VPL];
     le_i16(xm + o, v);
     const int ex = xE[w];
-#pragma unroll
-    for (int i = 0; i < VPL; i++) ee[i] = ex;
     int8_t q[VPL];
-    const int Eo = quant8<VPL, LPB>(v, ee, q, kid, o);
+    const int Eo = quant8_u8<VPL, LPB>(v, ex, q, kid, o);            // one exponent per block
     grava_i8(ym + o, q);
     if ((threadIdx.x & (LPB - 1)) == 0) yE[w] = (int8_t)Eo;
 }
@@ -328,7 +326,7 @@ __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)
             if (g[i] >= LIM || g[i] <= -LIM) reporta(E_ACUM, kid, o + i, g[i], eg[i]);
     }
     int8_t q[NV];
-    const int Em = quant8_mom<NV, NL>(v, ee, eg, q, kid, o);
+    const int Em = quant8_f<NV, NL>(v, ee, q, kid, o);
     grava_i8(d.Mm + o, q);
     if (lider) d.ME[w] = (int8_t)Em;
     // peso with the new momentum: one exponent per block from here on

@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
         ee[i] = ec + sh2 - k - (emax - G / 2);
     }
     int8_t q[VPR];
-    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    const int Eo = quant8_d<VPR, LPB>(v, ee, q, kid, o);            // |ee| < 600
     if constexpr (SOMA) {                                            // z = soma(x, dx): ec = max(xE, E) - 21
         const int ec2 = max(ex, Eo) - 21;
         const Desl da(ec2 - ex), dq(ec2 - Eo);
@@ -127,16 +127,15 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
     s = g_sum<LPR>(s);
     if (s <= 0) { if (lr == 0) reporta(E_DIV, kid, (long long)row * V, s, umax); s = 1; }
     const int inv = s > 256 ? div_exata(1 << 28, s) : (1 << 28) / s;   // s >= 4095 (exp(0) >> 3 of the row maximum): 2^28 / s < 2^20
-    int v[VPR], ee[VPR];
+    int v[VPR];
 #pragma unroll
     for (int i = 0; i < VPR; i++) {
         const int col = lr * VPR + i;
         v[i] = ((ex[i] * inv + (1 << 15)) >> 16) - (col == t ? 4096 : 0);
-        ee[i] = -12 - log2M;
         if (col == t) d_alvo[row] = umax - u[i];
     }
     int8_t q[VPR];
-    const int Eo = quant8<VPR, LPB>(v, ee, q, kid, o);
+    const int Eo = quant8_u8<VPR, LPB>(v, -12 - log2M, q, kid, o);   // one exponent per row
     grava_i8(gm + o, q);
     if ((lr & (LPB - 1)) == 0) gE[(long long)row * nb + lr / LPB] = (int8_t)Eo;
     if (lr == 0) soma_o[row] = s;
@@ -179,7 +178,7 @@ __device__ __forceinline__ void transpoe_tile(const int8_t* __restrict__ X, cons
         const int col = c0 + 4 * cg + cc;
         const long long o = (long long)col * R + r0 + rc * 8;
         int8_t q[8];
-        const int E = quant8<8, LPB>(m[cc], e, q, kid, o);
+        const int E = quant8_d<8, LPB>(m[cc], e, q, kid, o);           // int8 exponents
         grava_i8(Y + o, q);
         if ((rc & (LPB - 1)) == 0) EY[(size_t)col * (R / BLK) + (r0 + rc * 8) / BLK] = (int8_t)E;
     }
