@@ -92,9 +92,9 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
     {
         int v[16];
         abre_i8(rv, v);
-        const int sv = emv - evt;
+        const Desl dv(emv - evt);                                    // rnd(v << GA, emv - evt), one shift per block
 #pragma unroll
-        for (int k = 0; k < 16; k++) w.vt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), sv);
+        for (int k = 0; k < 16; k++) w.vt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)dv(shl(v[k], GA));
     }
 }
 
@@ -167,6 +167,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 #pragma unroll
     for (int v = 0; v < 4; v++) { lq[v][0] = qL[4 * lg + v][0]; lq[v][1] = qL[4 * lg + v][1]; }
     const long long idx = (long long)(b0 + i0) * D + h * HD;
+    const Desl dsu(su);                                              // the scores' rounding shift, one per head
     int uu[NTW][4], mx[4] = {U_MIN, U_MIN, U_MIN, U_MIN};
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
@@ -179,7 +180,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
         for (int v = 0; v < 4; v++) {
             const int i = i0 + v;
             const int s = shl(p0[v], lq[v][0] + lk0) + shl(p1[v], lq[v][1] + lk1);
-            const int r = su >= 0 ? rnd_d(s, su) : rnd(s, su, kid, idx);
+            const int r = su >= 0 ? dsu(s) : rnd(s, su, kid, idx);
             const int u = j <= i ? r - ((i - j) << incl) : U_MIN;
             uu[n][v] = u;
             mx[v] = max(mx[v], u);
@@ -404,12 +405,13 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         int v[16];
         abre_i8(rg, v);
         const int s = emg - egt;
+        const Desl ds(s);
         int8_t m8[16];
         int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
-            const int al = rnd_d(shl(v[k], GA), s);
+            const int al = ds(shl(v[k], GA));
             amax = max(amax, abs(al));
             w.gt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)al;
         }
@@ -420,12 +422,13 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         int v[16];
         abre_i8(rv, v);
         const int s = emv - evt;
+        const Desl ds(s);
         int8_t m8[16];
         int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
-            if (LIMITE) v1 += abs(rnd_d(shl(v[k], GA), s));
+            if (LIMITE) v1 += abs(ds(shl(v[k], GA)));
         }
         grava_i8(w.vm8 + tt * 64 + 16 * c4, m8);
         if ((c4 & 1) == 0) w.vL[tt * 2 + half] = (int8_t)L;
@@ -434,10 +437,10 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     for (int x = 0; x < 2; x++) {   // q (x = 0), k (x = 1): aligned f16, transposed
         int v[16];
         abre_i8(x ? rk : rq, v);
-        const int s = (x ? emk : emq) - (x ? ekt : eqt);
+        const Desl ds((x ? emk : emq) - (x ? ekt : eqt));
         _Float16* dst = x ? w.kt : w.qt;
 #pragma unroll
-        for (int k = 0; k < 16; k++) dst[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)rnd_d(shl(v[k], GA), s);
+        for (int k = 0; k < 16; k++) dst[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)ds(shl(v[k], GA));
     }
     if (LIMITE) {
         v1 = quad_soma(v1);
@@ -499,6 +502,7 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
     __shared__ int sred[4][16];
     ATB_TILE_Q
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T);
+    const Desl dsh(sh);                                              // gP's shrink, one shift per head
     const FragQ f = frag_q(w, hb, qt, lr, lg);
     const uint8_t* Pb = P + (size_t)bh * T * T;
     int x[NTW][4];
@@ -513,7 +517,7 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
         pr[n] = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);     // P_ij, rows i0 .. i0 + 3
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int xv = j <= i0 + v ? rnd_d(o[v], sh) : 0;
+            const int xv = j <= i0 + v ? dsh(o[v]) : 0;
             const int p = (pr[n] >> (8 * v)) & 255;
             x[n][v] = xv;
             s[v] += p * xv;
@@ -595,6 +599,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
     auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     ATB_TILE_Q
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const Desl dsh(sh), dsh2(sh2);                                   // gP's and dS's shrinks, one shift each per head
     const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
     const int eds = ego + ev + sh - 9 + sh2;
     const FragQ f = frag_q(w, hb, qt, lr, lg);
@@ -612,7 +617,7 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int p = (pr >> (8 * v)) & 255;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? rnd_d(p * (rnd_d(o[v], sh) - sl[v]), sh2) : 0);
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? dsh2(p * (dsh(o[v]) - sl[v])) : 0);
         }
     }
     if (nv & 1)
@@ -684,6 +689,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
     const size_t hb = (size_t)bh * T;
     const int nv = (nqt - kt - wv + 3) / 4;                          // this wave's query tiles kt + wv + 4 n, n < nv
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const Desl dsh(sh), dsh2(sh2);                                   // gP's and dS's shrinks, one shift each per head
     const int ego = w.mx[bh * 4], eq = w.mx[bh * 4 + 1], ev = w.mx[bh * 4 + 3];
     const int eds = ego + ev + sh - 9 + sh2;
     // v fragments of the tile's 16 keys as the A operand (rows = keys)
@@ -707,7 +713,7 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
         for (int v = 0; v < 4; v++) {
             const int j = jr + v;
             const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? rnd_d(p * (rnd_d(o[v], sh) - sl), sh2) : 0);
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? dsh2(p * (dsh(o[v]) - sl)) : 0);
             pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)p;
         }
     }
