@@ -135,14 +135,30 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     }
     // shift tables of K-blocks b0 .. b0 + nbc - 1 from the staged exponent bytes (rows of nbc bytes); then the
     // stage buffers are free again
+    // A thread's row r = tid % 32 and column c = tid % 128 are the same in every iteration, so their maxima are read
+    // once; the exponent bytes of U iterations are read before any table entry is written (the writes could alias
+    // the reads for the compiler, which would otherwise wait on every read).
     auto desloca_tab = [&](int nbc) {
-        for (int i = tid; i < BM * nbc; i += 256 * KS) {            // i = b * BM + r
-            const int r = i & (BM - 1), b = i >> 5;
-            na_s[i] = max((int)st_s[r * nbc + b] + 4 - ra_s[r], -100);
+        const int r = tid & (BM - 1), c = tid & (BN - 1);
+        const int ra4 = 4 - ra_s[r], rbn = -rb_s[c];
+        const int8_t* ea = st_s + r * nbc;
+        const int8_t* eb = st_s + (BM + c) * nbc;
+        constexpr int U = 4, SA = 8 * KS, SB = 2 * KS;
+        for (int b0 = tid >> 5; b0 < nbc; b0 += U * SA) {           // entries b * BM + r
+            int e[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) e[u] = b0 + u * SA < nbc ? (int)ea[b0 + u * SA] : 0;
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (b0 + u * SA < nbc) na_s[(b0 + u * SA) * BM + r] = max(e[u] + ra4, -100);
         }
-        for (int i = tid; i < BN * nbc; i += 256 * KS) {            // i = b * BN + c
-            const int c = i & (BN - 1), b = i >> 7;
-            nb_s[i] = (int8_t)max((int)st_s[(BM + c) * nbc + b] - rb_s[c], -100);
+        for (int b0 = tid >> 7; b0 < nbc; b0 += 2 * U * SB) {       // entries b * BN + c
+            int e[2 * U];
+#pragma unroll
+            for (int u = 0; u < 2 * U; u++) e[u] = b0 + u * SB < nbc ? (int)eb[b0 + u * SB] : 0;
+#pragma unroll
+            for (int u = 0; u < 2 * U; u++)
+                if (b0 + u * SB < nbc) nb_s[(b0 + u * SB) * BN + c] = (int8_t)max(e[u] + rbn, -100);
         }
         __syncthreads();
     };
