@@ -40,19 +40,25 @@ inline Ws parte(void* base, long long BH, int T) {
 }
 }
 
+// Largest block exponent of the 64 / blk blocks of a head slice in one token's exponent row e (column c0): at
+// BLK = 32 the slice's two bytes in one 2-byte load (c0 / 32 is even), at BLK = 128 its one byte.
+__device__ __forceinline__ int emx_fatia(const int8_t* e, int c0, int blk) {
+    if (blk == 32) {
+        const int x = *reinterpret_cast<const short*>(e + c0 / 32);
+        return max((int)(int8_t)x, x >> 8);
+    }
+    return (int)e[c0 / blk];
+}
+
 // Largest block exponents of three head slices (columns c0 + [0, 64) of E, one per slice) over the T tokens of
-// sequence b0 / T: one pass and one workgroup reduction (256 threads).
+// sequence b0 / T: one token per thread (T <= 512: at most two), one workgroup reduction (256 threads).
 __device__ __forceinline__ void emx3(const int8_t* E, int ld, int ca, int cb, int cc, int blk, int b0, int T, int (&red)[3][4], int& a, int& b,
                                      int& c) {
-    const int r = threadIdx.x & 3, nbl = ld / blk, ba = (ca + 16 * r) / blk, bb = (cb + 16 * r) / blk, bc = (cc + 16 * r) / blk;
+    const int nbl = ld / blk;
     int ma = SEM_TOPO, mb = SEM_TOPO, mc = SEM_TOPO;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {                                    // T <= 512: all loads issued together
-        const int t = (threadIdx.x >> 2) + 64 * k;
-        if (t < T) {
-            const int8_t* e = E + (size_t)(b0 + t) * nbl;
-            ma = max(ma, (int)e[ba]); mb = max(mb, (int)e[bb]); mc = max(mc, (int)e[bc]);
-        }
+    for (int t = threadIdx.x; t < T; t += 256) {
+        const int8_t* e = E + (size_t)(b0 + t) * nbl;
+        ma = max(ma, emx_fatia(e, ca, blk)); mb = max(mb, emx_fatia(e, cb, blk)); mc = max(mc, emx_fatia(e, cc, blk));
     }
     ma = g_max<64>(ma); mb = g_max<64>(mb); mc = g_max<64>(mc);
     if ((threadIdx.x & 63) == 0) { red[0][threadIdx.x >> 6] = ma; red[1][threadIdx.x >> 6] = mb; red[2][threadIdx.x >> 6] = mc; }
@@ -62,10 +68,23 @@ __device__ __forceinline__ void emx3(const int8_t* E, int ld, int ca, int cb, in
     c = max(max(red[2][0], red[2][1]), max(red[2][2], red[2][3]));
 }
 
+// The workgroup's 64 tokens x 64 dimensions of a transposed f16 array ([BH][64][T]), staged in LDS by the threads
+// that converted them, written out as 16-byte chunks of each dimension's 128-byte row segment (two per thread)
+// instead of sixteen scattered 2-byte stores per thread. Call after a barrier that follows the tile's writes.
+typedef _Float16 TileT[64][72];                                      // rows padded to 144 bytes (16-byte aligned)
+__device__ __forceinline__ void grava_t64(const TileT& tile, _Float16* __restrict__ cab, int T, int t0) {
+#pragma unroll
+    for (int x = threadIdx.x; x < 64 * 8; x += 256) {
+        const int row = x >> 3, ch = x & 7;
+        *reinterpret_cast<int4*>(cab + (size_t)row * T + t0 + 8 * ch) = *reinterpret_cast<const int4*>(&tile[row][8 * ch]);
+    }
+}
+
 __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, int T, int H, int D,
                                                   int blk, int GA) {
     constexpr int HD = 64;
     __shared__ int red[3][4];
+    __shared__ __align__(16) TileT tv;
     const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, nbl = ld / blk, tid = threadIdx.x;
     // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t; its k and v values are loaded before the head
@@ -94,8 +113,10 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         abre_i8(rv, v);
         const Desl dv(emv - evt);                                    // rnd(v << GA, emv - evt), one shift per block
 #pragma unroll
-        for (int k = 0; k < 16; k++) w.vt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)dv(shl(v[k], GA));
+        for (int k = 0; k < 16; k++) tv[16 * c4 + k][tid >> 2] = (_Float16)dv(shl(v[k], GA));
     }
+    __syncthreads();
+    grava_t64(tv, w.vt + (size_t)bh * 64 * T, T, part * 64);
 }
 
 // NTW = key tiles a wave can own (T / 64)
@@ -362,6 +383,7 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     constexpr int HD = 64;
     __shared__ int red[4][4];
     __shared__ int red1[4];
+    __shared__ __align__(16) TileT tg, tq, tk;
     const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, tid = threadIdx.x, nbl = ld / blk, nbg = D / blk;
     // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t. Every value it converts is loaded first, so the
@@ -376,17 +398,13 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     // head maxima of the q, k, v and dO exponents in one reduction
     int emq, emk, emv, emg;
     {
-        const int r = tid & 3, ba = (h * HD + 16 * r) / blk, bb = (D + h * HD + 16 * r) / blk, bc = (2 * D + h * HD + 16 * r) / blk;
-        const int bg = (h * HD + 16 * r) / blk;
         int m[4] = {SEM_TOPO, SEM_TOPO, SEM_TOPO, SEM_TOPO};
-#pragma unroll
-        for (int k = 0; k < 8; k++) {                                // T <= 512: all loads issued together
-            const int tk = (tid >> 2) + 64 * k;
-            if (tk < T) {
-                const int8_t* e = qE + (size_t)(b0 + tk) * nbl;
-                m[0] = max(m[0], (int)e[ba]); m[1] = max(m[1], (int)e[bb]); m[2] = max(m[2], (int)e[bc]);
-                m[3] = max(m[3], (int)goE[(size_t)(b0 + tk) * nbg + bg]);
-            }
+        for (int tk = tid; tk < T; tk += 256) {                      // one token per thread (T <= 512: at most two)
+            const int8_t* e = qE + (size_t)(b0 + tk) * nbl;
+            m[0] = max(m[0], emx_fatia(e, h * HD, blk));
+            m[1] = max(m[1], emx_fatia(e, D + h * HD, blk));
+            m[2] = max(m[2], emx_fatia(e, 2 * D + h * HD, blk));
+            m[3] = max(m[3], emx_fatia(goE + (size_t)(b0 + tk) * nbg, h * HD, blk));
         }
 #pragma unroll
         for (int x = 0; x < 4; x++) m[x] = g_max<64>(m[x]);
@@ -413,7 +431,7 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
             const int al = ds(shl(v[k], GA));
             amax = max(amax, abs(al));
-            w.gt[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)al;
+            tg[16 * c4 + k][tid >> 2] = (_Float16)al;
         }
         grava_i8(w.gm8 + tt * 64 + 16 * c4, m8);
         if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
@@ -438,10 +456,14 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         int v[16];
         abre_i8(x ? rk : rq, v);
         const Desl ds((x ? emk : emq) - (x ? ekt : eqt));
-        _Float16* dst = x ? w.kt : w.qt;
+        TileT& dst = x ? tk : tq;
 #pragma unroll
-        for (int k = 0; k < 16; k++) dst[((size_t)bh * 64 + 16 * c4 + k) * T + t] = (_Float16)ds(shl(v[k], GA));
+        for (int k = 0; k < 16; k++) dst[16 * c4 + k][tid >> 2] = (_Float16)ds(shl(v[k], GA));
     }
+    __syncthreads();
+    grava_t64(tg, w.gt + (size_t)bh * 64 * T, T, part * 64);
+    grava_t64(tq, w.qt + (size_t)bh * 64 * T, T, part * 64);
+    grava_t64(tk, w.kt + (size_t)bh * 64 * T, T, part * 64);
     if (LIMITE) {
         v1 = quad_soma(v1);
         const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
