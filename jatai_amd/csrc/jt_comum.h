@@ -243,8 +243,8 @@ struct Desl {
 // so max |q| = rnd(max |v|, E - e) and the overflow test (any |q| > 127 -> E + 1) is decided on the block
 // maximum before any value is rounded. Each value is then rounded once, and no |q| exceeds 127 (so the
 // saturation clamp of the spec never acts). Returns E (E_ZERO for a zero block; those mantissas are 0).
-template <int VPL, int LPB, bool REPORTA = true>
-__device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
+template <int VPL, int LPB, bool REPORTA = true, int MBITS = 7, int LIMQ = 127>
+__device__ __forceinline__ int quant_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
     // in double precision: bitlen(max |v|) is the exponent field of max |(double)v| (exact for int32), and each
     // value is rounded by one FMA with 1.5 * 2^52 (exact left shifts for s <= 0); the bump test is the rounding
     // of the largest |v|
@@ -260,9 +260,9 @@ __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL
             if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e);
     }
     const int bl = g_max<LPB>((__double2hiint(dmax) >> 20) - 1022);      // bitlen(max |v|); -1022 for all zeros
-    const int s0 = bl - 7;
+    const int s0 = bl - MBITS;
     const double k0 = __hiloint2double((1023 - s0) << 20, 0);            // 2^-s0
-    const int bump = g_max<LPB>(__double2loint(__builtin_fma(dmax, k0, 0x1.8p52))) > 127;
+    const int bump = g_max<LPB>(__double2loint(__builtin_fma(dmax, k0, 0x1.8p52))) > LIMQ;
     const int E = e + s0 + bump;
     const double k = bump ? k0 * 0.5 : k0;
     const bool zero = bl <= 0 || E < -126;
@@ -272,6 +272,10 @@ __device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL
     for (int i = 0; i < VPL; i++) q[i] = __double2loint(__builtin_fma(d[i], k, 0x1.8p52)) & manter;
     if (REPORTA && !zero && E > 126) reporta(E_EXP, kid, idx0, E, e + bl);
     return zero ? E_ZERO : E;
+}
+template <int VPL, int LPB, bool REPORTA = true>
+__device__ __forceinline__ int quant8_u(const int (&v)[VPL], int e, int (&q)[VPL], int kid, long long idx0) {
+    return quant_u<VPL, LPB, REPORTA, 7, 127>(v, e, q, kid, idx0);
 }
 
 // quant8_u with int8 mantissas out (sentinels reported)
