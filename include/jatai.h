@@ -100,6 +100,9 @@ int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void*
                      const void* xE, void* om, void* oE, int M, int D, int log2D, int G, int GB, int kid);
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V,
                   int log2M, int kid);
+/* no reference counterpart: the loss of modelo.py:93, mean over M rows of d_alvo / 256 + ln(soma / 4096) (int32 rows from
+ * jt_softmax_ce), as one float64 written to out, in one launch on the library's stream */
+int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid);
 
 /* ---- causal ALiBi attention, T % 64 == 0, T <= 256 (jatai_cuda.cu:1177-1194) */
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid);

@@ -458,6 +458,14 @@ int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, vo
     return fim();
 }
 
+// No reference counterpart: the loss mean(d / 256 + ln(s / 4096)) (modelo.py:93) into one float64, one launch.
+int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid) {
+    (void)kid;
+    if (M <= 0 || !d_alvo || !soma || !out || !alinhados(d_alvo, soma, out)) return (int)hipErrorInvalidValue;
+    k_perda<<<1, 1024, 0, g_stream>>>((const int*)d_alvo, (const int*)soma, (double*)out, M);
+    return fim();
+}
+
 // ---------------------------------------------------------------------------------------------- attention
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
     if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;

@@ -211,3 +211,22 @@ __global__ void __launch_bounds__(2 * TR) k_transpoe_lote(const LoteT L, int kid
     const int local = t - L.ini[i], ntx = L.C[i] / 64;
     transpoe_tile<BLK, TR>(L.X[i], L.EX[i], L.Y[i], L.EY[i], L.R[i], L.C[i], local % ntx, local / ntx, kid + i);
 }
+
+// The training loss from softmax_ce's per-row integers: mean over rows of d / 256 + ln(s / 4096) in float64
+// (modelo.py:93). One workgroup; each term is the same float64 expression, summed in a fixed order (per thread,
+// then across the wave, then the 16 wave sums in order).
+__global__ void __launch_bounds__(1024) k_perda(const int* __restrict__ d, const int* __restrict__ s, double* __restrict__ out, int M) {
+    __shared__ double ondas[16];
+    double t = 0.0;
+    for (int i = threadIdx.x; i < M; i += 1024) t += (double)d[i] / 256 + log((double)s[i] / 4096);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+    if ((threadIdx.x & 63) == 0) ondas[threadIdx.x >> 6] = t;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double u = 0.0;
+#pragma unroll
+        for (int w = 0; w < 16; w++) u += ondas[w];
+        out[0] = u / M;
+    }
+}

@@ -31,8 +31,11 @@ def zeros_como(t):
     return torch.zeros_like(t[0]), torch.full_like(t[1], O.E_ZERO)
 
 
-def perda_de(d_alvo, soma):
-    """Cross-entropy in nats from the integer softmax outputs: mean(d/256 + ln(s/4096)) in float64 (modelo.py:93)."""
+def perda_de(d_alvo, soma, ops=None):
+    """Cross-entropy in nats from the integer softmax outputs: mean(d/256 + ln(s/4096)) in float64 (modelo.py:93);
+    with `ops` (an ops object with `perda`), in its one launch instead of torch's six."""
+    if ops is not None:
+        return ops.perda(d_alvo, soma)
     return (d_alvo.double() / 256 + torch.log(soma.double() / 4096)).mean()
 
 
@@ -75,6 +78,8 @@ class Modelo:
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
         # the residual update of the backward, soma(gx, rms_back(...)), in one launch
         self.rms_soma = hasattr(ops, "rms_back_soma")
+        # the loss in one launch of the library (float64 sums in another order than torch's mean: equal to 1e-15)
+        self.perda_fundida = hasattr(ops, "perda")
         self._gbuf, self._tabela = None, None
 
     def _otim_no_gemm(self):
@@ -134,7 +139,7 @@ class Modelo:
                 nf, cf = ops.rms(ops.para8(x16) if r16 else x)
                 logits = ops.gemm(nf, p["out"], cru=True)
                 g, d_alvo, soma = ops.softmax_ce(logits, alvo)
-        perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma)
+        perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma, ops if self.perda_fundida else None)
         if k_lr is None:
             return perda
         prontas = {}
@@ -245,8 +250,9 @@ class PassoGravado:
     def __init__(self, modelo, Bt, T, k_lr):
         self.m, self.reg, self.k_lr = modelo, modelo.reg, k_lr
         lib = modelo.ops.lib
-        self.tok = torch.zeros(Bt, T, dtype=torch.long, device=modelo.dev)
-        self.alvo = torch.zeros(Bt, T, dtype=torch.long, device=modelo.dev)
+        # int32, the kernels' token type: the replay's copy_ converts, and the graph holds no conversion
+        self.tok = torch.zeros(Bt, T, dtype=torch.int32, device=modelo.dev)
+        self.alvo = torch.zeros(Bt, T, dtype=torch.int32, device=modelo.dev)
         self.grafo = torch.cuda.CUDAGraph()
         est, vig, pi = modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira
         modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = False, False, True
@@ -258,7 +264,7 @@ class PassoGravado:
             with torch.cuda.graph(self.grafo):
                 lib.jt_stream(torch.cuda.current_stream().cuda_stream)
                 self.d_alvo, self.soma = modelo.passo(self.tok, self.alvo, k_lr=k_lr)
-                self.perda = perda_de(self.d_alvo, self.soma)     # in the graph, as modelo.py:170 captures passo's loss
+                self.perda = perda_de(self.d_alvo, self.soma, modelo.ops if modelo.perda_fundida else None)     # in the graph, as modelo.py:170 captures passo's loss
         finally:
             lib.jt_stream(None)
             modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = est, vig, pi

@@ -33,7 +33,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
            "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
-           "jt_rms_back_soma")
+           "jt_rms_back_soma", "jt_perda")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -465,6 +465,16 @@ class OpsHip:
         self._lanca("softmax_ce", "jt_softmax_ce", (acc, e, alvo, g[0], g[1], d, s, M, V, int(math.log2(M))),
                     dict(acc=acc, e=e, alvo=alvo), (M, V))
         return g, d, s
+
+    # no reference counterpart: the loss of modelo.py:93 from softmax_ce's rows in one launch
+    def perda(self, d_alvo, soma):
+        """mean(d_alvo / 256 + ln(soma / 4096)) in float64, a 0-dim tensor on the device."""
+        M = d_alvo.shape[0] if d_alvo.dim() == 1 else -1
+        self.reg.exige(d_alvo.dtype == torch.int32 and soma.dtype == torch.int32 and d_alvo.dim() == 1 and soma.shape == d_alvo.shape
+                       and M > 0 and d_alvo.is_contiguous() and soma.is_contiguous(), "perda: d_alvo e soma int32 [M] contiguos")
+        out = torch.empty((), dtype=torch.float64, device=d_alvo.device)
+        self._lanca("perda", "jt_perda", (d_alvo, soma, out, M), dict(d_alvo=d_alvo, soma=soma), (M,))
+        return out
 
     # ---------------------------------------------------------------- optimizer, in place (ops.py:504-515)
     def momento(self, Gc, Mom):

@@ -30,7 +30,7 @@ def test_passo_r16_vs_oraculo():
         cpu = CS.Gravador(OpsOraculo(32), host)
         mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg, r16=True)
         mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub(), r16=True)
-        mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.rms_soma = False
+        mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.rms_soma = mg.perda_fundida = False
         mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg, r16=True)
         for p in range(2):
             x = R.tokens(R.substream(37, f"r16 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
@@ -47,7 +47,7 @@ def test_passo_r16_vs_oraculo():
             for k, (a, b) in enumerate(zip(gpu.log, cpu.log)):
                 assert list(a) == list(b), f"step {p}, op #{k} '{b[0]}' differs from the oracle"
             assert abs(pg - pc) <= 1e-12 * abs(pc)
-            assert pf == pg
+            assert abs(pf - pg) <= 1e-14 * abs(pg)     # the fused model's loss sums in another order
         est = lambda m: [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
         assert est(mf) == est(mg), "fused R16 step differs from the op-by-op step"
         pgraf = PassoGravado(mf, Bt, T, 4)
@@ -58,7 +58,7 @@ def test_passo_r16_vs_oraculo():
         torch.cuda.synchronize()
         reg.fim_passo()
         b = float(mg.passo(tok, alvo, k_lr=4))
-        assert a == b
+        assert abs(a - b) <= 1e-14 * abs(b)
         assert est(mf) == est(mg), "graph-replayed fused R16 step differs from the eager op-by-op step"
     finally:
         O.BLK = 128

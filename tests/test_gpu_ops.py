@@ -361,3 +361,20 @@ def test_ops_conferido_sobre_hip():
                               "rms_back", "momento", "peso", "softmax_ce"}
     finally:
         O.BLK = 128
+
+
+@pytest.mark.parametrize("M", [1, 2048, 16384, 100003])
+def test_perda(M):
+    """The loss in one launch: against torch's float64 form on the same rows (other summation order: equal to a
+    few ulps) and against the correctly rounded sum of the same float64 terms (math.fsum)."""
+    import math
+    gpu = GPU(32)
+    rng = np.random.default_rng(M)
+    d = rng.integers(0, 4096, M, dtype=np.int32)
+    s = rng.integers(4096, 4096 * 256, M, dtype=np.int32)
+    out = gpu.ops.perda(torch.from_numpy(d).cuda(), torch.from_numpy(s).cuda())
+    x = float(out)
+    ref = float((torch.from_numpy(d).double() / 256 + torch.log(torch.from_numpy(s).double() / 4096)).mean())
+    exato = math.fsum(float(a) / 256 + math.log(float(b) / 4096) for a, b in zip(d, s)) / M
+    assert out.dtype == torch.float64 and out.dim() == 0
+    assert abs(x - ref) <= 1e-14 * abs(ref) and abs(x - exato) <= 1e-14 * abs(exato), (x, ref, exato)
