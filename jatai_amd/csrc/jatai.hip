@@ -346,10 +346,11 @@ int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, 
 // No reference counterpart: n transposes in launches of up to 64 (host array of EntradaT, device pointers inside).
 // Each entry equals jt_transpoe(X, EX, Y, EY, R, C, kid + i).
 struct EntradaT { const void* X; const void* EX; void* Y; void* EY; int R; int C; };
+constexpr int TPW_T = 2;                         // tiles per workgroup of the batched transpose
 int jt_transpoe_lote(const void* entradas, int n, int kid) {
     if (n < 0 || (n > 0 && !entradas)) return (int)hipErrorInvalidValue;
     const EntradaT* e = (const EntradaT*)entradas;
-    const int TR = g_blk == 32 ? 64 : 128;
+    const int TR = 128;                          // 128-row tiles at both BLK: each column's output is a 128-byte line
     for (int base = 0; base < n; base += LOTE_T) {
         LoteT L;
         L.n = std::min(LOTE_T, n - base);
@@ -365,8 +366,9 @@ int jt_transpoe_lote(const void* entradas, int n, int kid) {
         if (tot > 0x7fffffff) return (int)hipErrorInvalidValue;
         L.ini[L.n] = (int)tot;
         if (tot == 0) continue;
-        if (g_blk == 32) k_transpoe_lote<32, 64><<<(unsigned)tot, 128, 0, g_stream>>>(L, kid + base);
-        else k_transpoe_lote<128, 128><<<(unsigned)tot, 256, 0, g_stream>>>(L, kid + base);
+        const unsigned wg = (unsigned)((tot + TPW_T - 1) / TPW_T);
+        if (g_blk == 32) k_transpoe_lote<32, 128, TPW_T><<<wg, 256, 0, g_stream>>>(L, kid + base);
+        else k_transpoe_lote<128, 128, TPW_T><<<wg, 256, 0, g_stream>>>(L, kid + base);
         const int r = fim();
         if (r) return r;
     }

@@ -184,8 +184,9 @@ __device__ __forceinline__ int quant8(const int (&v)[VPL], const int (&e)[VPL], 
 // exponent of d, so topo is read from the exponent field of the block's largest |d|. q = rnd(d 2^-E) is the low
 // word of fma(d, 2^-E, 1.5 * 2^52) (the sum lies where doubles are spaced by 1, so the FMA's rounding is the
 // half-to-even rounding), and that rounding is monotone: max |q| = rnd(max |d| 2^-E), so the bump test takes one
-// FMA per lane instead of a pass over the values. Same results and sentinels as quant8.
-template <int VPL, int LPB>
+// FMA per lane instead of a pass over the values. Same results and sentinels as quant8. CHECA = false drops the
+// accumulator-range sentinel for callers whose values are int8 mantissas (|v| <= 128 < LIM: it cannot fire).
+template <int VPL, int LPB, bool CHECA = true>
 __device__ __forceinline__ int quant8_d(const int (&v)[VPL], const int (&e)[VPL], int8_t (&m)[VPL], int kid, long long idx0) {
     double d[VPL], dmax = 0.0;
     unsigned fora = 0;                                              // max of v + LIM - 1 as unsigned: >= 2 LIM - 1 iff |v| >= LIM
@@ -193,9 +194,9 @@ __device__ __forceinline__ int quant8_d(const int (&v)[VPL], const int (&e)[VPL]
     for (int i = 0; i < VPL; i++) {
         d[i] = __builtin_ldexp((double)v[i], e[i]);
         dmax = __builtin_fmax(dmax, __builtin_fabs(d[i]));
-        fora = max(fora, (unsigned)v[i] + (unsigned)(LIM - 1));
+        if constexpr (CHECA) fora = max(fora, (unsigned)v[i] + (unsigned)(LIM - 1));
     }
-    if (fora >= 2u * LIM - 1) {
+    if (CHECA && fora >= 2u * LIM - 1) {
 #pragma unroll
         for (int i = 0; i < VPL; i++)
             if (v[i] >= LIM || v[i] <= -LIM) reporta(E_ACUM, kid, idx0 + i, v[i], e[i]);

@@ -147,21 +147,28 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
 // Lane (cg, rc) owns 4 columns (one 32-bit LDS word) x 8 rows: it reads 8 words, unpacks 32 values and runs 4
 // block quantizations side by side; the LPB = BLK/8 lanes of a column block are consecutive lanes. Rows of the
 // LDS tile are 17 words long so the word reads spread over the banks.
+// One tile's global loads (row tid / 2, half tid % 2: 32 bytes and the exponent byte of those 32 columns), kept in
+// registers so a workgroup can issue the loads of several tiles before it stages the first.
+struct CargaT {
+    int4 v0, v1;
+    int e;
+};
 template <int BLK, int TR>
-__device__ __forceinline__ void transpoe_tile(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
-                                              int8_t* __restrict__ EY, int R, int C, int bx, int by, int kid) {
+__device__ __forceinline__ CargaT transpoe_carga(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int C, int bx, int by) {
+    const int row = threadIdx.x >> 1, half = threadIdx.x & 1, r0 = by * TR, c0 = bx * 64;
+    const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
+    return CargaT{src[0], src[1], (int)EX[(size_t)(r0 + row) * (C / BLK) + (c0 + half * 32) / BLK]};
+}
+template <int BLK, int TR>
+__device__ __forceinline__ void transpoe_tile(const CargaT& cg_, int (&tile)[TR][17], int8_t (&er)[TR][2], int8_t* __restrict__ Y,
+                                              int8_t* __restrict__ EY, int R, int bx, int by, int kid) {
     constexpr int LPB = BLK / 8, RC = TR / 8;
-    __shared__ int tile[TR][17];
-    __shared__ int8_t er[TR][2];
-    const int r0 = by * TR, c0 = bx * 64, tid = threadIdx.x, nbx = C / BLK;
+    const int r0 = by * TR, c0 = bx * 64, tid = threadIdx.x;
     {
         const int row = tid >> 1, half = tid & 1;
-        const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
-        const int4 v0 = src[0], v1 = src[1];
         int* d = &tile[row][half * 8];
-        d[0] = v0.x; d[1] = v0.y; d[2] = v0.z; d[3] = v0.w; d[4] = v1.x; d[5] = v1.y; d[6] = v1.z; d[7] = v1.w;
-        // exponent of columns [c0 + 32 half, c0 + 32 half + 32)
-        er[row][half] = EX[(size_t)(r0 + row) * nbx + (c0 + half * 32) / BLK];
+        d[0] = cg_.v0.x; d[1] = cg_.v0.y; d[2] = cg_.v0.z; d[3] = cg_.v0.w; d[4] = cg_.v1.x; d[5] = cg_.v1.y; d[6] = cg_.v1.z; d[7] = cg_.v1.w;
+        er[row][half] = (int8_t)cg_.e;
     }
     __syncthreads();
     const int cg = tid / RC, rc = tid % RC;                         // columns c0 + 4 cg .. +3, rows r0 + 8 rc .. +7
@@ -178,7 +185,7 @@ __device__ __forceinline__ void transpoe_tile(const int8_t* __restrict__ X, cons
         const int col = c0 + 4 * cg + cc;
         const long long o = (long long)col * R + r0 + rc * 8;
         int8_t q[8];
-        const int E = quant8_d<8, LPB>(m[cc], e, q, kid, o);           // int8 exponents
+        const int E = quant8_d<8, LPB, false>(m[cc], e, q, kid, o);    // int8 mantissas and exponents
         grava_i8(Y + o, q);
         if ((rc & (LPB - 1)) == 0) EY[(size_t)col * (R / BLK) + (r0 + rc * 8) / BLK] = (int8_t)E;
     }
@@ -187,12 +194,15 @@ __device__ __forceinline__ void transpoe_tile(const int8_t* __restrict__ X, cons
 template <int BLK, int TR>
 __global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
                                                      int8_t* __restrict__ EY, int R, int C, int kid) {
-    transpoe_tile<BLK, TR>(X, EX, Y, EY, R, C, blockIdx.x, blockIdx.y, kid);
+    __shared__ int tile[TR][17];
+    __shared__ int8_t er[TR][2];
+    transpoe_tile<BLK, TR>(transpoe_carga<BLK, TR>(X, EX, C, blockIdx.x, blockIdx.y), tile, er, Y, EY, R, blockIdx.x, blockIdx.y, kid);
 }
 
 // Many transposes in one launch. The tensor list travels by value in the kernel arguments (no device table, so
-// a captured graph keeps it); tensor i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over its
-// (R / TR) x (C / 64) tiles.
+// a captured graph keeps it); tensor i owns the tiles [ini_i, ini_{i+1}) of the list, row-major over its
+// (R / TR) x (C / 64) tiles, and workgroup w takes tiles TPW w .. TPW w + TPW - 1 (of any tensors): it issues
+// every tile's loads first, then stages and writes them one by one, each in its own LDS buffer.
 constexpr int LOTE_T = 64;
 struct LoteT {
     const int8_t* X[LOTE_T];
@@ -203,13 +213,25 @@ struct LoteT {
     int n;
 };
 
-template <int BLK, int TR>
+template <int BLK, int TR, int TPW>
 __global__ void __launch_bounds__(2 * TR) k_transpoe_lote(const LoteT L, int kid) {
-    const int t = blockIdx.x;
-    int i = 0;                                                      // uniform: kernel arguments, scalar loads
-    while (i + 1 < L.n && L.ini[i + 1] <= t) i++;
-    const int local = t - L.ini[i], ntx = L.C[i] / 64;
-    transpoe_tile<BLK, TR>(L.X[i], L.EX[i], L.Y[i], L.EY[i], L.R[i], L.C[i], local % ntx, local / ntx, kid + i);
+    __shared__ int tile[TPW][TR][17];
+    __shared__ int8_t er[TPW][TR][2];
+    int ti[TPW], bx[TPW], by[TPW];
+    CargaT c[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int t = min(blockIdx.x * TPW + j, L.ini[L.n] - 1);   // past the list's end: a copy of the last tile, not stored
+        int i = 0;                                                  // uniform: kernel arguments, scalar loads
+        while (i + 1 < L.n && L.ini[i + 1] <= t) i++;
+        const int local = t - L.ini[i], ntx = L.C[i] / 64;
+        ti[j] = i; bx[j] = local % ntx; by[j] = local / ntx;
+        c[j] = transpoe_carga<BLK, TR>(L.X[i], L.EX[i], L.C[i], bx[j], by[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+        if (j == 0 || (int)blockIdx.x * TPW + j < L.ini[L.n])
+            transpoe_tile<BLK, TR>(c[j], tile[j], er[j], L.Y[ti[j]], L.EY[ti[j]], L.R[ti[j]], bx[j], by[j], kid + ti[j]);
 }
 
 // The training loss from softmax_ce's per-row integers: mean over rows of d / 256 + ln(s / 4096) in float64
