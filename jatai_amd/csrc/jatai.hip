@@ -623,8 +623,7 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
         k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                              \
         if (!LM) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                                          \
         k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \
-        k_atbq<NTW, LM, B><<<gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);                    \
-        k_atbkv<NTW, LM, B><<<gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);                   \
+        k_atbqkv<NTW, LM, B><<<2 * gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);              \
     }
 #define VAR(B) { if (T <= 256) { if (limite) FASES(4, 1, B) else FASES(4, 0, B) } else { if (limite) FASES(8, 1, B) else FASES(8, 0, B) } }
     if (bloco) VAR(true) else VAR(false)

@@ -491,8 +491,9 @@ __device__ __forceinline__ void gp_tile(const atw::WsB& w, size_t hb, const Frag
              f.lx, w.vL[j * 2], w.vL[j * 2 + 1], o);
 }
 // query tile of this workgroup, in decreasing work across all heads (tile qt pairs with qt + 1 key tiles)
-#define ATB_TILE_Q                                                                                                     \
-    const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, qt = nqt - 1 - (int)(blockIdx.x / BH);          \
+#define ATB_TILE_Q ATB_TILE_Q_(blockIdx.x, gridDim.x)
+#define ATB_TILE_Q_(BX, GX)                                                                                            \
+    const int nqt = T / 16, BH = (GX) / nqt, bh = (BX) % BH, qt = nqt - 1 - (int)((BX) / BH);                          \
     const int b = bh / H, h = bh % H, b0 = b * T;                                                                      \
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4; \
     const size_t hb = (size_t)bh * T;                                                                                  \
@@ -610,16 +611,15 @@ __device__ __forceinline__ void soma_ondas_bloco(int (&parc)[4][16][64], const i
     __syncthreads();
 }
 
+// gq of workgroup blk of nblk. lds: dS tiles, then (after a barrier) the waves' 32-bit partial sums in the same
+// LDS (LDS_ATBQKV bytes).
 template <int NTW, int LIMITE, bool BLOCO = false>
-__global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge, int T,
-                                              int H, int D, int dsb, int kid) {
+__device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
+                                           int T, int H, int D, int dsb, int kid, char* lds, const int blk, const int nblk) {
     constexpr int LP = 16 * (NTW + 1);
-    // dS tiles, then (after a barrier) the waves' 32-bit partial sums in the same LDS: 16 KiB per workgroup, so
-    // every workgroup of the launch is resident at once
-    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP, sizeof(int) * 4 * 16 * 64)];
     auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
     auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
-    ATB_TILE_Q
+    ATB_TILE_Q_(blk, nblk)
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
     const Desl dsh(sh), dsh2(sh2);                                   // gP's and dS's shrinks, one shift each per head
     const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
@@ -694,18 +694,18 @@ __global__ void __launch_bounds__(256) k_atbq(atw::WsB w, const uint8_t* __restr
     }
 }
 
+// gk, gv of workgroup blk of nblk. lds: dS and P tiles, then (after a barrier) the waves' 32-bit partial sums in
+// the same LDS (LDS_ATBQKV bytes).
+template <int NTW> constexpr size_t LDS_ATBQKV = cmax_(sizeof(short) * 4 * 16 * 16 * (NTW + 1) + 4 * 16 * 16 * (NTW + 1), sizeof(int) * 4 * 16 * 64);
 template <int NTW, int LIMITE, bool BLOCO = false>
-__global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
-                                               int T, int H, int D, int dsb, int kid) {
+__device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
+                                            int T, int H, int D, int dsb, int kid, char* lds, const int blk, const int nblk) {
     constexpr int LP = 16 * (NTW + 1);
-    // dS and P tiles, then (after a barrier) the waves' 32-bit partial sums in the same LDS: 16 KiB per workgroup,
-    // so every workgroup of the launch is resident at once
-    __shared__ __align__(16) char lds[cmax_(sizeof(short) * 4 * 16 * LP + 4 * 16 * LP, sizeof(int) * 4 * 16 * 64)];
     auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
     auto pw = reinterpret_cast<uint8_t (*)[16][LP]>(lds + sizeof(short) * 4 * 16 * LP);
     auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     // key tile kt pairs with the query tiles kt .. nqt - 1: decreasing work is increasing kt
-    const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, kt = (int)(blockIdx.x / BH);
+    const int nqt = T / 16, BH = nblk / nqt, bh = blk % BH, kt = (int)(blk / BH);
     const int b = bh / H, h = bh % H, b0 = b * T;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4;
     const size_t hb = (size_t)bh * T;
@@ -811,4 +811,16 @@ __global__ void __launch_bounds__(256) k_atbkv(atw::WsB w, const uint8_t* __rest
         Ge[o + D] = (int16_t)(eds + eq);
         Ge[o + 2 * D] = (int16_t)(ego - 8);
     }
+}
+
+// gk, gv (workgroups [0, G)) and gq (workgroups [G, 2G)) of the backward in one launch. Both read only what
+// k_atb_prep and k_atb2 wrote and write disjoint columns of G, so their latency-bound workgroups run side by side
+// (16 KiB of LDS and at most 64 VGPRs each: all 2G workgroups of config 4 are resident at once).
+template <int NTW, int LIMITE, bool BLOCO = false>
+__global__ void __launch_bounds__(256) k_atbqkv(atw::WsB w, const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
+                                                int T, int H, int D, int dsb, int kid) {
+    __shared__ __align__(16) char lds[LDS_ATBQKV<NTW>];
+    const int G = (int)gridDim.x / 2;
+    if ((int)blockIdx.x < G) atbkv_corpo<NTW, LIMITE, BLOCO>(w, P, Gacc, Ge, T, H, D, dsb, kid, lds, (int)blockIdx.x, G);
+    else atbq_corpo<NTW, LIMITE, BLOCO>(w, P, Gacc, Ge, T, H, D, dsb, kid, lds, (int)blockIdx.x - G, G);
 }
