@@ -400,7 +400,7 @@ int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
     switch (LEN) {                                                           \
         case 128: K3(4, 32); break;                                          \
         case 256: K3(4, 64); break;                                          \
-        case 512: K3(8, 64); break;                                          \
+        case 512: K3(16, 32); break;                                         \
         case 1024: K3(16, 64); break;                                        \
         default: return (int)hipErrorInvalidValue;                           \
     }
