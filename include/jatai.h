@@ -91,7 +91,8 @@ int jt_entrada_t_bytes(void);          /* sizeof of one entry (40) */
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid);
 int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid);
 
-/* ---- rows, D and V in {128, 256, 512, 1024} (jatai_cuda.cu:1167-1176, 1195-1200) */
+/* ---- rows (jatai_cuda.cu:1167-1176, 1195-1200): rms / rms_back take any D <= 1024 that is a multiple of BLK
+ * (ops.py:453), softmax_ce any V <= 1024 that is a multiple of 128 (ops.py:496) */
 int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid);
 int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om,
                 void* oE, int M, int D, int log2D, int G, int GB, int kid);
@@ -104,7 +105,9 @@ int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, vo
  * jt_softmax_ce), as one float64 written to out, in one launch on the library's stream */
 int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid);
 
-/* ---- causal ALiBi attention, T % 64 == 0, T <= 256 (jatai_cuda.cu:1177-1194) */
+/* ---- causal ALiBi attention (jatai_cuda.cu:1177-1194). Head width D / H = 4, the reference's: T % 32 == 0,
+ * T <= 256 (the reference: T <= 128), H <= 64, ALiBi slope 8 - h / 8 (ops.py:208, 475). No reference counterpart:
+ * head widths 16, 32, 64 with T % 64 == 0, T <= 512 and slope 8 - 8h / H. */
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid);
 /* no reference counterpart: jt_atencao with a caller workspace of jt_atencao_ws_bytes(Bt, T, H, D) bytes (16-byte
  * aligned); same outputs. At head width 64 on matrix cores (T <= 512) k and v are converted once per (sequence,

@@ -8,6 +8,9 @@
 // state (stream, block size, tuning knobs) is global and not thread-safe.
 //
 // One translation unit: the kernels and the device error record `g_erro` live in the same code object.
+#include <algorithm>
+#include <type_traits>
+
 #include "jt_comum.h"
 #include "jt_elem.hip"
 #include "jt_linhas.hip"
@@ -395,69 +398,89 @@ int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
 }
 
 // ---------------------------------------------------------------------------------------------- rows
-// one row per LPR lanes with VPR values each: D (or V) in {128, 256, 512, 1024}
-#define POR_LINHA(LEN, K3)                                                   \
-    switch (LEN) {                                                           \
-        case 128: K3(4, 32); break;                                          \
-        case 256: K3(4, 64); break;                                          \
-        case 512: K3(16, 32); break;                                         \
-        case 1024: K3(16, 64); break;                                        \
-        default: return (int)hipErrorInvalidValue;                           \
+// One row per LP lanes with VP values each. The widths 128, 256, 512 and 1024 have layouts of their own; any other
+// multiple of BLK up to 1024 (the reference's domain: ops.py:453 for rms, ops.py:496 for softmax_ce) runs with 16
+// values per lane on the next power of two of lanes, the lanes past the row idle (CH = false).
+}  // extern "C"
+template <int VP_, int LP_, bool CH_>
+struct FormaLinha { static constexpr int VP = VP_, LP = LP_; static constexpr bool CH = CH_; };
+// Calls f(FormaLinha<...>{}, integral_constant BLK) for the layout of a row of `len` values; false if len is not
+// a multiple of BLK in (0, 1024].
+template <class F>
+static bool por_linha(int len, F&& f) {
+    if (len <= 0 || len > 1024 || len % g_blk) return false;
+    auto blk = [&](auto fm) {
+        using FM = decltype(fm);
+        if (g_blk == 32) f(fm, std::integral_constant<int, 32>{});
+        else if constexpr (128 / FM::VP <= FM::LP) f(fm, std::integral_constant<int, 128>{});   // a block in LP lanes
+    };
+    switch (len) {
+        case 128: blk(FormaLinha<4, 32, true>{}); return true;
+        case 256: blk(FormaLinha<4, 64, true>{}); return true;
+        case 512: blk(FormaLinha<16, 32, true>{}); return true;
+        case 1024: blk(FormaLinha<16, 64, true>{}); return true;
     }
+    int l = std::max(2, g_blk / 16);
+    while (l * 16 < len) l *= 2;
+    switch (l) {
+        case 2: blk(FormaLinha<16, 2, false>{}); break;
+        case 4: blk(FormaLinha<16, 4, false>{}); break;
+        case 8: blk(FormaLinha<16, 8, false>{}); break;
+        case 16: blk(FormaLinha<16, 16, false>{}); break;
+        case 32: blk(FormaLinha<16, 32, false>{}); break;
+        default: blk(FormaLinha<16, 64, false>{}); break;
+    }
+    return true;
+}
+static unsigned grade_linhas(int M, int LP) { return (unsigned)((M + 256 / LP - 1) / (256 / LP)); }
+extern "C" {
+
 int jt_rms(const void* Xm, const void* XE, void* Ym, void* YE, void* cr, void* cemax, int M, int D, int log2D, int G, int kid) {
-    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (M <= 0) return (int)hipErrorInvalidValue;
     if (!alinhados(Xm, XE, Ym, YE, cr, cemax)) return (int)hipErrorInvalidValue;
-#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                               \
-        if (g_blk == 32) k_rms<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE, \
-                                                                     (int*)cr, (int*)cemax, M, log2D, G, kid);                       \
-        else k_rms<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE,             \
-                                                           (int*)cr, (int*)cemax, M, log2D, G, kid); }
-    POR_LINHA(D, K3)
-#undef K3
-    return fim();
+    const bool ok = por_linha(D, [&](auto fm, auto bl) {
+        using FM = decltype(fm);
+        k_rms<FM::VP, FM::LP, decltype(bl)::value, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+            (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Ym, (int8_t*)YE, (int*)cr, (int*)cemax, M, log2D, G, kid, D);
+    });
+    return ok ? fim() : (int)hipErrorInvalidValue;
 }
 int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, void* om, void* oE, int M,
                 int D, int log2D, int G, int GB, int kid) {
-    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (M <= 0) return (int)hipErrorInvalidValue;
     if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE)) return (int)hipErrorInvalidValue;
-#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                       \
-        if (g_blk == 32) k_rms_back<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,             \
-            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid);                          \
-        else k_rms_back<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,                        \
-            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid); }
-    POR_LINHA(D, K3)
-#undef K3
-    return fim();
+    const bool ok = por_linha(D, [&](auto fm, auto bl) {
+        using FM = decltype(fm);
+        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, false, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+            (const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym, (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om,
+            (int8_t*)oE, M, log2D, G, GB, kid, nullptr, nullptr, 0, D);
+    });
+    return ok ? fim() : (int)hipErrorInvalidValue;
 }
 // No reference counterpart: soma(x, rms_back(g, y, cache)) in one launch (the backward's residual update); equals
 // jt_rms_back into a temporary then jt_soma(x, temporary). Launch ids: kid for the rms_back part, kid + 1 for soma.
 int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, const void* xm,
                      const void* xE, void* om, void* oE, int M, int D, int log2D, int G, int GB, int kid) {
-    if (M <= 0 || D % g_blk) return (int)hipErrorInvalidValue;
+    if (M <= 0) return (int)hipErrorInvalidValue;
     if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE) || !alinhados(xm, xE)) return (int)hipErrorInvalidValue;
-#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                       \
-        if (g_blk == 32) k_rms_back<VP, LP, 32, true><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,       \
-            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm,         \
-            (const int8_t*)xE, kid + 1);                                                                                                     \
-        else k_rms_back<VP, LP, 128, true><<<g, 256, 0, g_stream>>>((const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym,                  \
-            (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om, (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm,         \
-            (const int8_t*)xE, kid + 1); }
-    POR_LINHA(D, K3)
-#undef K3
-    return fim();
+    const bool ok = por_linha(D, [&](auto fm, auto bl) {
+        using FM = decltype(fm);
+        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, true, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+            (const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym, (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om,
+            (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm, (const int8_t*)xE, kid + 1, D);
+    });
+    return ok ? fim() : (int)hipErrorInvalidValue;
 }
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V, int log2M,
                   int kid) {
-    if (M <= 0 || V % g_blk) return (int)hipErrorInvalidValue;
+    if (M <= 0 || V % 128) return (int)hipErrorInvalidValue;
     if (!alinhados(acc, e, alvo, gm, gE, d_alvo, soma)) return (int)hipErrorInvalidValue;
-#define K3(VP, LP) { const unsigned g = (unsigned)((M + 256 / LP - 1) / (256 / LP));                                                    \
-        if (g_blk == 32) k_softmax_ce<VP, LP, 32><<<g, 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (const int*)alvo,           \
-            (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid);                                                           \
-        else k_softmax_ce<VP, LP, 128><<<g, 256, 0, g_stream>>>((const int*)acc, (const int16_t*)e, (const int*)alvo,                     \
-            (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid); }
-    POR_LINHA(V, K3)
-#undef K3
-    return fim();
+    const bool ok = por_linha(V, [&](auto fm, auto bl) {
+        using FM = decltype(fm);
+        k_softmax_ce<FM::VP, FM::LP, decltype(bl)::value, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+            (const int*)acc, (const int16_t*)e, (const int*)alvo, (int8_t*)gm, (int8_t*)gE, (int*)d_alvo, (int*)soma, M, log2M, kid, V);
+    });
+    return ok ? fim() : (int)hipErrorInvalidValue;
 }
 
 // No reference counterpart: the loss mean(d / 256 + ln(s / 4096)) (modelo.py:93) into one float64, one launch.
@@ -469,19 +492,27 @@ int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid) {
 }
 
 // ---------------------------------------------------------------------------------------------- attention
+// Shapes: head width 4 (the reference's, jatai_cuda.cu:1176-1187 with ops.py:475) takes T a multiple of 32 up to
+// 256 and H <= 64 (the ALiBi schedule 8 - h // 8 of ops.py:208); head widths 16, 32, 64 (no reference
+// counterpart) take T a multiple of 64 up to 512.
+static bool atencao_forma(int Bt, int T, int H, int D) {
+    if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return false;
+    if (D / H == 4) return T % 32 == 0 && T <= 256 && H <= 64;
+    return T % 64 == 0 && T <= 512;
+}
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd == 4) {
-        if (T > 256) return (int)hipErrorInvalidValue;
+        const int nt = (T + 63) & ~63;                   // whole waves; threads past T only join the reductions
         if (T <= 128)
-            k_atencao4<128><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+            k_atencao4<128><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
         else
-            k_atencao4<256><<<Bt * H, T, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+            k_atencao4<256><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
         return fim();
     }
-    if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
+    if ((hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
     const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
     if (hd == 64 && g_atencao_mfma) {                // matrix-core forward (scores kept in registers: T <= 256)
         const size_t Tk = (size_t)T, lds_mf = Tk * 64 + ((Tk * 2 + 15) & ~(size_t)15) + 64 * Tk * 2 + 4 * 16 * Tk * 2;
@@ -523,7 +554,7 @@ static int atencao_ws(const void* qm, const void* qE, void* O1, void* O2, void* 
 }
 int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
                   long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, kid);
     return atencao_ws(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, ws, ws_bytes, false, kid);
 }
@@ -538,24 +569,24 @@ int jt_atencao_ws_q(const void* qm, const void* qE, void* Om, void* OE, void* P,
 }
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
     if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);
     if (hd == 4) {
-        if (T > 256) return (int)hipErrorInvalidValue;
+        const int nt = (T + 63) & ~63;
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
         if (T <= 128) {
-            if (limite) k_atencao4_back<128, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
-            else k_atencao4_back<128, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+            if (limite) k_atencao4_back<128, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS);
+            else k_atencao4_back<128, 0><<<Bt * H, nt, 0, g_stream>>>(ARGS);
         } else {
-            if (limite) k_atencao4_back<256, 1><<<Bt * H, T, 0, g_stream>>>(ARGS);
-            else k_atencao4_back<256, 0><<<Bt * H, T, 0, g_stream>>>(ARGS);
+            if (limite) k_atencao4_back<256, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS);
+            else k_atencao4_back<256, 0><<<Bt * H, nt, 0, g_stream>>>(ARGS);
         }
 #undef ARGS
         return fim();
     }
-    if (T > 512 || (hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
+    if ((hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
     const unsigned g = (unsigned)(Bt * H * (T / hd::QB));
     if (hd == 64 && g_atencao_mfma && T <= 256) {        // matrix-core backward: 5 launches
         const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
@@ -633,7 +664,7 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
 }
 int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
                        int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
     return atencao_back_ws(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, ws, ws_bytes, false, kid);
 }

@@ -1,9 +1,10 @@
 // Causal ALiBi attention at head width 4 (the spec's shape, ops.py:186-258): one workgroup per
-// (sequence, head), one thread per query row i (T <= 256 threads).
+// (sequence, head), one thread per query row i. T is a multiple of 32 up to 256; the workgroup has T rounded up
+// to whole waves of 64 threads, and the threads past T take part in the reductions with neutral values only.
 //
 // Forward: q, k, v of the head aligned to the head's largest exponent over the sequence with GA guard bits
 // (a = rnd(m << GA, emx - e)); u_ij = rnd(q_i . k_j, -(eq + ek - 1 + 8)) - (i - j) << incl with
-// incl = 8 - 8h/H; ex = exp_int(max - u) >> 3; P = min((ex * (2^28 / sum ex) + 2^19) >> 20, 255) as uint8,
+// incl = 8 - h // 8 (ops.py:208; H <= 64); ex = exp_int(max - u) >> 3; P = min((ex * (2^28 / sum ex) + 2^19) >> 20, 255) as uint8,
 // stored transposed [j][i]; o_i = sum_j P_ij v_j (raw, exponent ev - 8).
 // Backward: gP = dO . v^T shrunk to 15 bits by its causal maximum (or an upper bound in the LIMITE variant),
 // s_i = rnd(sum_j P gP, 8), dS = P (gP - s) shrunk to DSB bits, then gq = dS k, gk = dS^T q, gv = P^T dO
@@ -20,15 +21,17 @@ __device__ __forceinline__ int bloco_max(int v, int* red) {
     return r;
 }
 
-// aligned values of this thread's token for one head slice of 4 columns (jatai_cuda.cu:789-818 restated)
-__device__ __forceinline__ void alinha4(const int8_t* m, const int8_t* E, int ld, int col, int blk, int b0, int GA, int* red,
+// aligned values of this thread's token for one head slice of 4 columns (jatai_cuda.cu:789-818 restated);
+// a thread past the sequence (t >= T) loads nothing and holds zeros
+__device__ __forceinline__ void alinha4(const int8_t* m, const int8_t* E, int ld, int col, int blk, int b0, int T, int GA, int* red,
                                         int (*al)[4], int& eo) {
     const int t = threadIdx.x;
-    const int e = E[(size_t)(b0 + t) * (ld / blk) + col / blk];
+    const bool ativo = t < T;
+    const int e = ativo ? (int)E[(size_t)(b0 + t) * (ld / blk) + col / blk] : SEM_TOPO;
     const int emx = bloco_max(e, red);
-    const int w = *reinterpret_cast<const int*>(m + (size_t)(b0 + t) * ld + col);
+    const int w = ativo ? *reinterpret_cast<const int*>(m + (size_t)(b0 + t) * ld + col) : 0;
 #pragma unroll
-    for (int d = 0; d < 4; d++) al[t][d] = rnd_d(((w << (24 - 8 * d)) >> 24) << GA, emx - e);
+    for (int d = 0; d < 4; d++) al[t][d] = ativo ? rnd_d(((w << (24 - 8 * d)) >> 24) << GA, emx - e) : 0;
     eo = emx - GA;
 }
 
@@ -40,12 +43,13 @@ __global__ void __launch_bounds__(TMAX) k_atencao4(const int8_t* __restrict__ qm
     __shared__ int red[TMAX / 64];
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     int eq, ek, ev;
-    alinha4(qm, qE, ld, h * 4, blk, b0, GA, red, qa, eq);
-    alinha4(qm, qE, ld, D + h * 4, blk, b0, GA, red, ka, ek);
-    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, GA, red, va, ev);
+    alinha4(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
+    alinha4(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
+    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
     __syncthreads();
-    const int su = -(eq + ek - 1 + 8), incl = 8 - (8 * h) / H;
+    const int su = -(eq + ek - 1 + 8), incl = 8 - h / 8;
     const int i = threadIdx.x, row = b0 + i;
+    if (i >= T) return;                                             // no barrier follows
     const int q0 = qa[i][0], q1 = qa[i][1], q2 = qa[i][2], q3 = qa[i][3];
     const long long idx = (long long)row * D + h * 4;
     auto sc = [&](int j) {
@@ -89,12 +93,14 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     const uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
     int eq, ek, ev, ego;
-    alinha4(gom, goE, D, h * 4, blk, b0, GA, red, goa, ego);
-    alinha4(qm, qE, ld, h * 4, blk, b0, GA, red, qa, eq);
-    alinha4(qm, qE, ld, D + h * 4, blk, b0, GA, red, ka, ek);
-    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, GA, red, va, ev);
+    alinha4(gom, goE, D, h * 4, blk, b0, T, GA, red, goa, ego);
+    alinha4(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
+    alinha4(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
+    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
     __syncthreads();
-    const int i = threadIdx.x;
+    // threads past the sequence stay for the barriers of the reductions: their row loops are empty (ie = -1),
+    // their aligned values zero, and they write nothing
+    const int i = threadIdx.x, ie = i < T ? i : -1;
     const int g0 = goa[i][0], g1 = goa[i][1], g2 = goa[i][2], g3 = goa[i][3];
     auto gp_ij = [&](int j) { return g0 * va[j][0] + g1 * va[j][1] + g2 * va[j][2] + g3 * va[j][3]; };
     // shift of gP: exact causal maximum, or max_i ||dO_i||_inf * max_j ||v_j||_1
@@ -104,13 +110,13 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         const int b2 = abs(va[i][0]) + abs(va[i][1]) + abs(va[i][2]) + abs(va[i][3]);
         mg = bloco_max(b1, red) * bloco_max(b2, red);
     } else {
-        for (int j = 0; j <= i; j++) mg = max(mg, abs(gp_ij(j)));
+        for (int j = 0; j <= ie; j++) mg = max(mg, abs(gp_ij(j)));
         mg = bloco_max(mg, red);
     }
     const int sh = max(bitlen(mg) - 15, 0), egp = ego + ev + sh;
     // s_i = rnd(sum_j P_ij gP'_ij, 8)
     int s = 0, pm = 0, gm = 0;
-    for (int j = 0; j <= i; j++) {
+    for (int j = 0; j <= ie; j++) {
         const int p = Pb[(size_t)j * T + i], gp = rnd_d(gp_ij(j), sh);
         s += p * gp;
         if constexpr (LIMITE) { pm = max(pm, p); gm = max(gm, abs(gp)); }
@@ -124,18 +130,19 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         const int pmb = bloco_max(pm, red), gmb = bloco_max(gm, red), smb = bloco_max(abs(sl), red);
         md = pmb * (gmb + smb);
     } else {
-        for (int j = 0; j <= i; j++) md = max(md, abs((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(j), sh) - sl)));
+        for (int j = 0; j <= ie; j++) md = max(md, abs((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(j), sh) - sl)));
         md = bloco_max(md, red);                                   // also publishes slin
     }
     const int sh2 = max(bitlen(md) - DSB, 0), eds = egp - 9 + sh2;
     // rows: gq_i = sum_j dS_ij k_j
     {
         int gq[4] = {0, 0, 0, 0};
-        for (int j = 0; j <= i; j++) {
+        for (int j = 0; j <= ie; j++) {
             const int ds = rnd_d((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(j), sh) - sl), sh2);
 #pragma unroll
             for (int d = 0; d < 4; d++) gq[d] += ds * ka[j][d];
         }
+        if (ie < 0) return;                                         // no barrier follows
 #pragma unroll
         for (int d = 0; d < 4; d++) {
             const size_t o = (size_t)(b0 + i) * ld + h * 4 + d;

@@ -1,28 +1,36 @@
-// Row kernels: rms, rms_back, softmax_ce (one row per LPR consecutive lanes, VPR values per lane,
-// LPR * VPR = row length), and transpoe (128 x 64 byte tiles through LDS).
+// Row kernels: rms, rms_back, softmax_ce (one row per LPR consecutive lanes, VPR values per lane), and transpoe
+// (128 x 64 byte tiles through LDS). CHEIO: the row length is LPR * VPR. Otherwise it is Dr (a multiple of BLK
+// below LPR * VPR, for the widths that are not powers of two): the lanes past Dr load and store nothing and join
+// the row's reductions with neutral values (0 for sums, the smallest exponent for maxima).
 #include "jt_comum.h"
 
 // ---------------------------------------------------------------------------------------------- RMSNorm
 // Y = quant(x * 2^k / r, e_b - k - emax + G/2), with ss = sum_b rnd(sum(m^2) << G, 2 (emax - e_b)),
 // r = isqrt(ss >> log2 D), k = bitlen(r) + 10. Caches (r, emax) per row (ops.py:153-165).
-template <int VPR, int LPR, int BLK>
+template <int VPR, int LPR, int BLK, bool CHEIO = true>
 __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, const int8_t* __restrict__ XE, int8_t* __restrict__ Ym,
                                              int8_t* __restrict__ YE, int* __restrict__ cr, int* __restrict__ cemax, int M, int log2D,
-                                             int G, int kid) {
-    constexpr int D = VPR * LPR, nb = D / BLK, LPB = BLK / VPR;
+                                             int G, int kid, int Dr = 0) {
+    constexpr int LPB = BLK / VPR;
+    const int D = CHEIO ? VPR * LPR : Dr, nb = D / BLK;
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
     if (row >= M) return;
+    const bool ativo = CHEIO || lr * VPR < D;
     const long long o = (long long)row * D + lr * VPR;
     int x[VPR];
-    le_i8(Xm + o, x);
-    const int b = lr / LPB, eb = XE[(long long)row * nb + b];
+    if (ativo) le_i8(Xm + o, x);
+    else {
+#pragma unroll
+        for (int i = 0; i < VPR; i++) x[i] = 0;
+    }
+    const int b = lr / LPB, eb = ativo ? (int)XE[(long long)row * nb + b] : -128;
     const int emax = g_max<LPR>(eb);
     int sq = 0;
 #pragma unroll
     for (int i = 0; i < VPR; i++) sq += x[i] * x[i];
     sq = g_sum<LPB>(sq);
     const bool lider = (lr & (LPB - 1)) == 0;
-    const int ss = g_sum<LPR>(lider ? rnd(sq << G, 2 * (emax - eb), kid, (long long)row * D) : 0);
+    const int ss = g_sum<LPR>(lider && ativo ? rnd(sq << G, 2 * (emax - eb), kid, (long long)row * D) : 0);
     if (ss >= LIM && lr == 0) reporta(E_ACUM, kid, (long long)row * D, ss, -1);
     // inv = 2^k / r lies in (2^10, 2^11]: the quotient bound of div_exata holds
     const int r = isqrt_i(ss >> log2D), k = bitlen(r) + 10, inv = div_exata(1 << k, r);
@@ -30,6 +38,7 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
 #pragma unroll
     for (int i = 0; i < VPR; i++) v[i] = x[i] * inv;            // |v| < 2^18, one exponent per block
     const int Eo = quant8_u<VPR, LPB>(v, eb - k - emax + G / 2, q, kid, o);
+    if (!ativo) return;
     grava_q8(Ym + o, q);
     if (lider) YE[(long long)row * nb + b] = (int8_t)Eo;
     if (lr == 0) { cr[row] = r; cemax[row] = emax; }
@@ -40,28 +49,42 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
 // The block-uniform alignments run through Desl: |g y| << GB < 2^21 shifts right, g shifts left by at most 21
 // (ec >= eg + 7 - 28) and y S by at most 6 (|S| <= 2^15, ec >= ey + eS + 22 - 28), so every value stays below 2^28
 // and the spec's left-shift checks cannot fire. Every load (x included) is issued before the first reduction.
-template <int VPR, int LPR, int BLK, bool SOMA = false>
+template <int VPR, int LPR, int BLK, bool SOMA = false, bool CHEIO = true>
 __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ ym,
                                                   const int8_t* __restrict__ yE, const int* __restrict__ cr, const int* __restrict__ cemax,
                                                   int8_t* __restrict__ om, int8_t* __restrict__ oE, int M, int log2D, int G, int GB, int kid,
-                                                  const int8_t* __restrict__ xm = nullptr, const int8_t* __restrict__ xE = nullptr, int kid2 = 0) {
-    constexpr int D = VPR * LPR, nb = D / BLK, LPB = BLK / VPR;
+                                                  const int8_t* __restrict__ xm = nullptr, const int8_t* __restrict__ xE = nullptr, int kid2 = 0,
+                                                  int Dr = 0) {
+    constexpr int LPB = BLK / VPR;
+    const int D = CHEIO ? VPR * LPR : Dr, nb = D / BLK;
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
     if (row >= M) return;
+    const bool ativo = CHEIO || lr * VPR < D;
     const long long o = (long long)row * D + lr * VPR;
     const int b = lr / LPB;
     int g[VPR], y[VPR], a[VPR];
-    le_i8(gm + o, g);
-    le_i8(ym + o, y);
-    const int eg = gE[(long long)row * nb + b], ey = yE[(long long)row * nb + b];
+    int eg = -128, ey = -128, ex = 0;
+    if (ativo) {
+        le_i8(gm + o, g);
+        le_i8(ym + o, y);
+        eg = gE[(long long)row * nb + b];
+        ey = yE[(long long)row * nb + b];
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPR; i++) g[i] = y[i] = 0;
+    }
     const int r = cr[row], emax = cemax[row];
-    int ex = 0;
     if constexpr (SOMA) {
-        le_i8(xm + o, a);
-        ex = xE[(long long)row * nb + b];
+        if (ativo) {
+            le_i8(xm + o, a);
+            ex = xE[(long long)row * nb + b];
+        } else {
+#pragma unroll
+            for (int i = 0; i < VPR; i++) a[i] = 0;
+        }
     }
     const int smax = g_max<LPR>(eg + ey);
-    const Desl d1(smax - (eg + ey));
+    const Desl d1(ativo ? smax - (eg + ey) : 0);
     int S = 0;
 #pragma unroll
     for (int i = 0; i < VPR; i++) S += d1((g[i] * y[i]) << GB);
@@ -93,10 +116,12 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
 #pragma unroll
         for (int i = 0; i < VPR; i++) zs[i] = da(a[i]) + dq((int)q[i]);
         const int Ez = quant8_u<VPR, LPB>(zs, ec2, qz, kid2, o);
+        if (!ativo) return;
         grava_q8(om + o, qz);
         if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Ez;
         return;
     }
+    if (!ativo) return;
     grava_i8(om + o, q);
     if ((lr & (LPB - 1)) == 0) oE[(long long)row * nb + b] = (int8_t)Eo;
 }
@@ -104,26 +129,33 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
 // ---------------------------------------------------------------------------------------------- softmax + CE
 // raw logits -> g = (P - 1[target]) in block format with exponent -12 - log2 M; d_alvo = umax - u_target and
 // soma = sum of ex per row, from which the host derives the float64 loss (ops.py:260-271; modelo.py:93).
-template <int VPR, int LPR, int BLK>
+template <int VPR, int LPR, int BLK, bool CHEIO = true>
 __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc, const int16_t* __restrict__ e, const int* __restrict__ alvo,
                                                     int8_t* __restrict__ gm, int8_t* __restrict__ gE, int* __restrict__ d_alvo,
-                                                    int* __restrict__ soma_o, int M, int log2M, int kid) {
-    constexpr int V = VPR * LPR, nb = V / BLK, LPB = BLK / VPR;
+                                                    int* __restrict__ soma_o, int M, int log2M, int kid, int Vr = 0) {
+    constexpr int LPB = BLK / VPR;
+    const int V = CHEIO ? VPR * LPR : Vr, nb = V / BLK;
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
     if (row >= M) return;
+    const bool ativo = CHEIO || lr * VPR < V;
     const int t = alvo[row];
     if (t < 0 || t >= V) { if (lr == 0) reporta(E_ARG, kid, (long long)row * V, t, V); return; }
     const long long o = (long long)row * V + lr * VPR;
     int a[VPR], ea[VPR], u[VPR];
-    le_i32(acc + o, a);
-    le_i16(e + o, ea);
+    if (ativo) {
+        le_i32(acc + o, a);
+        le_i16(e + o, ea);
+    }
     int umax = U_MIN;
 #pragma unroll
-    for (int i = 0; i < VPR; i++) { u[i] = rnd(a[i], -(ea[i] + 8), kid, o + i); umax = max(umax, u[i]); }
+    for (int i = 0; i < VPR; i++) {
+        u[i] = ativo ? rnd(a[i], -(ea[i] + 8), kid, o + i) : U_MIN;
+        umax = max(umax, u[i]);
+    }
     umax = g_max<LPR>(umax);
     int ex[VPR], s = 0;
 #pragma unroll
-    for (int i = 0; i < VPR; i++) { ex[i] = exp_dif(umax, u[i]) >> 3; s += ex[i]; }
+    for (int i = 0; i < VPR; i++) { ex[i] = ativo ? exp_dif(umax, u[i]) >> 3 : 0; s += ex[i]; }
     s = g_sum<LPR>(s);
     if (s <= 0) { if (lr == 0) reporta(E_DIV, kid, (long long)row * V, s, umax); s = 1; }
     const int inv = s > 256 ? div_exata(1 << 28, s) : (1 << 28) / s;   // s >= 4095 (exp(0) >> 3 of the row maximum): 2^28 / s < 2^20
@@ -136,6 +168,7 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
     }
     int8_t q[VPR];
     const int Eo = quant8_u8<VPR, LPB>(v, -12 - log2M, q, kid, o);   // one exponent per row
+    if (!ativo) return;
     grava_i8(gm + o, q);
     if ((lr & (LPB - 1)) == 0) gE[(long long)row * nb + lr / LPB] = (int8_t)Eo;
     if (lr == 0) soma_o[row] = s;

@@ -1,32 +1,49 @@
-"""Launch registry of the INT8 training step: launch ids, host-side format guards, the device error record and
-per-op timing. Same contract and messages as the reference's `Registro` (jatai_cuda/registro.py:42-221):
+"""Launch registry of the INT8 training step: every kernel launch gets an id, and anything that goes wrong -- a
+malformed tensor, a refused launch, an event a kernel raised on the device -- becomes one exception that says
+what happened, in which op and scope, where in the output and with which value.
 
-  1. before a launch: tensor formats (dtype, shape, contiguity, on the GPU, exponent shape for BLK);
-  2. after a launch: the runtime's return code;
-  3. device sentinels: the first event of a step (accumulator >= 2^30, exponent > 126, saturation, division by
-     zero, lossy left shift, bad token) is read from `g_erro` with the launch id `kid`, which maps back to the
-     op, its scope path and the (row, column) of the output;
-  4. per-op GPU time from events around each launch (perfil) and JSONL events.
+The parts:
 
-The block size for the shape checks is read from jatai_amd.ops.BLK at call time.
+  `Lancamento`  one record per launch, in launch order: id (its index), op name, scope path, inputs, output shape.
+                The id travels to the kernel as its last argument (`kid`), so a device event names its record.
+  `Evento`      the device's error record (the first event since the last clear: count, code, kid, flat index,
+                value, extra datum; `jt_erro_le`), decoded against the launch records.
+  `Diario`      the append-only JSONL log of a run (`<pasta>/<nome>.jsonl`).
+  `Registro`    the object the operator layer and the model hold: format guards before a launch, the return code
+                after it, the device record once per step (or after every launch with `vigiar`), per-op GPU time
+                with `perfil`, and tensor statistics.
+
+A device event saves the inputs of the launch that raised it (`<pasta>/falha_passo<P>_<kid>_<op>.pt`, a dict of
+CPU tensors; load it with torch.load(..., weights_only=True)) so the event can be re-run, e.g. through the CPU
+oracle. In a replayed graph the saved tensors are the graph's own buffers read after the replay: inputs that a
+later kernel of the same step overwrites are saved as that kernel left them.
+
+Interface kept from the reference's `Registro` (jatai_cuda/registro.py:42-221), because the operator layer and
+the model code call it: registra / depois / confere_bloco / confere_cru / confere_r16 / exige / falha / trecho /
+novo_passo / fim_passo / confere_device / relatorio_tempos / estatistica and the attributes lib, lancamentos,
+vigiar, perfil. A device event's message carries the three lines callers match
+(jatai_cuda/teste_erro_grafo.py:26): the scope path, "linha R, coluna C" and "valor    : V".
 """
 import contextlib
 import ctypes
+import dataclasses
 import json
 import os
+import sys
 import time
 
 import torch
 
 from . import ops as O
 
-CODIGOS = {
-    1: "acumulador passou de 2^30 (estouraria o registrador int32)",
-    2: "expoente do bloco passou de 126 (estouro para cima do INT8; abaixo de -126 o bloco vira zero)",
-    3: "mantissa passou de +-127 mesmo depois de subir o expoente",
-    4: "divisao por zero (soma do softmax <= 0)",
-    5: "shift a esquerda perderia bits (resultado >= 2^30)",
-    6: "argumento invalido (token ou alvo fora do vocabulario)",
+# device event codes (csrc/jt_comum.h: E_ACUM .. E_ARG), as the kernels report them
+EVENTOS = {
+    1: "accumulator reached 2^30 (beyond the int32 range the format keeps)",
+    2: "block exponent above 126 (INT8 exponent overflow)",
+    3: "mantissa beyond +-127 after the exponent bump",
+    4: "division by zero (softmax sum <= 0)",
+    5: "left shift would lose bits (result >= 2^30)",
+    6: "invalid argument (token or target outside the vocabulary)",
 }
 
 
@@ -34,21 +51,83 @@ class ErroJatai(RuntimeError):
     pass
 
 
+@dataclasses.dataclass
+class Lancamento:
+    kid: int
+    op: str
+    trecho: str
+    entradas: dict
+    forma: tuple
+
+
+@dataclasses.dataclass
+class Evento:
+    """The first device event of a step, decoded."""
+    n: int
+    codigo: int
+    kid: int
+    idx: int
+    valor: int
+    aux: int
+    lancamento: Lancamento = None
+    arquivo: str = None
+
+    def posicao(self):
+        forma = self.lancamento.forma if self.lancamento else None
+        if forma and len(forma) == 2 and forma[1]:
+            return f"linha {self.idx // forma[1]}, coluna {self.idx % forma[1]} (forma {tuple(forma)})"
+        return f"indice {self.idx}"
+
+    def mensagem(self):
+        l = self.lancamento
+        return "\n".join([
+            EVENTOS.get(self.codigo, f"device event code {self.codigo}"),
+            f"  operacao : {l.op}",
+            f"  trecho   : {l.trecho}",
+            f"  posicao  : {self.posicao()}",
+            f"  valor    : {self.valor}   (extra: {self.aux})",
+            f"  eventos  : {self.n} this step (the first one is shown)",
+            f"  entradas : {_formas(l.entradas)}",
+            f"  salvas em: {self.arquivo}",
+        ])
+
+
+def _formas(ent):
+    return {k: (tuple(v.shape) if torch.is_tensor(v) else v) for k, v in ent.items()}
+
+
+class Diario:
+    """Append-only JSONL log; each record carries the time, its type, the step and the scope."""
+
+    def __init__(self, caminho):
+        self.arq = open(caminho, "a")
+
+    def grava(self, tipo, passo, trecho, **campos):
+        rec = dict(hora=time.strftime("%H:%M:%S"), tipo=tipo, passo=passo, trecho=trecho, **campos)
+        self.arq.write(json.dumps(rec, ensure_ascii=False, default=str) + "\n")
+        self.arq.flush()
+        return rec
+
+
 class Registro:
     def __init__(self, pasta, nome, lib=None, vigiar=False, perfil=False, eco=True):
         os.makedirs(pasta, exist_ok=True)
         self.pasta, self.nome, self.lib = pasta, nome, lib
         self.vigiar, self.perfil, self.eco = vigiar, perfil, eco
-        self.arq = open(os.path.join(pasta, f"{nome}.jsonl"), "a")
-        self.pilha, self.lancamentos, self.passo = [], [], None
-        self.eventos, self.tempos = [], {}
+        self.diario = Diario(os.path.join(pasta, f"{nome}.jsonl"))
+        self.escopo = []                 # current scope path, innermost last
+        self.lancamentos = []            # Lancamento per launch id of the current step (or of a captured graph)
+        self.passo = None
+        self._cronos = []                # (op, start event, end event) of the current step, with perfil
+        self.tempos = {}                 # op -> accumulated GPU ms over the steps since the last report
+        self.ultimo_evento = None
 
-    # ------------------------------------------------------------------ writing
+    # ------------------------------------------------------------------ log and failure
+    def onde(self):
+        return " / ".join(self.escopo) or "-"
+
     def escreve(self, tipo, **kw):
-        rec = {"hora": time.strftime("%H:%M:%S"), "tipo": tipo, "passo": self.passo, "trecho": self.onde(), **kw}
-        self.arq.write(json.dumps(rec, ensure_ascii=False, default=str) + "\n")
-        self.arq.flush()
-        return rec
+        return self.diario.grava(tipo, self.passo, self.onde(), **kw)
 
     def info(self, msg, **kw):
         self.escreve("info", msg=msg, **kw)
@@ -57,169 +136,166 @@ class Registro:
 
     def aviso(self, msg, **kw):
         self.escreve("aviso", msg=msg, **kw)
-        print(f"[AVISO] passo {self.passo} | {self.onde()} | {msg}", flush=True)
+        print(f"[warning] step {self.passo} | {self.onde()} | {msg}", file=sys.stderr, flush=True)
 
     def falha(self, msg, **kw):
         self.escreve("erro", msg=msg, **kw)
         raise ErroJatai(f"\n[ERRO] passo {self.passo} | {self.onde()}\n{msg}")
 
-    def onde(self):
-        return " / ".join(self.pilha) or "-"
+    def exige(self, cond, msg):
+        if not cond:
+            self.falha(msg)
 
     @contextlib.contextmanager
     def trecho(self, nome):
-        self.pilha.append(nome)
+        self.escopo.append(nome)
         try:
             yield
         finally:
-            self.pilha.pop()
+            self.escopo.pop()
 
     # ------------------------------------------------------------------ steps and launches
     def novo_passo(self, passo):
         self.passo = passo
         self.lancamentos = []
-        self.eventos = []
+        self._cronos = []
         if self.lib is not None:
             self.lib.jt_erro_limpa()
 
     def registra(self, op, entradas, forma_saida, tempo=True):
-        """tempo=False: a further launch id of a batched launch timed under the batch's first id."""
+        """Records a launch and returns its id. tempo=False: a further id of a batched launch, whose time is
+        counted under the batch's first id."""
         kid = len(self.lancamentos)
-        self.lancamentos.append({"op": op, "trecho": self.onde(), "entradas": entradas, "forma": forma_saida})
+        self.lancamentos.append(Lancamento(kid, op, self.onde(), entradas, tuple(forma_saida) if forma_saida else None))
         if self.perfil and tempo:
-            ini, fim = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ini.record()
-            self.eventos.append((op, ini, fim))
+            par = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            par[0].record()
+            self._cronos.append((op, *par))
         return kid
 
     def depois(self, kid, codigo):
-        if self.perfil:
-            self.eventos[-1][2].record()
+        if self.perfil and self._cronos:
+            self._cronos[-1][2].record()
         if codigo != 0:
-            lanc = self.lancamentos[kid]
-            self.falha(f"o HIP recusou o lancamento de '{lanc['op']}' (hipError {codigo}). "
-                       f"Formas das entradas: {self._formas(lanc['entradas'])}")
+            l = self.lancamentos[kid]
+            self.falha(f"the HIP runtime refused the launch of '{l.op}' (hipError {codigo}); inputs {_formas(l.entradas)}")
         if self.vigiar:
             self.confere_device()
 
-    def confere_device(self):
-        """Reads the device error record (synchronizes the GPU)."""
+    def _le_device(self):
         buf = (ctypes.c_longlong * 6)()
         n = self.lib.jt_erro_le(buf)
         if n < 0:
-            self.falha(f"falha do HIP ao ler o registro de erro (hipError {-n}); um kernel anterior "
-                       f"provavelmente abortou. Ultimo lancamento: {self._resumo(len(self.lancamentos) - 1)}")
-        if n == 0:
-            return
-        _, codigo, kid, idx, valor, aux = list(buf)
-        lanc = self.lancamentos[kid] if 0 <= kid < len(self.lancamentos) else None
-        if lanc is None:
-            self.falha(f"{CODIGOS.get(codigo, codigo)} em kernel de id {kid} desconhecido (idx {idx}, valor {valor})")
-        forma = lanc["forma"]
-        pos = f"indice {idx}"
-        if forma and len(forma) == 2:
-            pos = f"linha {idx // forma[1]}, coluna {idx % forma[1]} (forma {tuple(forma)})"
-        arq = os.path.join(self.pasta, f"erro_passo{self.passo}_{lanc['op']}.pt")
+            ult = self.lancamentos[-1] if self.lancamentos else None
+            self.falha(f"reading the device error record failed (hipError {-n}): an earlier kernel probably aborted; "
+                       f"last launch {ult.op + ' in ' + ult.trecho if ult else '-'}")
+        return Evento(*[int(x) for x in buf]) if n > 0 else None
+
+    def _salva(self, ev):
+        l = ev.lancamento
+        arq = os.path.join(self.pasta, f"falha_passo{self.passo}_{l.kid}_{l.op.replace('+', '_')}.pt")
         try:
-            torch.save({k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in lanc["entradas"].items()}, arq)
-        except Exception as e:  # saving must not hide the original error
-            arq = f"(nao salvou: {e})"
-        msg = (f"{CODIGOS.get(codigo, f'codigo {codigo}')}\n"
-               f"  operacao : {lanc['op']}\n"
-               f"  trecho   : {lanc['trecho']}\n"
-               f"  posicao  : {pos}\n"
-               f"  valor    : {valor}   (dado extra: {aux})\n"
-               f"  eventos  : {n} no total neste passo (so o primeiro e detalhado)\n"
-               f"  entradas : {self._formas(lanc['entradas'])}\n"
-               f"  salvas em: {arq}")
-        self.pilha = [lanc["trecho"]]
-        self.falha(msg, codigo=codigo, op=lanc["op"], idx=idx, valor=valor, aux=aux)
+            torch.save({k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in l.entradas.items()}, arq)
+            return arq
+        except Exception as e:          # the save must not hide the event itself
+            return f"(not saved: {e})"
+
+    def confere_device(self):
+        """Reads the device error record (synchronizes the device); a recorded event raises ErroJatai."""
+        ev = self._le_device()
+        if ev is None:
+            return
+        if not 0 <= ev.kid < len(self.lancamentos):
+            self.falha(f"{EVENTOS.get(ev.codigo, ev.codigo)} in an unknown launch id {ev.kid} (index {ev.idx}, value {ev.valor})")
+        ev.lancamento = self.lancamentos[ev.kid]
+        ev.arquivo = self._salva(ev)
+        self.ultimo_evento = ev
+        self.escopo = [ev.lancamento.trecho]
+        self.falha(ev.mensagem(), codigo=ev.codigo, op=ev.lancamento.op, idx=ev.idx, valor=ev.valor, aux=ev.aux, arquivo=ev.arquivo)
 
     def fim_passo(self):
         if self.lib is not None:
             self.confere_device()
         if self.perfil:
             torch.cuda.synchronize()
-            for op, ini, fim in self.eventos:
-                self.tempos[op] = self.tempos.get(op, 0.0) + ini.elapsed_time(fim)
+            for op, a, b in self._cronos:
+                self.tempos[op] = self.tempos.get(op, 0.0) + a.elapsed_time(b)
 
     def relatorio_tempos(self, passos):
         if not self.tempos:
             return
         tot = sum(self.tempos.values())
-        linhas = [f"  {op:16s} {ms / passos:8.3f} ms/passo  {100 * ms / tot:5.1f}%"
-                  for op, ms in sorted(self.tempos.items(), key=lambda x: -x[1])]
-        self.info("tempo de GPU por operacao:\n" + "\n".join(linhas) + f"\n  {'total':16s} {tot / passos:8.3f} ms/passo",
+        ordem = sorted(self.tempos.items(), key=lambda kv: -kv[1])
+        linhas = [f"  {op:24s} {ms / passos:8.3f} ms/step  {100 * ms / tot:5.1f}%" for op, ms in ordem]
+        self.info("GPU time per op:\n" + "\n".join(linhas) + f"\n  {'total':24s} {tot / passos:8.3f} ms/step",
                   tempos={k: v / passos for k, v in self.tempos.items()})
         self.tempos = {}
 
-    # ------------------------------------------------------------------ format checks
+    # ------------------------------------------------------------------ format guards
+    def _formato(self, nome, m, E, tipo):
+        """Block formats: mantissa `tipo` [R, C] with C a multiple of BLK, int8 exponents [R, C / BLK], both
+        contiguous on the GPU (BLK read from jatai_amd.ops at call time)."""
+        erros = []
+        if m.dtype != tipo:
+            erros.append(f"mantissa {m.dtype}, expected {tipo}")
+        if E.dtype != torch.int8:
+            erros.append(f"exponent {E.dtype}, expected int8")
+        if not (m.is_cuda and E.is_cuda):
+            erros.append("not on the GPU")
+        if not (m.is_contiguous() and E.is_contiguous()):
+            erros.append("not contiguous")
+        if m.dim() != 2:
+            erros.append(f"mantissa of {m.dim()} dimensions, expected 2")
+        elif m.shape[1] % O.BLK:
+            erros.append(f"{m.shape[1]} columns, not a multiple of BLK={O.BLK}")
+        elif tuple(E.shape) != (m.shape[0], m.shape[1] // O.BLK):
+            erros.append(f"exponent shape {tuple(E.shape)}, expected {(m.shape[0], m.shape[1] // O.BLK)}")
+        if erros:
+            self.falha(f"argument '{nome}': " + "; ".join(erros))
+
     def confere_bloco(self, nome, t):
         m, E = t
         if not (torch.is_tensor(m) and torch.is_tensor(E)):
-            self.falha(f"'{nome}': esperava (mantissa, expoente) como tensores, veio {type(m)}, {type(E)}")
-        self._confere_formato(nome, m, E, torch.int8)
+            self.falha(f"argument '{nome}': expected a (mantissa, exponent) pair of tensors, got {type(m)}, {type(E)}")
+        self._formato(nome, m, E, torch.int8)
 
     def confere_r16(self, nome, t):
-        m, E = t
-        self._confere_formato(nome, m, E, torch.int16)
-
-    def _confere_formato(self, nome, m, E, dt):
-        blk = O.BLK
-        prob = []
-        if m.dtype != dt: prob.append(f"mantissa dtype {m.dtype} (esperado {dt})")
-        if E.dtype != torch.int8: prob.append(f"expoente dtype {E.dtype} (esperado int8)")
-        if not m.is_cuda or not E.is_cuda: prob.append("tensor fora da GPU")
-        if not m.is_contiguous() or not E.is_contiguous(): prob.append("tensor nao contiguo")
-        if m.dim() != 2: prob.append(f"mantissa com {m.dim()} dimensoes (esperado 2)")
-        elif m.shape[1] % blk: prob.append(f"colunas {m.shape[1]} nao multiplo de {blk}")
-        elif tuple(E.shape) != (m.shape[0], m.shape[1] // blk):
-            prob.append(f"expoente com forma {tuple(E.shape)}, esperado {(m.shape[0], m.shape[1] // blk)}")
-        if prob:
-            self.falha(f"argumento '{nome}' com formato invalido: " + "; ".join(prob))
+        self._formato(nome, t[0], t[1], torch.int16)
 
     def confere_cru(self, nome, t):
         acc, e = t
-        prob = []
-        if acc.dtype != torch.int32: prob.append(f"acumulador dtype {acc.dtype} (esperado int32)")
-        if e.dtype != torch.int16: prob.append(f"expoente dtype {e.dtype} (esperado int16)")
-        if acc.shape != e.shape: prob.append(f"formas diferentes {tuple(acc.shape)} x {tuple(e.shape)}")
-        if not acc.is_cuda or not acc.is_contiguous() or not e.is_contiguous(): prob.append("fora da GPU ou nao contiguo")
-        if prob:
-            self.falha(f"argumento '{nome}' (cru) com formato invalido: " + "; ".join(prob))
-
-    def exige(self, cond, msg):
-        if not cond:
-            self.falha(msg)
+        erros = []
+        if acc.dtype != torch.int32:
+            erros.append(f"accumulator {acc.dtype}, expected int32")
+        if e.dtype != torch.int16:
+            erros.append(f"exponent {e.dtype}, expected int16")
+        if acc.shape != e.shape:
+            erros.append(f"shapes differ: {tuple(acc.shape)} and {tuple(e.shape)}")
+        if not (acc.is_cuda and acc.is_contiguous() and e.is_contiguous()):
+            erros.append("not on the GPU or not contiguous")
+        if erros:
+            self.falha(f"raw argument '{nome}': " + "; ".join(erros))
 
     # ------------------------------------------------------------------ statistics
     def estatistica(self, nome, t, zeros_normais=False):
-        """Summary of a block tensor (report only; computed with torch outside the hot path)."""
+        """Summary of a block tensor, logged (torch reductions outside the hot path); warns on the patterns that
+        precede trouble: a tensor rounded to zero, a majority of zero mantissas, exponents near -126."""
         m, E = t
-        nz = E != O.E_ZERO
+        vivos = E != O.E_ZERO
+        nz = bool(vivos.any())
         rec = {
             "nome": nome,
             "zeros": round(float((m == 0).float().mean()), 4),
-            "blocos_zerados": round(float((~nz).float().mean()), 4),
-            "exp_min": int(E[nz].min()) if nz.any() else None,
-            "exp_max": int(E[nz].max()) if nz.any() else None,
+            "blocos_zerados": round(float((~vivos).float().mean()), 4),
+            "exp_min": int(E[vivos].min()) if nz else None,
+            "exp_max": int(E[vivos].max()) if nz else None,
             "maior_mantissa_media": round(float(m.abs().reshape(m.shape[0], -1, O.BLK).amax(-1).float().mean()), 1),
         }
         self.escreve("estatistica", **rec)
-        if not nz.any():
-            self.aviso(f"'{nome}' saiu inteiro zerado")
+        if not nz:
+            self.aviso(f"'{nome}' is all zero")
         elif not zeros_normais and rec["zeros"] > 0.5:
-            self.aviso(f"'{nome}' tem {rec['zeros']:.0%} de zeros: valores pequenos sumindo no arredondamento?")
+            self.aviso(f"'{nome}' has {rec['zeros']:.0%} zero mantissas: small values lost to rounding?")
         if rec["exp_min"] is not None and rec["exp_min"] < -110:
-            self.aviso(f"'{nome}' tem expoente {rec['exp_min']}, perto do limite -126 do INT8")
+            self.aviso(f"'{nome}' has exponent {rec['exp_min']}, close to the INT8 limit -126")
         return rec
-
-    @staticmethod
-    def _formas(ent):
-        return {k: (tuple(v.shape) if torch.is_tensor(v) else v) for k, v in ent.items()}
-
-    def _resumo(self, kid):
-        if kid < 0 or kid >= len(self.lancamentos):
-            return "-"
-        l = self.lancamentos[kid]
-        return f"{l['op']} em {l['trecho']}"

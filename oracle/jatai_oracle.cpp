@@ -262,6 +262,7 @@ static inline i64 desloca_est(i64 x, i64 s, uint32_t h) {
     const i64 u = (i64)(hash32(h ^ (uint32_t)x * 0x9E3779B1u) & (uint32_t)((1ull << s) - 1));
     return piso + (u < resto ? 1 : 0);
 }
+void or_hash32(const i64* x, i64* out, i64 n) { for (i64 i = 0; i < n; i++) out[i] = hash32((uint32_t)x[i]); }
 void or_soma_est(const int8_t* xm, const int8_t* xE, const int8_t* ym, const int8_t* yE, i64 R, int C, int blk, int8_t* zm, int8_t* zE) {
     const int nb = C / blk;
 #pragma omp parallel for schedule(static)
@@ -437,10 +438,12 @@ void or_rms_back(const int8_t* gm, const int8_t* gE, const int8_t* ym, const int
 //   alignment: every value of head h in token t is aligned to emx = the largest block exponent the head spans
 //              over all T tokens of its sequence (at hd = 4 a head spans one block);
 //   score:     u = rnd(q.k, -(eq + ek - log2(hd)/2 + 8))   (the spec's -1 is -log2(4)/2);
-//   ALiBi:     incl = 8 - (8 h) / H                         (the spec's 8 - h // 8 at H = 64);
+//   ALiBi:     incl = 8 - h // 8 at hd = 4 for every H (the spec, ops.py:208); for hd > 4, incl = 8 - (8 h) / H
+//              (eight slopes 2^0 .. 2^-7 spread evenly over the H heads; at H = 64 the same as the spec's);
 //   dS:        shrunk to 12 - max(0, log2(T) - 7) bits      (12 for T <= 128, keeping |gq|,|gk| < 2^30).
 static int att_lg(int hd) { return ilog2(hd) / 2; }
 static int att_dsbits(int T) { return 12 - std::max(0, ilog2(T) - 7); }
+static i64 att_incl(int h, int H, int hd) { return hd == 4 ? 8 - h / 8 : 8 - (8 * (i64)h) / H; }
 
 // aligned values a[t][d] = rnd(x << GA, emx - e) and the head exponent emx - GA (ops.py:186-192)
 static void alinha(const int8_t* m, const int8_t* E, int ld, int col0, int blk, int b, int T, int hd, int GA,
@@ -470,7 +473,7 @@ void or_atencao(const int8_t* qm, const int8_t* qE, int Bt, int T, int H, int D,
         alinha(qm, qE, ld, h * hd, blk, b, T, hd, GA, qa, eq);
         alinha(qm, qE, ld, D + h * hd, blk, b, T, hd, GA, ka, ek);
         alinha(qm, qE, ld, 2 * D + h * hd, blk, b, T, hd, GA, va, ev);
-        const i64 incl = 8 - (8 * (i64)h) / H, su = -(eq + ek - lg + 8);
+        const i64 incl = att_incl(h, H, hd), su = -(eq + ek - lg + 8);
         std::vector<i64> u(T), ex(T);
         for (int i = 0; i < T; i++) {
             i64 mx = -((i64)1 << 62);

@@ -99,6 +99,42 @@ def casos():
     return c
 
 
+def casos_dominio():
+    """The rest of the reference's shape domain, beyond the model shape of casos(): rms / rms_back at widths that
+    are multiples of 128 but not powers of two (ops.py:453, D <= 1024), softmax_ce at V = 384 and 640
+    (ops.py:496, V % 128 == 0), and head-width-4 attention at H = 32 and at T = 32 and 96 (ops.py:475:
+    T % 32 == 0, T <= 128, H * 4 == D, H <= 64). Same generators as casos()."""
+    c = []
+    a = c.append
+    Mr = 256
+    for Dd in (384, 640, 768, 896):
+        a((f"rms D={Dd}", lambda o, g, be, Dd=Dd: o.rms(g.bloco(Mr, Dd, espalha=6, zera=0.1))))
+    for Dd in (384, 896):
+        a((f"rms_back D={Dd}", lambda o, g, be, Dd=Dd: (lambda Y: o.rms_back(g.bloco(Mr, Dd, espalha=6), Y[0], Y[1]))(
+            o.rms(g.bloco(Mr, Dd)))))
+    for Vv in (384, 640):
+        a((f"softmax_ce V={Vv}", lambda o, g, be, Vv=Vv: o.softmax_ce(g.cru(Mr, Vv, bits=22, e0=-20), g.tok(Mr, Vv))))
+    for (bt, t, h) in ((4, 96, 32), (8, 32, 64), (2, 128, 32)):
+        dd = 4 * h
+        a((f"atencao Bt={bt} T={t} H={h}", lambda o, g, be, bt=bt, t=t, h=h, dd=dd:
+           o.atencao(g.bloco(bt * t, 3 * dd, espalha=3), bt, t, h)))
+        for lim in (False, True):
+            a((f"atencao_back Bt={bt} T={t} H={h}" + (" limite" if lim else ""),
+               lambda o, g, be, bt=bt, t=t, h=h, dd=dd, lim=lim: _att_back_forma(o, g, be, bt, t, h, dd, lim)))
+    return c
+
+
+def _att_back_forma(o, g, be, bt, t, h, dd, limite):
+    q = g.bloco(bt * t, 3 * dd, espalha=6, zera=0.05)
+    go = g.bloco(bt * t, dd, e0=-20, espalha=6)
+    P = o.atencao(q, bt, t, h)[1]
+    old = be.limite(limite)
+    try:
+        return o.atencao_back(go, q, P, bt, t, h)
+    finally:
+        be.limite(old)
+
+
 def _att_back(o, g, be, go_kw, q_kw, limite):
     """atencao_back on P from the same backend's forward (teste_ops.py:87-90: q drawn first, then dO)."""
     q = g.bloco(M, 3 * D, **q_kw)

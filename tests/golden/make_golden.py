@@ -9,13 +9,16 @@ Fixtures:
   ops_blk128.json   the 40 op cases of tests/cases.py (teste_ops.py:57-98) with the spec at BLK=128
   ops_blk32.json    the same cases with the spec's block constant set to 32 (ops.BLK is a module global the
                     spec reads everywhere: quant, expande, gemm, g_rms, _alinha)
+  ops_dominio_blk128.json, ops_dominio_blk32.json
+                    the cases of tests/cases.py casos_dominio(): the rest of the reference's shape domain (row
+                    widths that are not powers of two, attention at H = 32 and T = 32, 96)
   config1.json      BASELINE config 1: one 512x512x512 GEMM, exponents uniform in [-8, 0], at BLK 32 and 128
   primitives.json   exp_int over its whole domain, isqrt / bitlen / rnd on sampled inputs
   trace_r.json      every op output of two full training steps (Modelo.passo with k_lr=4) at the reference
                     model shape (V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=8), plus the per-step
                     (d_alvo, soma) hashes and float64 losses of N further steps
 
-Usage: python tests/golden/make_golden.py [--ref /root/reference] [--only ops|config1|prim|trace] [--passos N]
+Usage: python tests/golden/make_golden.py [--ref /root/reference] [--only ops|dominio|config1|prim|trace] [--passos N]
 """
 import argparse
 import contextlib
@@ -59,11 +62,11 @@ class Backend:
         return old
 
 
-def run_ops(O, blk):
+def run_ops(O, blk, casos=None):
     set_blk(O, blk)
     be = Backend(O)
     out = []
-    for i, (nome, fn) in enumerate(CS.casos()):
+    for i, (nome, fn) in enumerate(casos or CS.casos()):
         t0 = time.time()
         rec = CS.Gravador(be.ops, host)
         g = CS.Gen(R.substream(1000 + i, nome), blk, be.dev)
@@ -160,6 +163,9 @@ def main():
     if a.only in ("all", "ops"):
         for blk in (128, 32):
             w(f"ops_blk{blk}.json", run_ops(O, blk))
+    if a.only in ("all", "dominio"):
+        for blk in (128, 32):
+            w(f"ops_dominio_blk{blk}.json", run_ops(O, blk, CS.casos_dominio()))
     if a.only in ("all", "trace"):
         w("trace_r.json", run_trace(O, MO, a.passos))
 

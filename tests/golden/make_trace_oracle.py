@@ -9,6 +9,8 @@ run it.
   trace_c4.jsonl    BASELINE config 4 (V 256, D 512, 8 heads x 64, FF 2048, 12 layers, Bt 8, T 256, BLK 32,
                     k_lr 4): as many steps as asked. Attention at head width 64 is the declared extension of the
                     spec (it reduces to the spec at head width 4), so this trace is anchored on the oracle alone.
+  trace_c5.jsonl    BASELINE config 5 (the config-4 widths with 24 layers, Bt 64 x T 256 = 16384 tokens and the
+                    16-bit residual stream, modelo.py:60-130): 3 steps (about 3-4 minutes each on 8 cores).
 
 Both use seed-0 init (modelo.py:16-45) and the batches of tests/traco.py: uniform ids from substream 4242,
 (x[:, :-1], x[:, 1:]) as treino_int8_gpu/treino.py:41-44. Line 1 holds the shape and the init hashes; each
@@ -16,7 +18,7 @@ further line one step: the SHA-256 of the integer softmax outputs d_alvo and som
 them) and the float64 loss mean(d/256 + ln(s/4096)) (modelo.py:93) as a hex float. Lines are appended and
 flushed as steps finish, so a partial file is usable.
 
-Usage: python tests/golden/make_trace_oracle.py r600|c4 [--passos N] [--threads T]
+Usage: python tests/golden/make_trace_oracle.py r600|c4|c5 [--passos N] [--threads T]
 """
 import argparse
 import json
@@ -36,8 +38,9 @@ import traco as TR  # noqa: E402
 FORMAS = {
     "r600": dict(V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=8, BLK=128, k_lr=4, semente=0, tokens_seed=4242),
     "c4": dict(V=256, D=512, H=8, FF=2048, L=12, T=256, Bt=8, BLK=32, k_lr=4, semente=0, tokens_seed=4242),
+    "c5": dict(V=256, D=512, H=8, FF=2048, L=24, T=256, Bt=64, BLK=32, k_lr=4, semente=0, tokens_seed=4242, r16=True),
 }
-PASSOS = {"r600": 600, "c4": 600}
+PASSOS = {"r600": 600, "c4": 600, "c5": 3}
 
 
 def main():
@@ -54,7 +57,8 @@ def main():
     f = FORMAS[a.qual]
     n = a.passos or PASSOS[a.qual]
     O.BLK = f["BLK"]
-    m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cpu", OpsOraculo(f["BLK"]), TR.RegStub())
+    m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cpu", OpsOraculo(f["BLK"]), TR.RegStub(),
+               r16=f.get("r16", False))
     m.perda_inteira = True
     init = {k: [R.sha(t[0].numpy()), R.sha(t[1].numpy())] for k, t in m.p.items()}
     gold = TR.gold() if a.qual == "r600" else None

@@ -28,17 +28,17 @@ def test_superficie_python_usa_so_simbolos_declarados():
 
 
 def test_guardas_de_host_sem_gpu():
-    """Shape guards fire on the host before any launch (registro.py:161-189 contract)."""
+    """Format guards fire on the host before any launch (the reference's guards: jatai_cuda/registro.py:161-189)."""
     import pytest
     import torch
     from jatai_amd import ops as O
     from jatai_amd.registro import ErroJatai, Registro
     reg = Registro("/tmp/jatai_testes", "abi", eco=False)
-    with pytest.raises(ErroJatai, match="fora da GPU"):
+    with pytest.raises(ErroJatai, match="not on the GPU"):
         reg.confere_bloco("A", (torch.zeros(4, 128, dtype=torch.int8), torch.zeros(4, 1, dtype=torch.int8)))
     O.BLK = 32
     try:
-        with pytest.raises(ErroJatai, match="expoente com forma"):
+        with pytest.raises(ErroJatai, match="exponent shape"):
             reg.confere_bloco("A", (torch.zeros(4, 128, dtype=torch.int8), torch.zeros(4, 1, dtype=torch.int8)))
     finally:
         O.BLK = 128

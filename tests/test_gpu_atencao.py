@@ -1,7 +1,8 @@
 """Attention at head width 64 (the BASELINE configs' 8 heads x 64 of D = 512, T = 256): the HIP kernels against
 the CPU oracle's generalized restatement (jatai_oracle.cpp, which reduces to the spec at head width 4, pinned by
 the golden fixtures). Bit-exact: P, the raw output (acc, e), and the backward's raw (acc, e) in both variants.
-The generalization itself has no reference counterpart: parity beyond the head-width-4 reduction is unpinned."""
+The generalization has no reference counterpart; test_atencao_hd64_reduz_ao_spec_hd4 pins it to the spec's
+head-width-4 arithmetic on inputs where the two problems coincide (T <= 128)."""
 import pytest
 import torch
 
@@ -16,14 +17,22 @@ def _cmp(a, b, nome):
     assert d is None, f"{nome}: (flat index, gpu, oracle, count) = {d}"
 
 
-@pytest.fixture(params=[True, False], ids=["ws", "abi"])
+@pytest.fixture(params=["ws", "abi", "dot2"])
 def via_ws(request):
-    """True: OpsHip's default path (jt_atencao_ws, workspace kernels at head width 64); False: the reference
-    ABI's jt_atencao."""
+    """ws: OpsHip's default path (jt_atencao_ws, workspace kernels at head width 64); abi: the reference ABI's
+    jt_atencao (matrix-core kernels that stage their own operands); dot2: the same entry points with
+    jt_atencao_mfma(0), the v_dot2 kernel family."""
     from jatai_amd import ops as O
-    old, O.ATENCAO_WS = O.ATENCAO_WS, request.param
-    yield request.param
-    O.ATENCAO_WS = old
+    lib = O.carrega_lib()
+    old = O.ATENCAO_WS
+    O.ATENCAO_WS = request.param == "ws"
+    if request.param == "dot2":
+        lib.jt_atencao_mfma(0)
+    try:
+        yield request.param
+    finally:
+        O.ATENCAO_WS = old
+        lib.jt_atencao_mfma(1)
 
 
 # exponents e0 +- espalha stay in the range where the int32 sentinels stay silent (e0 + espalha <= 2, as the
@@ -77,3 +86,28 @@ def test_atencao_q_igual_a_quant(T, H, limite):
         gpu.limite(old)
     for nome, a, b in (("om", om[0], ref[0]), ("omE", om[1], ref[1]), ("P", P, P2), ("gq", gq[0], gref[0]), ("gqE", gq[1], gref[1])):
         _cmp(a, b, nome)
+
+
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_reduz_ao_spec_hd4(limite, via_ws):
+    """The head-width-64 kernels on inputs where each head carries one head-width-4 head of the spec's shape
+    (tests/reducoes.py) give that head's outputs as the oracle's head-width-4 code computes them -- the code the
+    reference's goldens pin (ops.py:186-258): P, o, and the backward's gq, gk, gv."""
+    import reducoes as RD
+    Bt, T = 2, 128
+    (q4, g4), (q64, g64) = RD.problemas(5151, Bt, T)
+    cpu = CPU(32)
+    gpu = GPU(32, vigiar=True)
+    Q4, G4 = (tuple(cpu.dev(v) for v in x) for x in (q4, g4))
+    Q64, G64 = (tuple(gpu.dev(v) for v in x) for x in (q64, g64))
+    old_c, old_g = cpu.limite(limite), gpu.limite(limite)
+    try:
+        f4 = cpu.ops.atencao(Q4, Bt, T, RD.H4)
+        f64 = gpu.ops.atencao(Q64, Bt, T, RD.H64)
+        b4 = cpu.ops.atencao_back(G4, Q4, f4[1], Bt, T, RD.H4)
+        b64 = gpu.ops.atencao_back(G64, Q64, f64[1], Bt, T, RD.H64)
+    finally:
+        cpu.limite(old_c)
+        gpu.limite(old_g)
+    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt)
+    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64])

@@ -102,6 +102,18 @@ def test_erro_no_grafo():
     msg = str(e.value)
     assert "forward / embedding" in msg and "linha 401, coluna 0" in msg and "valor    : 300" in msg, msg
     assert "operacao : embed" in msg
+    # the inputs of the failing launch were saved (registro.py's contract with jatai_cuda/registro.py:126-130):
+    # the embedding weights as the graph holds them and the replay's tokens, which reproduce the event on the CPU
+    ev = reg.ultimo_evento
+    assert ev.lancamento.op == "embed" and ev.idx == 401 * 256 and ev.valor == 300 and ev.arquivo in msg
+    salvo = torch.load(ev.arquivo, weights_only=True)
+    assert set(salvo) == {"W", "tok"}
+    assert torch.equal(salvo["W"], m.p["emb"][0].cpu())
+    assert int(salvo["tok"].reshape(-1)[401]) == 300 and torch.equal(salvo["tok"].reshape(-1).long(), ruim.reshape(-1).cpu())
+    from oracle.ops_oracle import OpsOraculo
+    W = (salvo["W"], m.p["emb"][1].cpu())
+    with pytest.raises(IndexError, match="1 tokens outside the vocabulary of 256"):
+        OpsOraculo(128).embed(W, salvo["tok"])
 
 
 @pytest.mark.parametrize("dw_lote", [True, False], ids=["otimizador-no-gemm", "tabela"])

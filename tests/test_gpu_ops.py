@@ -51,6 +51,27 @@ def test_caso_vs_spec(blk, i):
                     f"(flat index, gpu, oracle, count): {difs}")
 
 
+DOMINIO = CS.casos_dominio()
+
+
+@pytest.mark.parametrize("blk", [128, 32])
+@pytest.mark.parametrize("i", range(len(DOMINIO)), ids=[n for n, _ in DOMINIO])
+def test_dominio_vs_spec(blk, i):
+    """The rest of the reference's shape domain (rms widths 384-896, softmax V = 384 / 640, head-width-4 attention
+    at H = 32 and T = 32 / 96) against the spec's hashes (tests/golden/ops_dominio_blk*.json)."""
+    gold = _gold(f"ops_dominio_blk{blk}.json")[i]
+    nome, fn = DOMINIO[i]
+    gpu = GPU(blk, vigiar=True)
+    rec = CS.Gravador(gpu.ops, host)
+    saida = fn(rec, CS.Gen(R.substream(1000 + i, nome), blk, gpu.dev), gpu)
+    torch.cuda.synchronize()
+    if [list(x) for x in rec.log] != [list(x) for x in gold["chamadas"]]:
+        cpu = CPU(blk)
+        ref = fn(cpu.ops, CS.Gen(R.substream(1000 + i, nome), blk, cpu.dev), cpu)
+        difs = [primeira_diferenca(host(a), host(b)) for a, b in zip(CS.plano(saida), CS.plano(ref))]
+        pytest.fail(f"{nome} (BLK={blk}) differs from the spec; first difference per output vs the oracle: {difs}")
+
+
 @pytest.mark.parametrize("blk", [32, 128])
 def test_config1(blk):
     gold = _gold("config1.json")[str(blk)]
@@ -234,7 +255,8 @@ def _gemm_modos(ops, A, B, X):
 def test_gemm_k_longo_vs_oraculo(blk, K):
     """K beyond 4096 (up to 65536; the reference stops at 4096, ops.py:336-337): the kernel walks K in chunks of
     4096 with the row maxima RA, RB over all of K; every mode equals the CPU oracle, at the default K-split and
-    with K-splits forced on (split target 4096), K = 4608 leaving a short last chunk."""
+    with K-splits forced off (split target 1: one K-split) and on (split target 4096), K = 4608 leaving a short
+    last chunk."""
     gpu, cpu = GPU(blk), CPU(blk)
     M, N = 64, 256
     s = lambda t: R.substream(77, f"{t} {blk} {K}")
@@ -242,7 +264,7 @@ def test_gemm_k_longo_vs_oraculo(blk, K):
     B = R.bloco(s("B"), N, K, blk, espalha=5, e0=-12)
     X = R.bloco(s("X"), M, N, blk, espalha=3, e0=2)
     ref = [CS.plano(t) for t in _gemm_modos(cpu.ops, *[tuple(cpu.dev(v) for v in T) for T in (A, B, X)])]
-    for alvo in (1024, 4096):
+    for alvo in (1, 1024, 4096):
         gpu.ops.lib.jt_gemm_split(alvo)
         try:
             out = [CS.plano(t) for t in _gemm_modos(gpu.ops, *[tuple(gpu.dev(v) for v in T) for T in (A, B, X)])]
@@ -252,6 +274,27 @@ def test_gemm_k_longo_vs_oraculo(blk, K):
         for modo, (a, b) in enumerate(zip(out, ref)):
             for x, y in zip(a, b):
                 assert np.array_equal(host(x), host(y)), f"mode {modo}, split target {alvo}: {primeira_diferenca(host(x), host(y))}"
+
+
+def test_gemm_cru_lote_config5_dw():
+    """The weight-gradient GEMMs of a BASELINE config-5 step (K = 16384 tokens) as the step runs them: one grouped
+    launch (gemm_cru_lote -> k_gemm_lote, one K-split, four 4096-value chunks of shift tables) of the layer's five
+    shapes plus the output and embedding gradients, each equal to the CPU oracle's raw GEMM (ops.py:95-108)."""
+    blk, K, D, FF, V = 32, 16384, 512, 2048, 256
+    gpu, cpu = GPU(blk), CPU(blk)
+    formas = [("qkv", 3 * D, D), ("out-proj", D, D), ("ffn-up", FF, D), ("ffn-down", D, FF), ("out", V, D), ("emb", V, D)]
+    s = lambda t: R.substream(303, t)
+    ins = [(R.bloco(s(n + " dY"), M, K, blk, espalha=6, e0=-24, zera=0.02), R.bloco(s(n + " X"), N, K, blk, espalha=4, e0=-6))
+           for n, M, N in formas]
+    pares = [(tuple(gpu.dev(v) for v in a), tuple(gpu.dev(v) for v in b), None) for a, b in ins]
+    assert gpu.ops.lib.jt_gemm_divisoes(3 * D, D, K, 1) >= 1
+    out = gpu.ops.gemm_cru_lote(pares)
+    gpu.reg.confere_device()
+    for (n, M, N), (a, b), G in zip(formas, ins, out):
+        ref = cpu.ops.gemm(tuple(cpu.dev(v) for v in a), tuple(cpu.dev(v) for v in b), cru=True)
+        for x, y, parte in zip(G, ref, ("acc", "e")):
+            d = primeira_diferenca(host(x), host(y))
+            assert d is None, f"dW {n} [{M}x{N}, K={K}] {parte}: (flat index, gpu, oracle, count) = {d}"
 
 
 def test_gemm_k_longo_acumulador_fora_do_formato():

@@ -5,7 +5,10 @@ the integer softmax outputs (d_alvo, soma) of the CPU oracle's trace, hence the 
   trace_r600.jsonl  600 steps at the reference model shape (BLK 128, 64 heads x 4); its first 32 steps are the
                     reference spec's own (trace_r.json), the rest the oracle's extension of them;
   trace_c4.jsonl    BASELINE config 4 (D 512, 8 heads x 64, FF 2048, 12 layers, Bt 8, T 256, BLK 32): the
-                    steps the oracle wrote (parity unpinned by the reference beyond the head-width-4 reduction).
+                    steps the oracle wrote (parity unpinned by the reference beyond the head-width-4 reduction);
+  trace_c5.jsonl    BASELINE config 5 at its workload: 24 layers, Bt 64 x T 256 = 16384 tokens, the 16-bit
+                    residual stream (modelo.py:60-130) -- the step bench.py times, with its grouped
+                    weight-gradient GEMMs at K = 16384.
 
 Both fixtures come from tests/golden/make_trace_oracle.py."""
 import json
@@ -30,7 +33,7 @@ def _le(nome):
     return linhas[0], linhas[1:]
 
 
-@pytest.mark.parametrize("nome", ["trace_r600.jsonl", "trace_c4.jsonl"])
+@pytest.mark.parametrize("nome", ["trace_r600.jsonl", "trace_c4.jsonl", "trace_c5.jsonl"])
 def test_traco_longo_grafo(nome):
     from jatai_amd import ops as O
     from jatai_amd.modelo import Modelo, PassoGravado, perda_de
@@ -41,7 +44,7 @@ def test_traco_longo_grafo(nome):
     O.BLK = f["BLK"]
     try:
         reg = Registro(LOGS, "traco_longo", eco=False)
-        m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", O.OpsHip(reg), reg)
+        m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], "cuda", O.OpsHip(reg), reg, r16=f.get("r16", False))
         assert {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()} == cab["init"]
         pg = PassoGravado(m, f["Bt"], f["T"], f["k_lr"])
         print(f"{nome}: {len(passos)} steps, {len(pg.lancamentos)} launches per replay", flush=True)

@@ -107,6 +107,24 @@ def test_ops_vs_golden(blk):
     assert not falhas, f"oracle differs from the spec at BLK={blk}: {falhas}"
 
 
+@pytest.mark.parametrize("blk", [128, 32])
+def test_ops_dominio_vs_golden(blk):
+    """The rest of the reference's shape domain (row widths 384-896, softmax V = 384 / 640, head-width-4
+    attention at H = 32 and T = 32 / 96) against the spec's own outputs."""
+    gold = _gold(f"ops_dominio_blk{blk}.json")
+    be = BE(blk)
+    casos = CS.casos_dominio()
+    assert [c["nome"] for c in gold] == [n for n, _ in casos]
+    falhas = []
+    for i, ((nome, fn), gc) in enumerate(zip(casos, gold)):
+        rec = CS.Gravador(be.ops, host)
+        g = CS.Gen(R.substream(1000 + i, nome), blk, be.dev)
+        fn(rec, g, be)
+        if [list(x) for x in rec.log] != [list(x) for x in gc["chamadas"]]:
+            falhas.append(nome)
+    assert not falhas, f"oracle differs from the spec at BLK={blk}: {falhas}"
+
+
 def test_config1_vs_golden():
     gold = _gold("config1.json")
     for blk in (32, 128):
@@ -252,3 +270,144 @@ def test_ops_conferido_aponta_divergencia(tmp_path):
             OpsConferido(reg, Torto(32)).soma(X, Y)
     finally:
         O.BLK = 128
+
+
+# ---------------------------------------------------------------- pins of the functions without a spec
+def test_hash32_e_lowbias32():
+    """The stochastic rounding's hash (jatai_cuda.cu:146-149) is Wellons' lowbias32: two xorshift-multiply rounds
+    with 0x7feb352d and 0x846ca68b. Checked through its published inverse (xorshifts undone, the multipliers'
+    inverses mod 2^32: 0x43021123 and 0x1d69e2a5), which must return every input, and the multipliers'
+    inverses are checked as such."""
+    assert (0x846CA68B * 0x43021123) % (1 << 32) == 1 and (0x7FEB352D * 0x1D69E2A5) % (1 << 32) == 1
+    x = np.concatenate([np.arange(0, 4096), R.uniform_int(17, (20000,), 0, (1 << 32) - 1)]).astype(np.int64)
+    h = OpsOraculo.prim("hash32", x).astype(np.uint64)
+    M = np.uint64(0xFFFFFFFF)
+    y = h ^ (h >> np.uint64(16))
+    y = (y * np.uint64(0x43021123)) & M
+    y = y ^ (y >> np.uint64(15)) ^ (y >> np.uint64(30))
+    y = (y * np.uint64(0x1D69E2A5)) & M
+    y = y ^ (y >> np.uint64(16))
+    assert np.array_equal(y.astype(np.int64), x)
+    assert len(np.unique(h)) == len(np.unique(x))          # a bijection
+    assert int(OpsOraculo.prim("hash32", np.array([0]))[0]) == 0
+
+
+def _quant_exata(V, S, mbits, lim, blk):
+    """Block quantization of exact dyadic values V_k 2^S_k (Python ints), the spec's rules (ops.py:58-72) on exact
+    values: topo = max(S + bitlen(V)), E = topo - mbits, q = round half even (V 2^(S - E)), E + 1 if some |q| > lim,
+    zero block if all V are 0 or E < -126. Returns (mantissas, E) per block."""
+    def rhe(v, s):                                         # v 2^-s rounded half to even (s may be <= 0)
+        if s <= 0:
+            return v << -s
+        q, r = divmod(v, 1 << s)
+        meio = 1 << (s - 1)
+        return q + (1 if r > meio or (r == meio and q & 1) else 0)
+    ms, Es = [], []
+    for b in range(0, len(V), blk):
+        vb, sb = V[b:b + blk], S[b:b + blk]
+        topos = [s + abs(v).bit_length() for v, s in zip(vb, sb) if v]
+        if not topos:
+            ms += [0] * blk; Es.append(E_ZERO_)
+            continue
+        E = max(topos) - mbits
+        q = [rhe(v, E - s) for v, s in zip(vb, sb)]
+        if any(abs(x) > lim for x in q):
+            E += 1
+            q = [rhe(v, E - s) for v, s in zip(vb, sb)]
+        if E < -126:
+            ms += [0] * blk; Es.append(E_ZERO_)
+            continue
+        ms += [max(-lim, min(lim, x)) for x in q]
+        Es.append(E)
+    return ms, Es
+
+
+E_ZERO_ = -127
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_r16_formas_fechadas(blk):
+    """The 16-bit residual trio (no spec; jatai_cuda.cu:446-531) against closed forms on exact values:
+    para16 is exact (m << 7, E - 7; zero blocks stay zero blocks); para8 is the INT8 block quantization of the
+    exact R16 value; soma16 is the 15-bit block quantization (|m| <= 32767) of the exact sum x + y, rounded once --
+    its alignment to ec = max(ex + 15, ey + 7) - 28 loses nothing that the final rounding keeps. Exponent gaps from
+    -30 to +30 between x and y, and zero blocks on either side."""
+    ops = OpsOraculo(blk)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    Rn, C = 64, 4 * blk
+    x8 = R.bloco(91, Rn, C, blk, espalha=6, e0=-3, zera=0.1)
+    p16 = ops.para16(tuple(t(v) for v in x8))
+    m16, E16 = host(p16[0]).astype(np.int64), host(p16[1]).astype(np.int64)
+    assert np.array_equal(m16, x8[0].astype(np.int64) << 7)
+    assert np.array_equal(E16, np.where(x8[1] == E_ZERO_, E_ZERO_, x8[1].astype(np.int64) - 7))
+    # R16 inputs with full 15-bit mantissas and exponents spread around the INT8 addend's
+    xm = R.uniform_int(92, (Rn, C), -32767, 32767)
+    xm[:, :blk] //= 300                                      # a block with small mantissas (not normalized)
+    xE = R.uniform_int(93, (Rn, C // blk), -20, 20)
+    zx = R.uniform01(94, (Rn, C // blk)) < 0.05
+    xm.reshape(Rn, C // blk, blk)[zx] = 0
+    xE[zx] = E_ZERO_
+    ym, yE = R.bloco(95, Rn, C, blk, espalha=30, e0=-5, zera=0.1)
+    X16 = (t(xm.astype(np.int16)), t(xE.astype(np.int8)))
+    Y = (t(ym), t(yE))
+    z = ops.soma16(X16, Y)
+    zm, zE = host(z[0]).astype(np.int64).reshape(-1), host(z[1]).astype(np.int64).reshape(-1)
+    p8 = ops.para8(X16)
+    pm, pE = host(p8[0]).astype(np.int64).reshape(-1), host(p8[1]).astype(np.int64).reshape(-1)
+    for r in range(Rn):
+        V, S, V8, S8 = [], [], [], []
+        for b in range(C // blk):
+            ex, ey = int(xE[r, b]), int(yE[r, b])
+            for k in range(b * blk, (b + 1) * blk):
+                xv = int(xm[r, k]) if ex != E_ZERO_ else 0
+                yv = int(ym[r, k]) if ey != E_ZERO_ else 0
+                s0 = min(ex, ey)
+                V.append((xv << (ex - s0)) + (yv << (ey - s0)))
+                S.append(s0)
+                V8.append(xv)
+                S8.append(ex)
+        mq, Eq = _quant_exata(V, S, 15, 32767, blk)
+        assert list(zm[r * C:(r + 1) * C]) == mq and list(zE[r * (C // blk):(r + 1) * (C // blk)]) == Eq, f"soma16 row {r}"
+        mq, Eq = _quant_exata(V8, S8, 7, 127, blk)
+        assert list(pm[r * C:(r + 1) * C]) == mq and list(pE[r * (C // blk):(r + 1) * (C // blk)]) == Eq, f"para8 row {r}"
+
+
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_reduz_ao_spec_hd4(limite):
+    """The head-width-64 attention (the declared extension run at configs 4 and 5) on inputs where each head
+    carries one head-width-4 head of the spec's shape (tests/reducoes.py) gives that head's outputs: P, o and,
+    in the backward (both variants), gq, gk, gv. The head-width-4 side is the oracle code the reference's goldens
+    pin (ops.py:186-258). This pins the extension's alignment over a head's blocks, its score shift
+    -(log2 hd)/2, its ALiBi schedule 8 - 8h/H and its backward at T <= 128."""
+    import reducoes as RD
+    Bt, T = 2, 128
+    ops = OpsOraculo(32, limite=limite)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    (q4, g4), (q64, g64) = RD.problemas(5150, Bt, T)
+    Q4, G4, Q64, G64 = [tuple(t(v) for v in x) for x in (q4, g4, q64, g64)]
+    f4, f64 = ops.atencao(Q4, Bt, T, RD.H4), ops.atencao(Q64, Bt, T, RD.H64)
+    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt)
+    b4 = ops.atencao_back(G4, Q4, f4[1], Bt, T, RD.H4)
+    b64 = ops.atencao_back(G64, Q64, f64[1], Bt, T, RD.H64)
+    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64])
+
+
+def test_atencao_hd64_q_zero_so_alibi():
+    """With q = 0 every score is the ALiBi term alone, u_ij = -((i - j) << (8 - 8h/H)): P has the closed form
+    min((e_ij (2^28 // sum_j e_ij) + 2^19) >> 20, 255), e_ij = exp_int((i - j) << incl) >> 3 (exp_int pinned by
+    primitives.json), for every head of the head-width-64 problem (H = 8: slopes 2^0 .. 2^-7), T = 256."""
+    Bt, T, H, D, blk = 1, 256, 8, 512, 32
+    m = R.uniform_int(97, (Bt * T, 3 * D), -127, 127).astype(np.int8)
+    m[:, :D] = 0
+    E = R.uniform_int(98, (Bt * T, 3 * D // blk), -9, -3).astype(np.int8)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    (_, _), P = OpsOraculo(blk).atencao((t(m), t(E)), Bt, T, H)
+    P = host(P).reshape(H, T, T)                               # [h][j][i]
+    ex = OpsOraculo.prim("exp_int", np.arange(0, 256 << 8))
+    for h in range(H):
+        incl = 8 - (8 * h) // H
+        for i in (0, 1, 37, 128, 255):
+            e = [int(ex[min((i - j) << incl, len(ex) - 1)]) >> 3 for j in range(i + 1)]
+            inv = (1 << 28) // sum(e)
+            esperado = [min((v * inv + (1 << 19)) >> 20, 255) for v in e] + [0] * (T - i - 1)
+            assert list(P[h, :, i]) == esperado, (h, i)
