@@ -668,6 +668,46 @@ int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const v
     if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
     return atencao_back_ws(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, ws, ws_bytes, false, kid);
 }
+// No reference counterpart: jt_atencao_back_ws without a workspace argument and without any allocation, for callers
+// that cannot allocate (code under graph capture, serving loops, harnesses that forbid hipMalloc). The workspace is
+// the file-scope device array `scratch` (SCRATCH_BYTES, held by every GPU the library runs on until the process
+// ends); a call needing more (jt_atencao_back_ws_bytes > SCRATCH_BYTES) returns hipErrorOutOfMemory and launches
+// nothing. Nothing in the workspace has to start at zero (every slot a kernel reads was written earlier in the
+// same call), so the array needs no clearing. Calls that overlap on one GPU (two streams, two host threads) share
+// the array and race.
+constexpr size_t SCRATCH_BYTES = (size_t)16 << 20;
+static __device__ __align__(256) char scratch[SCRATCH_BYTES];
+}  // extern "C"
+// the device address of `scratch` on each device, looked up once per device with that device current (each GPU
+// holds its own copy of the array; the array's name in host code is not a device address)
+static void* scratch_por_device[64];
+static hipError_t scratch_do_device(void** p) {
+    int dev = 0;
+    hipError_t c = hipGetDevice(&dev);
+    if (c != hipSuccess) return c;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!scratch_por_device[dev]) {
+        void* q = nullptr;
+        c = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+        if (c != hipSuccess) return c;
+        scratch_por_device[dev] = q;
+    }
+    *p = scratch_por_device[dev];
+    return hipSuccess;
+}
+extern "C" {
+long long jt_scratch_bytes() { return (long long)SCRATCH_BYTES; }
+int jt_atencao_back_sem_alocar(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt,
+                               int T, int H, int D, int GA, int limite, int kid) {
+    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
+    const long long n = jt_atencao_back_ws_bytes(Bt, T, H, D);
+    if (n <= 0 || n > (long long)SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
+    void* ws = nullptr;
+    const hipError_t c = scratch_do_device(&ws);
+    if (c != hipSuccess) return (int)c;
+    return atencao_back_ws(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, ws, n, false, kid);
+}
 // No reference counterpart: jt_atencao_back_ws writing the gradient quantized to block format (Gm int8 [M, 3D],
 // GE int8 [M, 3D/32]), equal to jt_quant of the raw gradient. Head width 64 on matrix cores at BLK = 32 only;
 // hipErrorNotSupported otherwise.
