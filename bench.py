@@ -66,6 +66,37 @@ def args():
     return ap.parse_args()
 
 
+def tempo_grafo(ops, chamadas, vezes, reps=3):
+    """Average ms per call of the callables `chamadas`, captured `vezes` times each in one hipGraph on the stream the
+    library launches on and replayed `reps` times; HIP events recorded on that replay stream bracket the replays
+    (inputs resident in HBM)."""
+    import torch
+    for f in chamadas:
+        f()
+    torch.cuda.synchronize()
+    grafo = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(grafo):
+        ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+        try:
+            for _ in range(vezes):
+                for f in chamadas:
+                    f()
+        finally:
+            ops.lib.jt_stream(None)
+    grafo.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    with torch.cuda.stream(s):
+        ev[0].record(s)
+        for _ in range(reps):
+            grafo.replay()
+        ev[1].record(s)
+    torch.cuda.synchronize()
+    del grafo
+    return ev[0].elapsed_time(ev[1]) / (reps * vezes * len(chamadas))
+
+
 def gemm_formas(c):
     """(M, N, K, mode, count) of every GEMM of one step (modelo.py:51-134), one entry per distinct shape and mode:
     mode 0 block output, 1 raw, 2 + residual add, 3 + ReLU^2, 4 ReLU^2 backward."""
@@ -117,31 +148,207 @@ def mede_gemms(O, ops, c, rep=20):
         saida = ops.gemm(A, B, cru=True) if modo == 1 else None
         chama = {0: lambda: ops.gemm(A, B), 1: lambda: ops.gemm(A, B, cru=True, saida=saida), 2: lambda: ops.gemm_soma(A, B, X),
                  3: lambda: ops.gemm_relu2(A, B), 4: lambda: ops.gemm_relu2_back(A, B, X)}[modo]
-        chama()
-        torch.cuda.synchronize()
-        grafo = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(grafo):
-            ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
-            try:
-                for _ in range(rep):
-                    chama()
-            finally:
-                ops.lib.jt_stream(None)
-        grafo.replay()
-        torch.cuda.synchronize()
-        s = torch.cuda.Stream()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        with torch.cuda.stream(s):
-            ev[0].record(s)
-            for _ in range(3):
-                grafo.replay()
-            ev[1].record(s)
-        torch.cuda.synchronize()
-        ms = ev[0].elapsed_time(ev[1]) / (3 * rep)
+        ms = tempo_grafo(ops, [chama], rep)
         out[nome] = dict(M=M, N=N, K=K, modo=modo, por_passo=cont, ms=ms, tops=2 * M * N * K / (ms * 1e-3) / 1e12,
                          kernel=gemm_kernel(O, ops, M, N, K, modo))
-        del grafo
     return out
+
+
+def formas_dw(c):
+    """(name, M, N) of the weight-gradient GEMMs of one step, in the order the step groups them into one launch
+    (modelo.py:96-134 computes them in this order): output projection, then per layer from the last ffn-down,
+    ffn-up, out-proj, qkv, then the embedding. K = the step's tokens. C = T(dY) . T(X)^T, raw output."""
+    M, D, FF, V, L = c["Bt"] * c["T"], c["D"], c["FF"], c["V"], c["L"]
+    f = [("out", V, D)]
+    for _ in range(L):
+        f += [("ffn-down", D, FF), ("ffn-up", FF, D), ("out-proj", D, D), ("qkv", 3 * D, D)]
+    return f + [("emb", V, D)], M
+
+
+def mede_dw_lote(O, ops, c, rep=7):
+    """The step's dominant kernel at config 4: every weight-gradient GEMM of a step in one grouped launch
+    (gemm_cru_lote -> k_gemm_lote), with operands shaped and scaled like the step's (transposed gradients
+    T(dY) [N_out, M], exponents around -20; transposed activations T(X) [N_in, M], around -6). In the step this
+    launch runs once, right after the batched transposes that write its operands (so most of them are still in
+    the 256 MB last-level cache), between lighter kernels. Here likewise: before each of `rep` timed replays of
+    the one-launch hipGraph, the operands are rewritten by copies from other buffers (untimed); HIP events on
+    the replay stream bracket the launch alone, and the median is kept."""
+    import torch
+    blk = c["BLK"]
+    g = torch.Generator().manual_seed(4)
+
+    def bloco(R, C, e0):
+        return (torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda(),
+                (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda())
+    formas, K = formas_dw(c)
+    pares, fontes = [], []
+    for _, M, N in formas:
+        pares.append((bloco(M, K, -20), bloco(N, K, -6),
+                      (torch.empty(M, N, dtype=torch.int32, device="cuda"), torch.empty(M, N, dtype=torch.int16, device="cuda"))))
+        fontes.append((tuple(t.clone() for t in pares[-1][0]), tuple(t.clone() for t in pares[-1][1])))
+    f = lambda: ops.gemm_cru_lote(pares)
+    f()
+    torch.cuda.synchronize()
+    grafo = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(grafo):
+        ops.lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+        try:
+            f()
+        finally:
+            ops.lib.jt_stream(None)
+    s = torch.cuda.Stream()
+    vezes = []
+    for _ in range(rep):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            for (a_, b_, _), (fa, fb) in zip(pares, fontes):       # the operands just written, as in the step
+                for d_, f_ in zip((*a_, *b_), (*fa, *fb)):
+                    d_.copy_(f_)
+            ev[0].record(s)
+            grafo.replay()
+            ev[1].record(s)
+        torch.cuda.synchronize()
+        vezes.append(ev[0].elapsed_time(ev[1]))
+    del grafo
+    ms = sorted(vezes)[len(vezes) // 2]
+    ops_alg = sum(2 * M * N * K for _, M, N in formas)
+    tiles = sum((M // 32) * (N // 128) for _, M, N in formas)
+    lote = 64                                   # GEMMs per grouped launch (LOTE_G)
+    nk = 1
+    while nk < 4 and tiles * 2 * nk <= 1024 and (K // blk) >= 8 * nk:
+        nk *= 2
+    return dict(ms=ms, ms_each=[round(x, 4) for x in vezes], ops=ops_alg, gemms=len(formas), K=K, launches=(len(formas) + lote - 1) // lote,
+                symbol=f"k_gemm_lote<{blk}, {nk}>", workgroups=tiles, threads=256 * nk)
+
+
+def mede_dw_no_passo(ops, reg, c, rep=10):
+    """Duration of the grouped weight-gradient launch inside the training step: the step is captured as three
+    hipGraphs sharing one memory pool -- everything before that launch, the launch alone, everything after --
+    and replayed in order on one stream, with HIP events recorded on that stream between the first and second
+    and the second and third replays. The launch thus runs on the operands the step has just produced, as in
+    the one-graph step. Returns (median ms, the replays' ms)."""
+    import torch
+    from jatai_amd.modelo import Modelo
+    m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, "cuda", ops, reg, r16=c["r16"])
+    g = torch.Generator().manual_seed(2)
+    lote = lambda: torch.randint(0, c["V"], (c["Bt"], c["T"] + 1), generator=g).cuda()
+    x = lote()
+    reg.novo_passo(0)
+    m.passo(x[:, :-1].contiguous(), x[:, 1:].contiguous(), k_lr=4)
+    reg.fim_passo()
+    if m.otimizador_fundido and not m._otim_no_gemm():
+        m._prepara_otimizador()
+    tok = torch.zeros(c["Bt"], c["T"], dtype=torch.int32, device="cuda")
+    alvo = torch.zeros_like(tok)
+    gs = [torch.cuda.CUDAGraph() for _ in range(3)]
+    m.marcas["gradientes dos pesos"] = (lambda: (gs[0].capture_end(), gs[1].capture_begin(pool=gs[0].pool())),
+                                        lambda: (gs[1].capture_end(), gs[2].capture_begin(pool=gs[0].pool())))
+    m.perda_inteira = True
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        ops.lib.jt_stream(s.cuda_stream)
+        try:
+            gs[0].capture_begin()
+            m.passo(tok, alvo, k_lr=4)
+            gs[2].capture_end()
+        finally:
+            ops.lib.jt_stream(None)
+            m.marcas.clear()
+    vezes = []
+    for i in range(rep + 2):
+        x = lote()
+        tok.copy_(x[:, :-1])
+        alvo.copy_(x[:, 1:])
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            gs[0].replay()
+            ev[0].record(s)
+            gs[1].replay()
+            ev[1].record(s)
+            gs[2].replay()
+        torch.cuda.synchronize()
+        if i >= 2:
+            vezes.append(ev[0].elapsed_time(ev[1]))
+    del gs
+    return sorted(vezes)[rep // 2], [round(v, 4) for v in vezes]
+
+
+def mede_otimizador_e_transpostas(O, ops, c, rep=5):
+    """The fused optimizer over every weight of a step (50 tensors at config 4) and the step's three batched
+    transposes (weights, forward activations, gradients; modelo.py's lists), at the step's shapes."""
+    import torch
+    blk, M, D, FF, V, L = c["BLK"], c["Bt"] * c["T"], c["D"], c["FF"], c["V"], c["L"]
+    g = torch.Generator().manual_seed(6)
+
+    def bloco(R, C, e0=-8):
+        return (torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).cuda(),
+                (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda())
+    pesos = [(D, FF), (FF, D), (D, D), (3 * D, D)] * L + [(V, D), (V, D)]
+    itens = []
+    for R, C in pesos:
+        gc = (torch.randint(-(1 << 20), 1 << 20, (R, C), generator=g, dtype=torch.int32).cuda(),
+              torch.randint(-40, -30, (R, C), generator=g).to(torch.int16).cuda())
+        itens.append((gc, bloco(R, C, -15), bloco(R, C, -9), bloco(R, C, -20)))
+    tab = ops.tabela_otimizador(itens)
+    n_el = sum(R * C for R, C in pesos)
+    b = 1 + 1 / blk
+    ms_otim = tempo_grafo(ops, [lambda: ops.otimizador(tab, 4, True)], rep)
+    del itens, tab
+    listas = {
+        "weights": [bloco(R, C) for R, C in [(D, FF), (FF, D), (D, D), (3 * D, D)] * L + [(V, D)]],
+        "activations": [bloco(M, C) for C in [FF, D, D, D] * L + [D]],
+        "gradients": [bloco(M, C) for C in [V] + [D, D, 3 * D] * L + [V, D]],
+    }
+    tr = {}
+    for nome, xs in listas.items():
+        ms = tempo_grafo(ops, [lambda xs=xs: ops.transpoe_lote(xs)], rep)
+        el = sum(x[0].numel() for x in xs)
+        tr[nome] = dict(ms=ms, tensors=len(xs), bytes=2 * b * el)
+    return dict(otimizador=dict(ms=ms_otim, tensors=len(pesos), bytes=(6 + 6 * b) * n_el), transpostas=tr)
+
+
+def tabela_kernels(c, gem, dw, ops2, ot, ms_passo):
+    """The step's kernels by time per step (each measured alone at the step's shape, launches captured in a
+    graph): GEMM shapes in their step modes (the weight-gradient ones as the one grouped launch the step runs),
+    attention forward and backward, the row kernels, the fused optimizer and the batched transposes. Each row:
+    microseconds per launch, launches per step, microseconds per step, the share of the measured step, and its
+    roofline figure: TOP/s against the i8 MFMA peak and the format's VALU bound (GEMMs), or algorithmic GB/s
+    against 8 TB/s."""
+    L = c["L"]
+    lim = 2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS
+    lin = []
+    for nome, v in gem.items():
+        if nome.startswith("dW "):
+            continue
+        t = 2 * v["M"] * v["N"] * v["K"] / (v["ms"] * 1e-3)
+        lin.append(dict(name=f"gemm {nome}", kernel=v["kernel"]["symbol"], us=v["ms"] * 1e3, per_step=v["por_passo"],
+                        TOPS=t / 1e12, frac_i8_peak=t / PEAK_I8, frac_format_bound=t / lim))
+    t = dw["ops"] / (dw["ms"] * 1e-3)
+    lin.append(dict(name=f"weight-gradient GEMMs ({dw['gemms']} in one launch)", kernel=dw["symbol"], us=dw["ms"] * 1e3,
+                    per_step=dw["launches"], TOPS=t / 1e12, frac_i8_peak=t / PEAK_I8, frac_format_bound=t / lim))
+    for nome, chave, n in (("attention forward", "atencao_q", L), ("attention backward", "atencao_back_q", L)):
+        if chave in ops2:
+            lin.append(dict(name=nome, kernel="k_atf_prep + k_atf" if "back" not in chave else "k_atb_prep + k_atb1 + k_atb2 + k_atbqkv",
+                            us=ops2[chave]["us"], per_step=n))
+    for nome, chave, n in (("rms", "rms", 2 * L + 1), ("rms_back + soma", "rms_back+soma", 2 * L)):
+        e = ops2[chave]
+        lin.append(dict(name=nome, kernel=f"k_{chave.split('+')[0]}", us=e["us"], per_step=n, GBs=e["GB_s"], frac_hbm=e["frac_hbm"]))
+    o = ot["otimizador"]
+    lin.append(dict(name=f"fused optimizer ({o['tensors']} tensors)", kernel=f"k_otimizador<{c['BLK']}>", us=o["ms"] * 1e3, per_step=1,
+                    GBs=o["bytes"] / (o["ms"] * 1e-3) / 1e9, frac_hbm=o["bytes"] / (o["ms"] * 1e-3) / PEAK_HBM))
+    for nome, e in ot["transpostas"].items():
+        lin.append(dict(name=f"batched transposes, {nome} ({e['tensors']} tensors)", kernel="k_transpoe_lote", us=e["ms"] * 1e3,
+                        per_step=1, GBs=e["bytes"] / (e["ms"] * 1e-3) / 1e9, frac_hbm=e["bytes"] / (e["ms"] * 1e-3) / PEAK_HBM))
+    for e in lin:
+        e["us_per_step"] = e["us"] * e["per_step"]
+        e["share_of_step"] = e["us_per_step"] / (ms_passo * 1e3)
+        for k, v in list(e.items()):
+            if isinstance(v, float):
+                e[k] = round(v, 4 if k.startswith("frac") or k == "share_of_step" else 2)
+    return sorted(lin, key=lambda e: -e["us_per_step"])
 
 
 def mede_ops(O, ops, c, reg, rep=20, giga=1 << 30):
@@ -320,6 +527,13 @@ def trafego_despacha(O, ops, c):
             chama()
             torch.cuda.synchronize()
         print(f"dispatch: {nome} {gemm_kernel(O, ops, M, N, K, modo)['symbol']} x2", flush=True)
+    # the step's grouped weight-gradient launch (its dominant kernel), twice
+    formas, K = formas_dw(c)
+    pares = [(bloco(M, K, -20), bloco(N, K, -6), None) for _, M, N in formas]
+    for _ in range(2):
+        ops.gemm_cru_lote(pares)
+        torch.cuda.synchronize()
+    print(f"dispatch: dW grouped k_gemm_lote<{blk}, 1> x2", flush=True)
 
 
 def trafego(nome):
@@ -335,8 +549,9 @@ def trafego(nome):
 
 
 def cpu_baseline(c, segundos):
-    """The CPU oracle (int64 C++ restatement of the spec, OpenMP) running the same model's training step on a
-    bounded sample: batches of 2 sequences until `segundos` of wall time, tokens/s = tokens / wall."""
+    """The CPU oracle (int64 C++ restatement of the spec, OpenMP) running the same model's training step at the
+    benchmarked batch (Bt sequences of T tokens) on a bounded sample: whole steps until `segundos` of wall time,
+    tokens/s = tokens / wall."""
     import torch
     from jatai_amd import ops as O
     from jatai_amd.modelo import Modelo
@@ -349,7 +564,7 @@ def cpu_baseline(c, segundos):
     O.BLK = c["BLK"]
     m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, "cpu", OpsOraculo(c["BLK"]), Nada(), r16=c["r16"])
     g = torch.Generator().manual_seed(11)
-    bt = 2
+    bt = c["Bt"]
     n = 0
     t0 = time.perf_counter()
     while True:
@@ -375,20 +590,22 @@ def cpu_modelo():
     return "unknown CPU"
 
 
-def cpu_baseline_fp32(c, segundos):
-    """PyTorch float32 on the host cores: the reference's fp32 comparison model (ModeloFloat,
+def mede_fp32(c, segundos, dev="cpu", passos_min=2):
+    """PyTorch float32 training of the reference's fp32 comparison model (ModeloFloat,
     treino_int8_gpu/jatai_int8.py:399-428, without its ablation quantization points) at the same shape and batch,
     initialised from the integer model's seed-0 weights dequantized (m * 2^E), trained with
-    SGD(lr=2^-4, momentum=0.875) as jatai_cuda/treino_cuda.py:153-162. ALiBi slopes and the 1/sqrt(head width)
-    score scale follow the integer attention (slope 2^-floor(8h/H); 1/2 at the reference's head width 4).
-    One warm-up step, then whole steps until `segundos` of wall time (at least two)."""
+    SGD(lr=2^-4, momentum=0.875) as jatai_cuda/treino_cuda.py:153-162 does for its fp32 comparison. ALiBi slopes and
+    the 1/sqrt(head width) score scale follow the integer attention (slope 2^-floor(8h/H); 1/2 at the reference's
+    head width 4). On `dev` ("cpu": the host cores, torch's threads; "cuda": the GPU, whose fp32 comparison the
+    reference makes on its own GPU). One warm-up step, then whole steps until `segundos` of wall time (at least
+    `passos_min`), synchronized on the GPU before each clock read."""
     import torch
     import torch.nn.functional as F
     from jatai_amd.modelo import inicial
     V, D, H, FF, L, T, bt = (c[k] for k in ("V", "D", "H", "FF", "L", "T", "Bt"))
     HD = D // H
     g = torch.Generator().manual_seed(0)
-    deq = lambda t: (t[0].float() * torch.pow(2.0, t[1][:, :1].float())).contiguous().requires_grad_()
+    deq = lambda t: (t[0].float() * torch.pow(2.0, t[1][:, :1].float())).to(dev).contiguous().requires_grad_()
     w = {"emb": deq(inicial(g, V, D, "cpu", emb=True))}
     for l in range(L):
         for n in ("Wq", "Wk", "Wv", "Wo"):
@@ -396,10 +613,10 @@ def cpu_baseline_fp32(c, segundos):
         w[f"Wup{l}"] = deq(inicial(g, FF, D, "cpu"))
         w[f"Wd{l}"] = deq(inicial(g, D, FF, "cpu"))
     w["out"] = deq(inicial(g, V, D, "cpu"))
-    pos = torch.arange(T)
+    pos = torch.arange(T, device=dev)
     dist = pos[:, None] - pos[None, :]
     mascara = dist < 0
-    inclinacao = torch.pow(2.0, -((8 * torch.arange(H)) // H).float())
+    inclinacao = torch.pow(2.0, -((8 * torch.arange(H, device=dev)) // H).float())
     vies = -(dist.clamp(min=0)[None].float() * inclinacao[:, None, None])
     escala = HD ** -0.5
 
@@ -410,7 +627,7 @@ def cpu_baseline_fp32(c, segundos):
         for l in range(L):
             xn = rms(x)
             q, k, v = (cab(xn @ w[f"{n}{l}"].t()) for n in ("Wq", "Wk", "Wv"))
-            z = (q @ k.transpose(-1, -2)) * escala + vies
+            z = (q @ k.transpose(-1, -2).contiguous()) * escala + vies
             a = torch.softmax(z.masked_fill(mascara, float("-inf")), -1)
             x = x + (a @ v).transpose(1, 2).reshape(bt, T, D) @ w[f"Wo{l}"].t()
             xn = rms(x)
@@ -421,51 +638,75 @@ def cpu_baseline_fp32(c, segundos):
     opt = torch.optim.SGD(list(w.values()), lr=2.0 ** -4, momentum=0.875)
     gen = torch.Generator().manual_seed(11)
 
-    def passo():
-        x = torch.randint(0, V, (bt, T + 1), generator=gen)
+    def passo(i):
+        x = torch.randint(0, V, (bt, T + 1), generator=gen).to(dev)
         p = perda(x[:, :-1], x[:, 1:])
         opt.zero_grad()
         p.backward()
         opt.step()
-        return float(p.detach())
-    passo()
+        return p.detach()
+
+    def sinc():
+        if dev != "cpu":
+            torch.cuda.synchronize()
+    passo(0)
+    sinc()
     n, t0 = 0, time.perf_counter()
     while True:
-        ultima = passo()
+        ultima = passo(n)
         n += 1
+        sinc()
         dt = time.perf_counter() - t0
-        if dt >= segundos and n >= 2:
+        if dt >= segundos and n >= passos_min:
             break
-    threads = torch.get_num_threads()
-    return dict(value=n * bt * T / dt, unit="tokens/s", cores=threads, kind="port",
-                sample=f"{n} float32 training steps (forward, backward, SGD) of the same {L}-layer model at "
-                       f"Bt={bt} x T={T} after one warm-up, PyTorch {torch.__version__} on {threads} threads of "
-                       f"{cpu_modelo()}, {dt:.1f} s; last loss {ultima:.4f}")
+    ultima = float(ultima)
+    if dev == "cpu":
+        threads = torch.get_num_threads()
+        return dict(value=n * bt * T / dt, unit="tokens/s", cores=threads, kind="port",
+                    sample=f"{n} float32 training steps (forward, backward, SGD) of the same {L}-layer model at "
+                           f"Bt={bt} x T={T} after one warm-up, PyTorch {torch.__version__} on {threads} threads of "
+                           f"{cpu_modelo()}, {dt:.1f} s; last loss {ultima:.4f}")
+    return dict(value=n * bt * T / dt, unit="tokens/s", steps=n, seconds=round(dt, 3), last_loss=ultima,
+                what=f"PyTorch {torch.__version__} float32 on the GPU (rocBLAS/hipBLASLt GEMMs, eager launches)")
 
 
-def mede_passo(ops, reg, c, steps, warmup):
-    """Tokens/s of the training step of workload c replayed from one hipGraph: W untimed replays, then K timed
-    ones bracketed by device synchronizations (batches resident on the device). Returns (tokens/s, seconds of the
-    timed replays, last loss, graph launches)."""
+def mede_passo(ops, reg, c, steps, warmup, grafo=True):
+    """Tokens/s of the training step of workload c, following the reference's protocol
+    (jatai_cuda/treino_cuda.py:119-151, bench_grafo.py:29-37): per step, copy the batch into the step's input
+    buffers, clear the device error record, run the step, read the record. grafo=True replays the step captured
+    once as a hipGraph (PassoGravado); grafo=False launches it op by op from Python (the reference's "normal
+    launches"). W untimed steps, then K timed ones bracketed by device synchronizations; every step gets its own
+    batch of uniform random ids, all resident in HBM before the clock starts. Returns (tokens/s, seconds of the
+    timed steps, last loss, launches per step)."""
     import torch
     from jatai_amd.modelo import Modelo, PassoGravado
     dev = "cuda"
     m = Modelo(c["V"], c["D"], c["H"], c["FF"], c["L"], 0, dev, ops, reg, r16=c["r16"])
     g = torch.Generator().manual_seed(1)
-    nlotes = 6
     lotes = []
-    for _ in range(nlotes):
+    for _ in range(warmup + steps + 1):
         x = torch.randint(0, c["V"], (c["Bt"], c["T"] + 1), generator=g).to(dev)
         lotes.append((x[:, :-1].contiguous(), x[:, 1:].contiguous()))
     reg.novo_passo(0)
-    m.passo(*lotes[0], k_lr=4)
+    m.passo(*lotes[-1], k_lr=4)
     reg.fim_passo()
-    pg = PassoGravado(m, c["Bt"], c["T"], 4)
-    nlanc = len(pg.lancamentos)
+    if grafo:
+        pg = PassoGravado(m, c["Bt"], c["T"], 4)
+        nlanc = len(pg.lancamentos)
+        executa = lambda tok, alvo: pg(tok, alvo)
+    else:
+        nlanc = len(reg.lancamentos)
+        tok_b = torch.zeros(c["Bt"], c["T"], dtype=torch.int32, device=dev)
+        alvo_b = torch.zeros_like(tok_b)
+
+        def executa(tok, alvo):
+            tok_b.copy_(tok)
+            alvo_b.copy_(alvo)
+            return m.passo(tok_b, alvo_b, k_lr=4)
 
     def passo(i):
         reg.novo_passo(i)
-        perda = pg(*lotes[i % nlotes])
+        perda = executa(*lotes[i])
         reg.fim_passo()
         return perda
     for i in range(warmup):
@@ -473,7 +714,7 @@ def mede_passo(ops, reg, c, steps, warmup):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        perda = passo(i)
+        perda = passo(warmup + i)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return c["Bt"] * c["T"] * steps / dt, dt, float(perda), nlanc
@@ -505,32 +746,84 @@ def main():
         print(json.dumps({"metric": METRIC, "value": tps, "unit": "tokens/s", "ms_per_step": dt / a.steps * 1e3,
                           "steps": a.steps, "warmup": a.warmup, "graph_launches": nlanc, "config": c["nome"]}), flush=True)
         return
+    ms_passo = dt / a.steps * 1e3
     gem = mede_gemms(O, ops, c)
     tot_gemm_ms = sum(v["ms"] * v["por_passo"] for v in gem.values())
-    dom_nome, dom = max(gem.items(), key=lambda kv: kv[1]["ms"] * kv[1]["por_passo"])
-    achieved = 2 * dom["M"] * dom["N"] * dom["K"] / (dom["ms"] * 1e-3)
+    print("bench: grouped weight-gradient GEMMs, optimizer, transposes", file=sys.stderr, flush=True)
+    dw = mede_dw_lote(O, ops, c)
+    ms_dw_passo, amostras_passo = mede_dw_no_passo(ops, reg, c)
+    # the step's own launch, timed between the replays of the step split around it, is the figure the table and
+    # the roofline use; the standalone launch is reported beside it
+    dw["ms_standalone"], dw["ms_each_standalone"] = dw["ms"], dw["ms_each"]
+    dw["ms"], dw["ms_each"] = ms_dw_passo, amostras_passo
+    ot = mede_otimizador_e_transpostas(O, ops, c)
+    ops2 = mede_ops(O, ops, c, reg)
+    tabela = tabela_kernels(c, gem, dw, ops2, ot, ms_passo)
+    lim = 2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS
+    # the roofline line is the single kernel with the most time per step (the attention rows are four-launch
+    # sequences); at configs 4 and 5 that is the grouped weight-gradient launch (k_gemm_lote), whose algorithmic
+    # work is 2 M N K summed over its GEMMs
+    dom = next(e for e in tabela if "TOPS" in e)
+    if dom["kernel"].startswith("k_gemm_lote"):
+        achieved = dw["ops"] / (dw["ms"] * 1e-3)
+        kern = (f"{dw['symbol']} (all {dw['gemms']} weight-gradient GEMMs of a step in one launch, K={dw['K']} tokens, "
+                f"{dw['ops'] / 1e9:.1f} GOP, {dw['workgroups']} workgroups x {dw['threads']} threads)")
+        avg_ms, traf = dw["ms"], trafego("dW grouped")
+        amostras = {"in_step": dw["ms_each"], "standalone": dw["ms_each_standalone"],
+                    "timing": "median of in-step launches: the step captured as three graphs split around this launch, "
+                              "HIP events on the replay stream between them"}
+    else:
+        nome = dom["name"].replace("gemm ", "")
+        v = gem[nome]
+        achieved = 2 * v["M"] * v["N"] * v["K"] / (v["ms"] * 1e-3)
+        kern = (f"{v['kernel']['symbol']} ({nome} M={v['M']} N={v['N']} K={v['K']}, {v['kernel']['workgroups']} workgroups x "
+                f"{v['kernel']['threads']} threads)")
+        avg_ms, traf = v["ms"], trafego(nome)
+        amostras = None
     roof = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_I8 / 1e12, "unit": "TOP/s",
-            "frac": achieved / PEAK_I8, "traffic": trafego(dom_nome),
-            "kernel": f"{dom['kernel']['symbol']} ({dom_nome} M={dom['M']} N={dom['N']} K={dom['K']}, "
-                      f"{dom['kernel']['workgroups']} workgroups x {dom['kernel']['threads']} threads)",
-            "avg_ms": dom["ms"],
-            "format_bound": {"bound": "valu", "peak": 2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS / 1e12, "unit": "TOP/s",
-                             "frac": achieved / (2 * c["BLK"] / VALU_POR_BLOCO * VALU_LANE_OPS),
+            "frac": achieved / PEAK_I8, "traffic": traf, "kernel": kern, "avg_ms": avg_ms, "launch_ms_samples": amostras,
+            "format_bound": {"bound": "valu", "peak": lim / 1e12, "unit": "TOP/s", "frac": achieved / lim,
                              "valu_lane_ops_per_output_block": VALU_POR_BLOCO, "valu_lane_ops_per_s": VALU_LANE_OPS}}
     res = {"metric": METRIC, "value": tps, "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-           "ms_per_step": dt / a.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+           "ms_per_step": ms_passo, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": tps / c["publicado"] if c.get("publicado") else None, "dtype": "int8",
-           "data": "synthetic: uniform random token ids, random-init weights (modelo.py init, seed 0)",
+           "data": "synthetic: uniform random token ids (a fresh batch per step), random-init weights (modelo.py init, seed 0)",
            "config": {"workload": c["nome"], "layers": c["L"], "d_model": c["D"], "heads": c["H"], "ffn": c["FF"],
                       "vocab": c["V"], "seq_len": c["T"], "batch": c["Bt"], "tokens_per_step": tokens, "block": c["BLK"],
                       "graph_launches": nlanc, "parallelism": "single GPU"},
            "loss_last_step": perda,
            "roofline": roof,
+           "step_kernels_top6": tabela[:6],
            "gemm_shapes": {k: {"M": v["M"], "N": v["N"], "K": v["K"], "mode": v["modo"], "ms": round(v["ms"], 5),
                                "TOPS": round(v["tops"], 2), "pct_i8_peak": round(100 * v["tops"] * 1e12 / PEAK_I8, 2),
                                "per_step": v["por_passo"], "kernel": v["kernel"]} for k, v in gem.items()},
            "gemm_ms_per_step_eager_sum": tot_gemm_ms,
-           "ops_config2": mede_ops(O, ops, c, reg)}
+           "ops_config2": ops2}
+    if a.config != "r":
+        # the reference's only published throughput is at its own shape (12L, D 256, 64 heads x 4, BLK 128, Bt 16 x
+        # T 128 = 2048 tokens: 34,248 tokens/s with CUDA Graph, 32,714 with normal launches, 8,926 in fp32 PyTorch;
+        # GTX 1650, README.md:83-87): the same three measurements here
+        cr = CONFIGS["r"]
+        print(f"bench: {cr['nome']}", file=sys.stderr, flush=True)
+        O.BLK = cr["BLK"]
+        tg, dtg, _, ng = mede_passo(ops, reg, cr, 30, 3)
+        te, dte, _, ne = mede_passo(ops, reg, cr, 10, 2, grafo=False)
+        f32 = mede_fp32(cr, 3.0, dev="cuda", passos_min=10)
+        O.BLK = c["BLK"]
+        res["reference_native"] = {
+            "workload": cr["nome"], "tokens_per_step": cr["Bt"] * cr["T"],
+            "graph": {"value": tg, "unit": "tokens/s", "ms_per_step": dtg / 30 * 1e3, "steps": 30, "launches": ng,
+                      "vs_published": tg / cr["publicado"]},
+            "eager": {"value": te, "unit": "tokens/s", "ms_per_step": dte / 10 * 1e3, "steps": 10, "launches": ne,
+                      "vs_published": te / 32714.0},
+            "fp32_gpu": f32, "graph_vs_fp32_gpu": tg / f32["value"],
+            "published": {"graph": cr["publicado"], "eager": 32714.0, "fp32": 8926.0, "hardware": "GTX 1650",
+                          "source": "README.md:83-87"}}
+    else:
+        te, dte, _, ne = mede_passo(ops, reg, c, 10, 2, grafo=False)
+        f32 = mede_fp32(c, 3.0, dev="cuda", passos_min=10)
+        res["eager"] = {"value": te, "unit": "tokens/s", "ms_per_step": dte / 10 * 1e3, "launches": ne, "vs_published": te / 32714.0}
+        res["fp32_gpu"] = f32
     if a.config == "b4" and not a.sem_c5:
         # BASELINE config 5 beside it: the 24-layer, 16384-token step with the 16-bit residual stream
         c5 = CONFIGS["c5"]
@@ -541,7 +834,7 @@ def main():
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, a.cpu_seconds)
         res["speedup_vs_cpu_baseline"] = tps / res["cpu_baseline"]["value"]
-        res["cpu_baseline_fp32"] = cpu_baseline_fp32(c, a.cpu_seconds)
+        res["cpu_baseline_fp32"] = mede_fp32(c, a.cpu_seconds)
         res["speedup_vs_cpu_fp32"] = tps / res["cpu_baseline_fp32"]["value"]
     print(json.dumps(res), flush=True)
 

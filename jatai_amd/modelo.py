@@ -80,6 +80,10 @@ class Modelo:
         self.rms_soma = hasattr(ops, "rms_back_soma")
         # the loss in one launch of the library (float64 sums in another order than torch's mean: equal to 1e-15)
         self.perda_fundida = hasattr(ops, "perda")
+        # measurement hook: stage name -> (before, after) callables run around that stage of the step
+        # ("gradientes dos pesos": the grouped weight-gradient launch), e.g. to split a capture into three graphs
+        # so the stage can be timed between replays as the step runs it
+        self.marcas = {}
         self._gbuf, self._tabela = None, None
 
     def _otim_no_gemm(self):
@@ -225,8 +229,13 @@ class Modelo:
             return perda
         if adiados:
             with reg.trecho("gradientes dos pesos"):
+                marca = self.marcas.get("gradientes dos pesos")
+                if marca:
+                    marca[0]()
                 for (n, _, _), G in zip(adiados, ops.gemm_cru_lote([(A, B, gb[n] if gb else None) for n, A, B in adiados])):
                     grads[n] = G
+                if marca:
+                    marca[1]()
         with reg.trecho("otimizador"):
             if self.otimizador_fundido:
                 ops.otimizador(self._tabela, k_lr, self.error_feedback)
