@@ -127,7 +127,9 @@ def gemm_formas(c):
 def gemm_kernel(O, ops, M, N, K, modo):
     """Symbol and grid the library launches for this shape, to match rocprof rows."""
     ks = ops.lib.jt_gemm_divisoes(M, N, K, modo)
-    return {"symbol": f"k_gemm<{O.BLK}, {modo}, {ks}>", "workgroups": (M // 32) * (N // 128), "threads": 256 * ks}
+    bm = ops.lib.jt_gemm_tile(M, N, modo)
+    return {"symbol": f"k_gemm<{O.BLK}, {modo}, {ks}, {bm // 32}>", "workgroups": (M // bm) * (N // 128),
+            "threads": 256 * (bm // 32) * ks, "tile_rows": bm}
 
 
 def mede_gemms(O, ops, c, rep=20):
@@ -219,7 +221,7 @@ def mede_dw_lote(O, ops, c, rep=7):
     while nk < 4 and tiles * 2 * nk <= 1024 and (K // blk) >= 8 * nk:
         nk *= 2
     return dict(ms=ms, ms_each=[round(x, 4) for x in vezes], ops=ops_alg, gemms=len(formas), K=K, launches=(len(formas) + lote - 1) // lote,
-                symbol=f"k_gemm_lote<{blk}, {nk}>", workgroups=tiles, threads=256 * nk)
+                symbol=f"k_gemm_lote<{blk}, {nk}, 1>", workgroups=tiles, threads=256 * nk)
 
 
 def mede_dw_no_passo(ops, reg, c, rep=10):
@@ -533,7 +535,7 @@ def trafego_despacha(O, ops, c):
     for _ in range(2):
         ops.gemm_cru_lote(pares)
         torch.cuda.synchronize()
-    print(f"dispatch: dW grouped k_gemm_lote<{blk}, 1> x2", flush=True)
+    print(f"dispatch: dW grouped k_gemm_lote<{blk}, 1, 1> x2", flush=True)
 
 
 def trafego(nome):

@@ -26,8 +26,10 @@ void jt_stream(void* stream);          /* every later launch goes to this hipStr
 
 /* ---- tuning knobs (jatai_cuda.cu:1087-1091) */
 void jt_gemm_split(int alvo_wg);       /* split-K target workgroup count for raw GEMM outputs */
-void jt_gemm_bm(int bm);               /* accepted; the MFMA GEMM has a single tile shape */
-void jt_atencao_linhas(int n);         /* accepted; attention runs one query row per thread */
+void jt_gemm_bm(int bm);               /* jatai_cuda.cu:1090: GEMM tile rows: 0 automatic (32), 64 or 128 forced (32 forces the
+                                        * default); a forced tile that does not divide M falls back to one that does; same bits */
+void jt_atencao_linhas(int n);         /* jatai_cuda.cu:1091: query rows per thread of the head-width-4 attention: 1 (default)
+                                        * or 2 (rows i and T - 1 - i); same bits */
 int jt_res_estocastico(int ligado);    /* jatai_cuda.cu:1087: 1 = gemm_soma's residual add rounds stochastically (0 = off, the default) */
 
 /* ---- no reference counterpart: attention kernel family at head width 64, matrix cores (1, default) or dot2 (0) */
@@ -45,7 +47,9 @@ int jt_bloco_atual(void);
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
               const void* Xm, const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid);
 int jt_gemm_divisoes(int M, int N, int K, int modo);   /* no reference counterpart: K-splits jt_gemm_f uses
-                                                        * for a shape (workgroup = 256 x splits threads) */
+                                                        * for a shape (workgroup = 256 x tile rows / 32 x splits threads) */
+int jt_gemm_tile(int M, int N, int modo);              /* no reference counterpart: tile rows (32, 64, 128) jt_gemm_f
+                                                        * uses for a shape and mode */
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
             int M, int N, int K, int modo, int kid);
 

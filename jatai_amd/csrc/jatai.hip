@@ -38,7 +38,8 @@ __global__ void k_erro_limpa() {
 static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
 static int g_alvo_wg = 1024;            // GEMM K-split target: tiles x K-splits per launch
-static int g_gemm_bm = 0, g_linhas = 1; // accepted for interface parity (see jt_gemm_bm / jt_atencao_linhas)
+static int g_gemm_bm = 0;               // GEMM tile rows: 0 = automatic, or 32, 64, 128 forced (jt_gemm_bm)
+static int g_linhas = 1;                // attention query rows per thread at head width 4: 1 or 2 (jt_atencao_linhas)
 static int g_atencao_mfma = 1;          // head width 64: matrix-core attention (1) or the dot2 kernels (0)
 
 static int fim() { return (int)hipGetLastError(); }
@@ -80,13 +81,26 @@ static void lds_max(K* k, size_t lds) {
 // number of K-blocks must be a multiple of 16
 static bool k_ok(int K) { return K <= 4096 || (K <= 65536 && (K / g_blk) % 16 == 0); }
 
-static int gemm_divisoes(int M, int N, int K, int modo) {
-    const long long tiles = (long long)(M / gemm::BM) * (N / gemm::BN);
-    const int nb = K / g_blk, ksmax = (g_blk == 32 && modo < 2) ? 4 : 2;
+// Tile of 32 R rows. Forced by jt_gemm_bm: 64 (R = 2) or 128 (R = 4), falling back to the tallest tile that
+// divides M (every M here is a multiple of 32). Automatic: R = 1, except the fused ReLU^2 GEMMs (modes 3 and 4)
+// when 128-row tiles make one or two workgroups per CU -- measured on MI355X at M = N = 2048, K = 512 (config 4):
+// 20.4 / 19.7 us against 21.5 / 21.2 at 32 rows; with many more tiles (config 5, M = 16384) and at every other
+// step shape 32 rows are fastest.
+static int gemm_r(int M, int N = 0, int modo = 0) {
+    int r = g_gemm_bm >= 128 ? 4 : g_gemm_bm >= 64 ? 2 : 1;
+    const long long t128 = (long long)(M / 128) * (N / 128);
+    if (g_gemm_bm == 0 && (modo == 3 || modo == 4) && t128 >= 256 && t128 <= 512) r = 4;
+    while (r > 1 && M % (32 * r)) r /= 2;
+    return r;
+}
+static int gemm_divisoes_r(int M, int N, int K, int modo, int r) {
+    const long long tiles = (long long)(M / (32 * r)) * (N / gemm::BN);
+    const int nb = K / g_blk, ksmax = std::min((g_blk == 32 && modo < 2) ? 4 : 2, 4 / r);   // 256 R KS <= 1024 threads
     int ks = 1;
     while (ks < ksmax && tiles * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
     return ks;
 }
+static int gemm_divisoes(int M, int N, int K, int modo) { return gemm_divisoes_r(M, N, K, modo, gemm_r(M, N, modo)); }
 
 extern "C" {
 
@@ -109,8 +123,11 @@ int jt_erro_limpa() {
 int jt_sincroniza() { return (int)hipDeviceSynchronize(); }
 void jt_stream(void* st) { g_stream = (hipStream_t)st; }
 void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 1024; }
-void jt_gemm_bm(int bm) { g_gemm_bm = bm; }       // the MFMA kernel has one tile shape; kept for the interface
-void jt_atencao_linhas(int n) { g_linhas = n; }   // one query row per thread; kept for the interface
+// jatai_cuda.cu:1090: GEMM tile rows, 0 automatic (32), or 64 / 128 forced (32 forces the default); same bits.
+void jt_gemm_bm(int bm) { g_gemm_bm = bm; }
+// jatai_cuda.cu:1091: query rows per thread of the head-width-4 attention, 1 (default) or 2 (rows i and T - 1 - i,
+// which balances the causal work); same bits.
+void jt_atencao_linhas(int n) { g_linhas = n == 2 ? 2 : 1; }
 // No reference counterpart: selects the matrix-core (1, default) or dot2 (0) attention kernels at head width 64.
 void jt_atencao_mfma(int ligado) { g_atencao_mfma = ligado ? 1 : 0; }
 // jatai_cuda.cu:1087: stochastic rounding of gemm_soma's residual add. A synchronous copy into the device global
@@ -130,24 +147,27 @@ int jt_bloco_atual() { return g_blk; }
 // ---------------------------------------------------------------------------------------------- GEMM
 // No reference counterpart: the K-split count jt_gemm_f uses for a shape (workgroup = 256 x splits threads).
 int jt_gemm_divisoes(int M, int N, int K, int modo) { return gemm_divisoes(M, N, K, modo); }
+// No reference counterpart: the tile rows (32, 64 or 128) jt_gemm_f uses for a shape and mode.
+int jt_gemm_tile(int M, int N, int modo) { return 32 * gemm_r(M, N, modo); }
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
               const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
     using namespace gemm;
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || !k_ok(K) || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
-    const int nb = K / g_blk;
+    const int nb = K / g_blk, r = gemm_r(M, N, modo);
     // mode 4 with Om2: the transposed copy needs a single K-split (BLK = 32 only)
     if (modo == 4 && (Om2 || OE2) && (g_blk != 32 || !Om2 || !OE2)) return (int)hipErrorInvalidValue;
-    const int ks = (modo == 4 && Om2) ? 1 : gemm_divisoes(M, N, K, modo);
-    const dim3 grade(N / BN, M / BM);
-    const size_t lds = gemm_lds(nb, ks, g_blk);
+    const int ks = (modo == 4 && Om2) ? 1 : gemm_divisoes_r(M, N, K, modo, r);
+    const dim3 grade(N / BN, M / (32 * r));
+    const size_t lds = gemm_lds(nb, ks, g_blk, r);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \
              (const int8_t*)Xm, (const int8_t*)XE, (int8_t*)Om2, (int8_t*)OE2, M, N, K, kid
-#define L(BL, MD, S) (lds_max(k_gemm<BL, MD, S>, lds), k_gemm<BL, MD, S><<<grade, 256 * S, lds, g_stream>>>(ARGS))
-#define LS2(BL, MD) (ks == 1 ? L(BL, MD, 1) : L(BL, MD, 2))
-#define LS4(BL, MD) (ks == 1 ? L(BL, MD, 1) : ks == 2 ? L(BL, MD, 2) : L(BL, MD, 4))
-#define LB2(MD) (g_blk == 32 ? LS2(32, MD) : LS2(128, MD))
-#define LB4(MD) (g_blk == 32 ? LS4(32, MD) : LS2(128, MD))
+#define L(BL, MD, S, RR) (lds_max(k_gemm<BL, MD, S, RR>, lds), k_gemm<BL, MD, S, RR><<<grade, 256 * RR * S, lds, g_stream>>>(ARGS))
+#define LS2(BL, MD, RR) (ks == 1 ? L(BL, MD, 1, RR) : L(BL, MD, 2, RR))
+#define LS4(BL, MD) (ks == 1 ? L(BL, MD, 1, 1) : ks == 2 ? L(BL, MD, 2, 1) : L(BL, MD, 4, 1))
+#define LR(BL, MD, LS1) (r == 1 ? LS1 : r == 2 ? LS2(BL, MD, 2) : L(BL, MD, 1, 4))
+#define LB2(MD) (g_blk == 32 ? LR(32, MD, LS2(32, MD, 1)) : LR(128, MD, LS2(128, MD, 1)))
+#define LB4(MD) (g_blk == 32 ? LR(32, MD, LS4(32, MD)) : LR(128, MD, LS2(128, MD, 1)))
     switch (modo) {
         case 0: LB4(0); break;
         case 1: LB4(1); break;
@@ -157,6 +177,7 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
     }
 #undef LB2
 #undef LB4
+#undef LR
 #undef LS2
 #undef LS4
 #undef L
@@ -179,6 +200,8 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
         LoteG L;
         L.n = std::min(LOTE_G, n - base);
         L.K = e[base].K;
+        int r = 4;                                                   // the tallest forced tile every M of the group allows
+        for (int i = 0; i < L.n; i++) r = std::min(r, gemm_r(e[base + i].M > 0 ? e[base + i].M : 32));
         long long tot = 0;
         for (int i = 0; i < L.n; i++) {
             const EntradaG& x = e[base + i];
@@ -186,22 +209,24 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
             if (!alinhados(x.A, x.EA, x.B, x.EB, x.C32, x.Ce)) return (int)hipErrorInvalidValue;
             L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
             L.C32[i] = (int*)x.C32; L.Ce[i] = (int16_t*)x.Ce; L.M[i] = x.M; L.N[i] = x.N; L.ini[i] = (int)tot;
-            tot += (long long)(x.M / BM) * (x.N / BN);
+            tot += (long long)(x.M / (32 * r)) * (x.N / BN);
         }
         if (tot > 0x7fffffff) return (int)hipErrorInvalidValue;
         L.ini[L.n] = (int)tot;
         if (tot == 0) continue;
         // K-splits for the whole group, by the rule of jt_gemm_f with the group's tile count
-        const int nb = L.K / g_blk, ksmax = g_blk == 32 ? 4 : 2;
+        const int nb = L.K / g_blk, ksmax = std::min(g_blk == 32 ? 4 : 2, 4 / r);
         int ks = 1;
         while (ks < ksmax && tot * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
-        const size_t lds = gemm_lds(nb, ks, g_blk);
-#define L_(BL, S) (lds_max(k_gemm_lote<BL, S>, lds), k_gemm_lote<BL, S><<<(unsigned)tot, 256 * S, lds, g_stream>>>(L, kid + base))
-        if (g_blk == 32) { if (ks == 1) L_(32, 1); else if (ks == 2) L_(32, 2); else L_(32, 4); }
-        else { if (ks == 1) L_(128, 1); else L_(128, 2); }
+        const size_t lds = gemm_lds(nb, ks, g_blk, r);
+#define L_(BL, S, RR) (lds_max(k_gemm_lote<BL, S, RR>, lds), k_gemm_lote<BL, S, RR><<<(unsigned)tot, 256 * RR * S, lds, g_stream>>>(L, kid + base))
+        if (r == 4) { if (g_blk == 32) L_(32, 1, 4); else L_(128, 1, 4); }
+        else if (r == 2) { if (g_blk == 32) { if (ks == 1) L_(32, 1, 2); else L_(32, 2, 2); } else { if (ks == 1) L_(128, 1, 2); else L_(128, 2, 2); } }
+        else if (g_blk == 32) { if (ks == 1) L_(32, 1, 1); else if (ks == 2) L_(32, 2, 1); else L_(32, 4, 1); }
+        else { if (ks == 1) L_(128, 1, 1); else L_(128, 2, 1); }
 #undef L_
-        const int r = fim();
-        if (r) return r;
+        const int rc = fim();
+        if (rc) return rc;
     }
     return 0;
 }
@@ -505,11 +530,12 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd == 4) {
-        const int nt = (T + 63) & ~63;                   // whole waves; threads past T only join the reductions
-        if (T <= 128)
-            k_atencao4<128><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
-        else
-            k_atencao4<256><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P, T, H, D, g_blk, GA, kid);
+        const int nt = (T / g_linhas + 63) & ~63;        // whole waves; threads without a row only join the reductions
+#define A4(TM, NR) k_atencao4<TM, NR><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, \
+                                                                    (uint8_t*)P, T, H, D, g_blk, GA, kid)
+        if (T <= 128) { if (g_linhas == 2) A4(128, 2); else A4(128, 1); }
+        else { if (g_linhas == 2) A4(256, 2); else A4(256, 1); }
+#undef A4
         return fim();
     }
     if ((hd != 16 && hd != 32 && hd != 64) || hd % g_blk && g_blk % hd) return (int)hipErrorInvalidValue;
@@ -574,15 +600,13 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     const int hd = D / H;
     const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);
     if (hd == 4) {
-        const int nt = (T + 63) & ~63;
+        const int nt = (T / g_linhas + 63) & ~63;
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
-        if (T <= 128) {
-            if (limite) k_atencao4_back<128, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS);
-            else k_atencao4_back<128, 0><<<Bt * H, nt, 0, g_stream>>>(ARGS);
-        } else {
-            if (limite) k_atencao4_back<256, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS);
-            else k_atencao4_back<256, 0><<<Bt * H, nt, 0, g_stream>>>(ARGS);
-        }
+#define B4(TM, LM) { if (g_linhas == 2) k_atencao4_back<TM, LM, 2><<<Bt * H, nt, 0, g_stream>>>(ARGS); \
+                     else k_atencao4_back<TM, LM, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS); }
+        if (T <= 128) { if (limite) B4(128, 1) else B4(128, 0) }
+        else { if (limite) B4(256, 1) else B4(256, 0) }
+#undef B4
 #undef ARGS
         return fim();
     }

@@ -1,6 +1,7 @@
 // Causal ALiBi attention at head width 4 (the spec's shape, ops.py:186-258): one workgroup per
-// (sequence, head), one thread per query row i. T is a multiple of 32 up to 256; the workgroup has T rounded up
-// to whole waves of 64 threads, and the threads past T take part in the reductions with neutral values only.
+// (sequence, head), one or two query rows per thread. T is a multiple of 32 up to 256; the workgroup has T / NR
+// threads rounded up to whole waves of 64, and the threads without a row take part in the reductions with
+// neutral values only.
 //
 // Forward: q, k, v of the head aligned to the head's largest exponent over the sequence with GA guard bits
 // (a = rnd(m << GA, emx - e)); u_ij = rnd(q_i . k_j, -(eq + ek - 1 + 8)) - (i - j) << incl with
@@ -21,21 +22,39 @@ __device__ __forceinline__ int bloco_max(int v, int* red) {
     return r;
 }
 
-// aligned values of this thread's token for one head slice of 4 columns (jatai_cuda.cu:789-818 restated);
-// a thread past the sequence (t >= T) loads nothing and holds zeros
+// Rows per thread (jt_atencao_linhas, jatai_cuda.cu:1091): with NR = 1 thread t owns query row t; with NR = 2 it
+// owns rows t and T - 1 - t (t < T / 2), a short and a long causal row, so the threads' work is even. The backward
+// assigns its columns (keys) the same way. -1: no row (a thread past the sequence).
+template <int NR>
+__device__ __forceinline__ int linha_de(int t, int k, int T) {
+    if constexpr (NR == 1) return t < T ? t : -1;
+    else return t < T / 2 ? (k == 0 ? t : T - 1 - t) : -1;
+}
+
+// aligned values of the thread's tokens for one head slice of 4 columns (jatai_cuda.cu:789-818 restated):
+// al[t][d] = rnd(m << GA, emx - e) with emx the head's largest exponent over the sequence; eo = emx - GA
+template <int NR>
 __device__ __forceinline__ void alinha4(const int8_t* m, const int8_t* E, int ld, int col, int blk, int b0, int T, int GA, int* red,
                                         int (*al)[4], int& eo) {
-    const int t = threadIdx.x;
-    const bool ativo = t < T;
-    const int e = ativo ? (int)E[(size_t)(b0 + t) * (ld / blk) + col / blk] : SEM_TOPO;
-    const int emx = bloco_max(e, red);
-    const int w = ativo ? *reinterpret_cast<const int*>(m + (size_t)(b0 + t) * ld + col) : 0;
+    int e[NR], w[NR], tk[NR], emx = SEM_TOPO;
 #pragma unroll
-    for (int d = 0; d < 4; d++) al[t][d] = ativo ? rnd_d(((w << (24 - 8 * d)) >> 24) << GA, emx - e) : 0;
+    for (int k = 0; k < NR; k++) {
+        tk[k] = linha_de<NR>(threadIdx.x, k, T);
+        e[k] = tk[k] >= 0 ? (int)E[(size_t)(b0 + tk[k]) * (ld / blk) + col / blk] : SEM_TOPO;
+        w[k] = tk[k] >= 0 ? *reinterpret_cast<const int*>(m + (size_t)(b0 + tk[k]) * ld + col) : 0;
+        emx = max(emx, e[k]);
+    }
+    emx = bloco_max(emx, red);
+#pragma unroll
+    for (int k = 0; k < NR; k++)
+        if (tk[k] >= 0) {
+#pragma unroll
+            for (int d = 0; d < 4; d++) al[tk[k]][d] = rnd_d(((w[k] << (24 - 8 * d)) >> 24) << GA, emx - e[k]);
+        }
     eo = emx - GA;
 }
 
-template <int TMAX>
+template <int TMAX, int NR>
 __global__ void __launch_bounds__(TMAX) k_atencao4(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, int* __restrict__ Oacc,
                                                    int16_t* __restrict__ Oe, uint8_t* __restrict__ P, int T, int H, int D, int blk, int GA,
                                                    int kid) {
@@ -43,47 +62,50 @@ __global__ void __launch_bounds__(TMAX) k_atencao4(const int8_t* __restrict__ qm
     __shared__ int red[TMAX / 64];
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     int eq, ek, ev;
-    alinha4(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
-    alinha4(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
-    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
+    alinha4<NR>(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
+    alinha4<NR>(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
+    alinha4<NR>(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
     __syncthreads();
     const int su = -(eq + ek - 1 + 8), incl = 8 - h / 8;
-    const int i = threadIdx.x, row = b0 + i;
-    if (i >= T) return;                                             // no barrier follows
-    const int q0 = qa[i][0], q1 = qa[i][1], q2 = qa[i][2], q3 = qa[i][3];
-    const long long idx = (long long)row * D + h * 4;
-    auto sc = [&](int j) {
-        const int s = q0 * ka[j][0] + q1 * ka[j][1] + q2 * ka[j][2] + q3 * ka[j][3];
-        return rnd(s, su, kid, idx) - ((i - j) << incl);
-    };
-    int mx = U_MIN;
-    for (int j = 0; j <= i; j++) mx = max(mx, sc(j));
-    int soma = 0;
-    for (int j = 0; j <= i; j++) soma += exp_dif(mx, sc(j)) >> 3;
-    if (soma <= 0) { reporta(E_DIV, kid, idx, soma, mx); soma = 1; }
-    const int inv = (1 << 28) / soma;
-    int o[4] = {0, 0, 0, 0};
     uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
-    for (int j = 0; j < T; j++) {
-        int p = 0;
-        if (j <= i) {
-            const int ex = exp_dif(mx, sc(j)) >> 3;
-            p = min((ex * inv + (1 << 19)) >> 20, 255);
+#pragma unroll 1
+    for (int k = 0; k < NR; k++) {                                  // no barrier below: threads without a row leave
+        const int i = linha_de<NR>(threadIdx.x, k, T), row = b0 + i;
+        if (i < 0) continue;
+        const int q0 = qa[i][0], q1 = qa[i][1], q2 = qa[i][2], q3 = qa[i][3];
+        const long long idx = (long long)row * D + h * 4;
+        auto sc = [&](int j) {
+            const int s = q0 * ka[j][0] + q1 * ka[j][1] + q2 * ka[j][2] + q3 * ka[j][3];
+            return rnd(s, su, kid, idx) - ((i - j) << incl);
+        };
+        int mx = U_MIN;
+        for (int j = 0; j <= i; j++) mx = max(mx, sc(j));
+        int soma = 0;
+        for (int j = 0; j <= i; j++) soma += exp_dif(mx, sc(j)) >> 3;
+        if (soma <= 0) { reporta(E_DIV, kid, idx, soma, mx); soma = 1; }
+        const int inv = (1 << 28) / soma;
+        int o[4] = {0, 0, 0, 0};
+        for (int j = 0; j < T; j++) {
+            int p = 0;
+            if (j <= i) {
+                const int ex = exp_dif(mx, sc(j)) >> 3;
+                p = min((ex * inv + (1 << 19)) >> 20, 255);
 #pragma unroll
-            for (int d = 0; d < 4; d++) o[d] += p * va[j][d];
+                for (int d = 0; d < 4; d++) o[d] += p * va[j][d];
+            }
+            Pb[(size_t)j * T + i] = (uint8_t)p;
         }
-        Pb[(size_t)j * T + i] = (uint8_t)p;
-    }
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-        const size_t x = (size_t)row * D + h * 4 + d;
-        if (o[d] >= LIM || o[d] <= -LIM) reporta(E_ACUM, kid, x, o[d], -3);
-        Oacc[x] = o[d];
-        Oe[x] = (int16_t)(ev - 8);
+        for (int d = 0; d < 4; d++) {
+            const size_t x = (size_t)row * D + h * 4 + d;
+            if (o[d] >= LIM || o[d] <= -LIM) reporta(E_ACUM, kid, x, o[d], -3);
+            Oacc[x] = o[d];
+            Oe[x] = (int16_t)(ev - 8);
+        }
     }
 }
 
-template <int TMAX, int LIMITE>
+template <int TMAX, int LIMITE, int NR>
 __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE,
                                                         const int8_t* __restrict__ qm, const int8_t* __restrict__ qE,
                                                         const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
@@ -93,56 +115,77 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     const uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
     int eq, ek, ev, ego;
-    alinha4(gom, goE, D, h * 4, blk, b0, T, GA, red, goa, ego);
-    alinha4(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
-    alinha4(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
-    alinha4(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
+    alinha4<NR>(gom, goE, D, h * 4, blk, b0, T, GA, red, goa, ego);
+    alinha4<NR>(qm, qE, ld, h * 4, blk, b0, T, GA, red, qa, eq);
+    alinha4<NR>(qm, qE, ld, D + h * 4, blk, b0, T, GA, red, ka, ek);
+    alinha4<NR>(qm, qE, ld, 2 * D + h * 4, blk, b0, T, GA, red, va, ev);
     __syncthreads();
-    // threads past the sequence stay for the barriers of the reductions: their row loops are empty (ie = -1),
-    // their aligned values zero, and they write nothing
-    const int i = threadIdx.x, ie = i < T ? i : -1;
-    const int g0 = goa[i][0], g1 = goa[i][1], g2 = goa[i][2], g3 = goa[i][3];
-    auto gp_ij = [&](int j) { return g0 * va[j][0] + g1 * va[j][1] + g2 * va[j][2] + g3 * va[j][3]; };
+    // the thread's rows (-1: none); every thread stays for the barriers of the block reductions
+    int lin[NR];
+#pragma unroll
+    for (int k = 0; k < NR; k++) lin[k] = linha_de<NR>(threadIdx.x, k, T);
+    auto gp_ij = [&](int i, int j) { return goa[i][0] * va[j][0] + goa[i][1] * va[j][1] + goa[i][2] * va[j][2] + goa[i][3] * va[j][3]; };
     // shift of gP: exact causal maximum, or max_i ||dO_i||_inf * max_j ||v_j||_1
     int mg = 0;
     if constexpr (LIMITE) {
-        const int b1 = max(max(abs(g0), abs(g1)), max(abs(g2), abs(g3)));
-        const int b2 = abs(va[i][0]) + abs(va[i][1]) + abs(va[i][2]) + abs(va[i][3]);
+        int b1 = 0, b2 = 0;
+#pragma unroll
+        for (int k = 0; k < NR; k++) {
+            const int i = lin[k];
+            if (i < 0) continue;
+            b1 = max(b1, max(max(abs(goa[i][0]), abs(goa[i][1])), max(abs(goa[i][2]), abs(goa[i][3]))));
+            b2 = max(b2, abs(va[i][0]) + abs(va[i][1]) + abs(va[i][2]) + abs(va[i][3]));
+        }
         mg = bloco_max(b1, red) * bloco_max(b2, red);
     } else {
-        for (int j = 0; j <= ie; j++) mg = max(mg, abs(gp_ij(j)));
+#pragma unroll
+        for (int k = 0; k < NR; k++)
+            for (int j = 0; j <= lin[k]; j++) mg = max(mg, abs(gp_ij(lin[k], j)));
         mg = bloco_max(mg, red);
     }
     const int sh = max(bitlen(mg) - 15, 0), egp = ego + ev + sh;
     // s_i = rnd(sum_j P_ij gP'_ij, 8)
-    int s = 0, pm = 0, gm = 0;
-    for (int j = 0; j <= ie; j++) {
-        const int p = Pb[(size_t)j * T + i], gp = rnd_d(gp_ij(j), sh);
-        s += p * gp;
-        if constexpr (LIMITE) { pm = max(pm, p); gm = max(gm, abs(gp)); }
+    int sl[NR], pm = 0, gm = 0;
+#pragma unroll
+    for (int k = 0; k < NR; k++) {
+        const int i = lin[k];
+        int s = 0;
+        for (int j = 0; j <= i; j++) {
+            const int p = Pb[(size_t)j * T + i], gp = rnd_d(gp_ij(i, j), sh);
+            s += p * gp;
+            if constexpr (LIMITE) { pm = max(pm, p); gm = max(gm, abs(gp)); }
+        }
+        if (s >= LIM || s <= -LIM) reporta(E_ACUM, kid, (long long)(b0 + i) * ld + h * 4, s, -4);
+        sl[k] = rnd_d(s, 8);
+        if (i >= 0) slin[i] = sl[k];
     }
-    if (s >= LIM || s <= -LIM) reporta(E_ACUM, kid, (long long)(b0 + i) * ld + h * 4, s, -4);
-    const int sl = rnd_d(s, 8);
-    slin[i] = sl;
     // shift of dS: exact maximum of |P (gP' - s)|, or max P * (max |gP'| + max |s|)
     int md = 0;
     if constexpr (LIMITE) {
-        const int pmb = bloco_max(pm, red), gmb = bloco_max(gm, red), smb = bloco_max(abs(sl), red);
+        int sm = 0;
+#pragma unroll
+        for (int k = 0; k < NR; k++) sm = max(sm, lin[k] >= 0 ? abs(sl[k]) : 0);
+        const int pmb = bloco_max(pm, red), gmb = bloco_max(gm, red), smb = bloco_max(sm, red);
         md = pmb * (gmb + smb);
     } else {
-        for (int j = 0; j <= ie; j++) md = max(md, abs((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(j), sh) - sl)));
+#pragma unroll
+        for (int k = 0; k < NR; k++)
+            for (int j = 0; j <= lin[k]; j++) md = max(md, abs((int)Pb[(size_t)j * T + lin[k]] * (rnd_d(gp_ij(lin[k], j), sh) - sl[k])));
         md = bloco_max(md, red);                                   // also publishes slin
     }
     const int sh2 = max(bitlen(md) - DSB, 0), eds = egp - 9 + sh2;
-    // rows: gq_i = sum_j dS_ij k_j
-    {
+    // no barrier below: a thread without rows is done
+#pragma unroll 1
+    for (int k = 0; k < NR; k++) {
+        const int i = lin[k];
+        if (i < 0) continue;
+        // row i: gq_i = sum_j dS_ij k_j
         int gq[4] = {0, 0, 0, 0};
-        for (int j = 0; j <= ie; j++) {
-            const int ds = rnd_d((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(j), sh) - sl), sh2);
+        for (int j = 0; j <= i; j++) {
+            const int ds = rnd_d((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(i, j), sh) - sl[k]), sh2);
 #pragma unroll
             for (int d = 0; d < 4; d++) gq[d] += ds * ka[j][d];
         }
-        if (ie < 0) return;                                         // no barrier follows
 #pragma unroll
         for (int d = 0; d < 4; d++) {
             const size_t o = (size_t)(b0 + i) * ld + h * 4 + d;
@@ -150,10 +193,8 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
             Gacc[o] = gq[d];
             Ge[o] = (int16_t)(eds + ek);
         }
-    }
-    // columns: gk_j = sum_{i >= j} dS_ij q_i, gv_j = sum_{i >= j} P_ij dO_i (row j of the stored P is contiguous)
-    {
-        const int jj = threadIdx.x;
+        // column jj = i: gk_j = sum_{i >= j} dS_ij q_i, gv_j = sum_{i >= j} P_ij dO_i (row j of the stored P is contiguous)
+        const int jj = i;
         const int v0 = va[jj][0], v1 = va[jj][1], v2 = va[jj][2], v3 = va[jj][3];
         const uint8_t* Pr = Pb + (size_t)jj * T;
         int gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0};

@@ -13,13 +13,14 @@
 // output and K-block the work is cvt, ldexp, fma and add: 4 VALU ops, against 9 in integer form. This per-block
 // VALU work, not the MFMA, bounds the kernel.
 //
-// Tiling: a workgroup of 4 x KS waves owns a 32 x 128 output tile (one 128-column block at BLK=128, four at
-// BLK=32). K is walked in stages of 128 bytes per row (4 blocks at BLK=32, 1 at BLK=128): wave group g
-// (4 waves) takes stages s = g (mod KS) and stages each one through its own double-buffered LDS tile of
-// 160 rows (32 of A, 128 of B) with coalesced 16-byte loads, issued one stage ahead of the MFMAs; wave w of the
-// group computes the 32 x 32 sub-tile of columns 32 w as 2 x 2 MFMA 16x16x32 tiles. The KS partial sums are
-// added in LDS (integer addition, exact in any order). The summed tile is then read in a row-block layout
-// (16 consecutive columns per lane) where the block quantization and the fused epilogues run:
+// Tiling: a workgroup of 4 R x KS waves owns a BM x 128 output tile, BM = 32 R rows (R = 1 by default; 2 and 4 are
+// the taller tiles jt_gemm_bm selects), one 128-column block at BLK=128, four at BLK=32. K is walked in stages of
+// 64 (BLK=32) or 128 (BLK=128) bytes per row: wave group g (4 R waves) takes stages s = g (mod KS) and stages each
+// one through its own double-buffered LDS tile of BM + 128 rows (BM of A, 128 of B) with coalesced loads, issued
+// two stages ahead of the MFMAs; wave w of the group computes the 32 x 32 sub-tile of rows 32 (w / 4) and columns
+// 32 (w % 4) as 2 x 2 MFMA 16x16x32 tiles. The KS partial sums are added in LDS (integer addition, exact in any
+// order). The summed tile is then read in a row-block layout (16 consecutive columns per lane) where the block
+// quantization and the fused epilogues run:
 //   MODO 0 block output | 1 raw output | 2 + residual add (soma) | 3 + ReLU^2 second output
 //   4 ReLU^2 backward with H
 // The fused epilogues compute exactly the separate ops on the quantized GEMM output (jatai_cuda.cu:195-200).
@@ -28,16 +29,16 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace gemm {
-constexpr int BM = 32, BN = 128, PAD = 4;
-constexpr int ROWS = BM + BN;            // rows of a stage tile: 32 of A then 128 of B
+constexpr int BM = 32, BN = 128, PAD = 4;   // BM: rows of the default tile (R = 1); a tile has 32 R rows
 // bytes of K per row and stage: 64 at BLK=32 (two blocks; smaller buffers, more resident waves), 128 at BLK=128
 // BLK=32: 64-byte rows, unpadded, with the 8-byte chunk c of tile row r stored at chunk c ^ ((r >> 1) & 7): the
 // MFMA fragment reads (16 rows x one chunk per half-wave) and the stage stores (8 rows x 8 chunks per wave) then
 // touch every LDS bank once. BLK=128: 128-byte rows padded by 8 bytes.
-template <int BLK> struct Est {
+template <int BLK, int R = 1> struct Est {
     static constexpr int SK = BLK == 32 ? 64 : 128;
     static constexpr bool SWZ = BLK == 32;
     static constexpr int LD = SWZ ? SK : SK + 8;   // LDS row stride of a stage tile
+    static constexpr int ROWS = 32 * R + BN;        // rows of a stage tile: 32 R of A then 128 of B
     static constexpr int STAGE = ROWS * LD;
     static constexpr int VB = SK / 8;    // bytes each of the 8 lanes of a row moves per stage
     __device__ static int pos(int r, int c) { return r * LD + 8 * (SWZ ? (c ^ ((r >> 1) & 7)) : c); }   // byte offset of chunk c
@@ -45,15 +46,21 @@ template <int BLK> struct Est {
 }
 
 // The body of one workgroup's tile (rows row0 .., columns col0 ..), shared by k_gemm and the grouped k_gemm_lote.
-template <int BLK, int MODO, int KS>
+template <int BLK, int MODO, int KS, int R = 1>
 __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                            const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                            const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
                                            int K, int kid, const int row0, const int col0, const Otim ot = Otim{}, int k_lr = 0,
                                            int ef = 0, int est = 0) {
-    using namespace gemm;
-    constexpr int SK = Est<BLK>::SK, LD = Est<BLK>::LD, STAGE = Est<BLK>::STAGE, VB = Est<BLK>::VB;
+    using gemm::BN;
+    using gemm::PAD;
+    using E = gemm::Est<BLK, R>;
+    constexpr int SK = E::SK, LD = E::LD, STAGE = E::STAGE, VB = E::VB;
+    constexpr int BM = 32 * R;                                      // tile rows
+    constexpr int GT = 256 * R;                                     // threads of a K-split group (4 R waves)
+    constexpr int NL = 1 + 4 / R;                                   // stage rows per thread: BM of A, then 128 of B
+    constexpr int OB = BM > 64 ? BM : 64;                           // first thread of the B-row maxima (wave aligned)
     extern __shared__ __align__(16) char smem[];
     const int nb = K / BLK, ns = (K + SK - 1) / SK;
     constexpr int BPS = SK / BLK;                                   // blocks per stage
@@ -74,28 +81,28 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nbc], EB rows [BN][nbc]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
-    const int g = wave >> 2, wq = wave & 3, wc = wq * 32, tg = tid & 255;
+    const int g = wave / (4 * R), wq = wave % (4 * R), wr = (wq >> 2) * 32, wc = (wq & 3) * 32, tg = tid & (GT - 1);
     char* meu = buf + (size_t)g * 2 * STAGE;                        // this group's two stage buffers
 
-    // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + 32 i, i = 0..4
-    // (row 0..31 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
-    // Addresses: a workgroup-uniform base per 32-row band (A's rows, then B's in four bands) plus one 32-bit lane
-    // offset vr K + vc shared by the five loads (< 128 * 65536 = 2^23), so the loads take a scalar base.
+    // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + BM i, i = 0 .. NL - 1
+    // (rows 0 .. BM - 1 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
+    // Addresses: a workgroup-uniform base per BM-row band (A's rows, then B's in 128 / BM bands) plus one 32-bit
+    // lane offset vr K + vc shared by the NL loads (< 128 * 65536 = 2^23), so the loads take a scalar base.
     const int vr = tg >> 3, vc = (tg & 7) * VB;
-    const int8_t* src[5];
+    const int8_t* src[NL];
     src[0] = A + (size_t)row0 * K;
 #pragma unroll
-    for (int i = 1; i < 5; i++) src[i] = B + (size_t)(col0 + 32 * (i - 1)) * K;
+    for (int i = 1; i < NL; i++) src[i] = B + (size_t)(col0 + BM * (i - 1)) * K;
     const unsigned vofs = (unsigned)(vr * K + vc);
-    int4 reg[5], reg2[5];                                           // two register sets: loads run two stages ahead
+    int4 reg[NL], reg2[NL];                                         // two register sets: loads run two stages ahead
     // The last stage may extend past K (nb not a multiple of the blocks per stage): its vectors past K re-read the
     // row's last vector instead (a uniform test; those bytes land in blocks >= nb, which are never computed).
-    auto busca = [&](int st, int4 (&r)[5]) {
+    auto busca = [&](int st, int4 (&r)[NL]) {
         int o = st * SK;
         if (o + SK > K) o = min(o + vc, K - VB) - vc;
         const unsigned d = vofs + (unsigned)o;
 #pragma unroll
-        for (int i = 0; i < 5; i++) {
+        for (int i = 0; i < NL; i++) {
             if constexpr (VB == 16) r[i] = *reinterpret_cast<const int4*>(src[i] + d);
             else {
                 const int2 t = *reinterpret_cast<const int2*>(src[i] + d);
@@ -103,26 +110,26 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             }
         }
     };
-    auto guarda = [&](int par, const int4 (&r)[5]) {
+    auto guarda = [&](int par, const int4 (&r)[NL]) {
         char* d = meu + par * STAGE;
 #pragma unroll
-        for (int i = 0; i < 5; i++) {
+        for (int i = 0; i < NL; i++) {
             if constexpr (VB == 16) {
-                int2* q = reinterpret_cast<int2*>(d + (vr + 32 * i) * LD + vc);
+                int2* q = reinterpret_cast<int2*>(d + (vr + BM * i) * LD + vc);
                 q[0] = make_int2(r[i].x, r[i].y);
                 q[1] = make_int2(r[i].z, r[i].w);
             } else {
-                *reinterpret_cast<int2*>(d + Est<BLK>::pos(vr + 32 * i, vc >> 3)) = make_int2(r[i].x, r[i].y);
+                *reinterpret_cast<int2*>(d + E::pos(vr + BM * i, vc >> 3)) = make_int2(r[i].x, r[i].y);
             }
         }
     };
-    // output-stage coordinates (threads 0..255): row orow, columns oc .. oc + 15
-    const int orow = (tid >> 3) & 31, oc = (tid & 7) * 16;
+    // output-stage coordinates (threads 0 .. GT - 1): row orow, columns oc .. oc + 15
+    const int orow = (tid >> 3) & (BM - 1), oc = (tid & 7) * 16;
     // Several chunks: RA and RB first, by one pass over the exponent rows in global memory (rows of nb bytes, nb a
     // multiple of 16 there: 16-byte loads). One chunk: from the staged exponents, below.
     if (nch > 1) {
         const int8_t* er = tid < BM ? EA + (size_t)(row0 + tid) * nb
-                                    : (tid >= 64 && tid < 64 + BN) ? EB + (size_t)(col0 + tid - 64) * nb : nullptr;
+                                    : (tid >= OB && tid < OB + BN) ? EB + (size_t)(col0 + tid - OB) * nb : nullptr;
         if (er) {
             int m = -128;
             for (int v = 0; v < nb / 16; v++) {
@@ -130,7 +137,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                 m = max(m, max(max(max_i8x4(t.x), max_i8x4(t.y)), max(max_i8x4(t.z), max_i8x4(t.w))));
             }
             if (tid < BM) ra_s[tid] = m;
-            else rb_s[tid - 64] = m;
+            else rb_s[tid - OB] = m;
         }
     }
     // shift tables of K-blocks b0 .. b0 + nbc - 1 from the staged exponent bytes (rows of nbc bytes); then the
@@ -143,8 +150,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         const int ra4 = 4 - ra_s[r], rbn = -rb_s[c];
         const int8_t* ea = st_s + r * nbc;
         const int8_t* eb = st_s + (BM + c) * nbc;
-        constexpr int U = 4, SA = 8 * KS, SB = 2 * KS;
-        for (int b0 = tid >> 5; b0 < nbc; b0 += U * SA) {           // entries b * BM + r
+        constexpr int U = 4, SA = GT * KS / BM, SB = GT * KS / BN;   // SA = 8 KS, SB = 2 R KS
+        for (int b0 = tid / BM; b0 < nbc; b0 += U * SA) {           // entries b * BM + r
             int e[U];
 #pragma unroll
             for (int u = 0; u < U; u++) e[u] = b0 + u * SA < nbc ? (int)ea[b0 + u * SA] : 0;
@@ -162,30 +169,30 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         __syncthreads();
     };
-    // one chunk (K <= 4096): the tile's 32 rows of A and 128 rows of B are two contiguous spans (32 nb and 128 nb
+    // one chunk (K <= 4096): the tile's BM rows of A and 128 rows of B are two contiguous spans (BM nb and 128 nb
     // bytes, multiples of 16): 16-byte loads in rounds of 4, all issued before the stores; indices past the span
     // re-read its last vector and store it to a junk slot after the span, so neither side branches. RA and RB
     // come from the staged bytes.
     auto tabelas_unica = [&]() {
-        const int nva = 2 * nb, nvt = 10 * nb;
+        const int nva = BM * nb / 16, nvt = (BM + BN) * nb / 16;
         const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
         const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
-        for (int v0 = tid; v0 < nvt; v0 += 4 * 256 * KS) {
+        for (int v0 = tid; v0 < nvt; v0 += 4 * GT * KS) {
             int4 t[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int v = min(v0 + k * 256 * KS, nvt - 1);
+                const int v = min(v0 + k * GT * KS, nvt - 1);
                 t[k] = v < nva ? ga[v] : gb[v - nva];
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int v = min(v0 + k * 256 * KS, nvt);
+                const int v = min(v0 + k * GT * KS, nvt);
                 *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
             }
         }
         __syncthreads();
         // RA, RB: 16 exponent bytes per LDS read when the rows are 16-byte aligned (nb a multiple of 16)
-        const int8_t* er = tid < BM ? st_s + tid * nb : (tid >= 64 && tid < 64 + BN) ? st_s + (BM + tid - 64) * nb : nullptr;
+        const int8_t* er = tid < BM ? st_s + tid * nb : (tid >= OB && tid < OB + BN) ? st_s + (BM + tid - OB) * nb : nullptr;
         if (er) {
             int m = -128;
             if (nb % 16 == 0) {
@@ -197,7 +204,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                 for (int b = 0; b < nb; b++) m = max(m, (int)er[b]);
             }
             if (tid < BM) ra_s[tid] = m;
-            else rb_s[tid - 64] = m;
+            else rb_s[tid - OB] = m;
         }
         __syncthreads();
         desloca_tab(nb);
@@ -206,7 +213,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // 16-byte vector at a time (this runs between chunks, with the accumulators live)
     auto tabelas_parte = [&](int b0, int nbc) {
         const int vpr = nbc / 16;
-        for (int v = tid; v < (BM + BN) * vpr; v += 256 * KS) {
+        for (int v = tid; v < (BM + BN) * vpr; v += GT * KS) {
             const int r = v / vpr, k = v - r * vpr;
             const int8_t* e = r < BM ? EA + (size_t)(row0 + r) * nb : EB + (size_t)(col0 + r - BM) * nb;
             *reinterpret_cast<int4*>(st_s + (size_t)r * nbc + 16 * k) = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
@@ -241,8 +248,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             long fa[2], fb[2];
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                fa[t] = *reinterpret_cast<const long*>(tile + Est<BLK>::pos(16 * t + lr, ch));
-                fb[t] = *reinterpret_cast<const long*>(tile + Est<BLK>::pos(BM + wc + 16 * t + lr, ch));
+                fa[t] = *reinterpret_cast<const long*>(tile + E::pos(wr + 16 * t + lr, ch));
+                fb[t] = *reinterpret_cast<const long*>(tile + E::pos(BM + wc + 16 * t + lr, ch));
             }
 #pragma unroll
             for (int ti = 0; ti < 2; ti++)
@@ -255,8 +262,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     auto escala = [](int nbv) { return __hiloint2double((1023 + nbv) << 20, 0); };
     auto arredonda = [&](int b, const v4i (&p)[2][2]) {
         const int bt = b - b0;                                      // block index in the chunk's tables
-        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 4 * lg);
-        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + 16 + 4 * lg);
+        const v4i na0 = *reinterpret_cast<const v4i*>(na_s + bt * BM + wr + 4 * lg);
+        const v4i na1 = *reinterpret_cast<const v4i*>(na_s + bt * BM + wr + 16 + 4 * lg);
         const double cb0 = escala(nb_s[bt * BN + wc + lr]), cb1 = escala(nb_s[bt * BN + wc + 16 + lr]);
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
@@ -325,10 +332,10 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
     int xin[16], exin = 0;
     if constexpr (MODO == 2 || MODO == 4) {
-        if (tid < 256) { le_i8(Xm + o, xin); exin = XE[oe]; }
+        if (tid < GT) { le_i8(Xm + o, xin); exin = XE[oe]; }
     }
     int base[16];
-    if (tid < 256) {
+    if (tid < GT) {
         const int ra = ra_s[orow];
 #pragma unroll
         for (int j = 0; j < 16; j++) base[j] = ra + rb_s[oc + j] - 4;
@@ -340,20 +347,20 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 #pragma unroll
         for (int tj = 0; tj < 2; tj++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
+            for (int i = 0; i < 4; i++) acc_s[g * TILE + (wr + 16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr] = acc[ti][tj][i];
     if (fora) {                                                     // K > 4096 only: an accumulator out of range
         const int e = __builtin_ctz(fora), ti = e >> 3, tj = (e >> 2) & 1, i = e & 3;
-        reporta(E_ACUM, kid, (long long)(row0 + 16 * ti + 4 * lg + i) * N + col0 + wc + 16 * tj + lr,
-                acc_s[g * TILE + (16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr], -3);
+        reporta(E_ACUM, kid, (long long)(row0 + wr + 16 * ti + 4 * lg + i) * N + col0 + wc + 16 * tj + lr,
+                acc_s[g * TILE + (wr + 16 * ti + 4 * lg + i) * (BN + PAD) + wc + 16 * tj + lr], -3);
     }
     OtimEnt<16> otx;                                               // mode 5: the optimizer's inputs, in flight during the LDS round trip
     if constexpr (MODO == 5) {
-        if (tid < 256) otx = otim_le<16>(ot, (long long)o, (long long)(o / BLK), ef);
+        if (tid < GT) otx = otim_le<16>(ot, (long long)o, (long long)(o / BLK), ef);
     }
     __syncthreads();
     if constexpr (MODO == 1) {
         // raw output, coalesced: thread t writes column t % 128 of rows 16 (t / 128) .. +15 (64 consecutive ints per wave)
-        if (tid < 256) {
+        if (tid < GT) {
             const int c = tid & 127, r0 = (tid >> 7) * 16;
             const int rbc = rb_s[c] - 4;
 #pragma unroll 4
@@ -369,7 +376,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         return;
     } else {
-        if (tid >= 256) return;
+        if (tid >= GT) return;
         int v[16];
 #pragma unroll
         for (int j = 0; j < 16; j += 4) {
@@ -438,7 +445,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Eg;
             if constexpr (KS == 1 && BLK == 32) {
-                // Om2 given: also the transpose T(gh) [N, M] blocked along M. The tile's 32 rows are one block of each
+                // Om2 given: also the transpose T(gh) [N, M] blocked along M. The tile's BM rows are R blocks of each
                 // of its 128 columns: the same requantization as k_transpoe (quant(m^T, expand(E)^T), ops.py:121-123),
                 // from the quantized tile staged in LDS. KS = 1: every thread is here, so the barriers are uniform.
                 if (Om2 != nullptr) {
@@ -448,19 +455,20 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                     grava_i8(qs + orow * (BN + 16) + oc, q);
                     if (lider) es[orow * (BN / 32) + oc / 32] = (int8_t)Eg;
                     __syncthreads();
-                    const int c = tid >> 1, hf = tid & 1;                   // column c, rows 16 hf .. 16 hf + 15
+                    // column c, rows 16 pt .. 16 pt + 15 (2 R threads per column; lanes 2j, 2j + 1 hold one block)
+                    const int c = tid / (2 * R), pt = tid % (2 * R);
                     int tv[16], te[16];
 #pragma unroll
                     for (int k = 0; k < 16; k++) {
-                        const int r = 16 * hf + k;
+                        const int r = 16 * pt + k;
                         tv[k] = qs[r * (BN + 16) + c];
                         te[k] = es[r * (BN / 32) + (c >> 5)];
                     }
                     int8_t t8[16];
-                    const long long ot = (long long)(col0 + c) * M + row0 + 16 * hf;
+                    const long long ot = (long long)(col0 + c) * M + row0 + 16 * pt;
                     const int Et = quant8_d<16, 2>(tv, te, t8, kid, ot);   // int8 exponents
                     grava_i8(Om2 + ot, t8);
-                    if (hf == 0) OE2[(size_t)(col0 + c) * (M / 32) + row0 / 32] = (int8_t)Et;
+                    if ((pt & 1) == 0) OE2[(size_t)(col0 + c) * (M / 32) + row0 / 32 + (pt >> 1)] = (int8_t)Et;
                 }
             }
         }
@@ -471,19 +479,19 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 // runs, so a captured graph follows the value set before each replay.
 __device__ int g_res_est = 0;
 
-template <int BLK, int MODO, int KS>
-__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
+template <int BLK, int MODO, int KS, int R = 1>
+__global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                                    const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                                    int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
                                                    int N, int K, int kid) {
-    gemm_corpo<BLK, MODO, KS>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * gemm::BM, blockIdx.x * gemm::BN,
+    gemm_corpo<BLK, MODO, KS, R>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * 32 * R, blockIdx.x * gemm::BN,
                               Otim{}, 0, 0, MODO == 2 ? g_res_est : 0);
 }
 
 // Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels
 // by value in the kernel arguments; GEMM i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over
-// its (M / 32) x (N / 128) tiles. Same tiles, same arithmetic as k_gemm<BLK, 1, KS>.
+// its (M / 32 R) x (N / 128) tiles. Same tiles, same arithmetic as k_gemm<BLK, 1, KS, R>.
 constexpr int LOTE_G = 64;                  // 3852 bytes of kernel arguments: every weight gradient of a step in one launch
 static_assert(sizeof(int8_t*) * 6 * LOTE_G + sizeof(int) * (3 * LOTE_G + 3) <= 4096, "kernel argument limit");
 struct LoteG {
@@ -497,15 +505,15 @@ struct LoteG {
     int n, K;
 };
 
-template <int BLK, int KS>
-__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_lote(const LoteG L, int kid) {
+template <int BLK, int KS, int R = 1>
+__global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_lote(const LoteG L, int kid) {
     const int t = blockIdx.x;
     int i = 0;                                                      // uniform: kernel arguments, scalar loads
     for (int s = 32; s; s >>= 1)
         if (i + s < L.n && L.ini[i + s] <= t) i += s;
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
-    gemm_corpo<BLK, 1, KS>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i], L.N[i],
-                           L.K, kid + i, (local / ntx) * gemm::BM, (local % ntx) * gemm::BN);
+    gemm_corpo<BLK, 1, KS, R>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i],
+                              L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN);
 }
 
 // The weight gradients of a step with the optimizer in the epilogue (mode 5): GEMM i's tile goes through
@@ -521,25 +529,28 @@ struct LoteGO {
     int n, K;
 };
 
-template <int BLK, int KS>
-__global__ void __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_otim_lote(const LoteGO L, int k_lr, int ef, int kid) {
+template <int BLK, int KS, int R = 1>
+__global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_otim_lote(const LoteGO L, int k_lr, int ef, int kid) {
     const int t = blockIdx.x;
     int i = 0;
     for (int s = 16; s; s >>= 1)
         if (i + s < L.n && L.ini[i + s] <= t) i += s;
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
-    gemm_corpo<BLK, 5, KS>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.M[i], L.N[i],
-                           L.K, kid + i, (local / ntx) * gemm::BM, (local % ntx) * gemm::BN, L.ot[i], k_lr, ef);
+    gemm_corpo<BLK, 5, KS, R>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.M[i],
+                              L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN, L.ot[i], k_lr, ef);
 }
 
-// dynamic LDS bytes for nb K-blocks and KS K-splits
-static inline size_t gemm_lds(int nb, int ks, int blk) {
-    using namespace gemm;
+// dynamic LDS bytes for nb K-blocks, KS K-splits and tiles of 32 R rows
+static inline size_t gemm_lds(int nb, int ks, int blk, int R = 1) {
+    using gemm::BN;
+    using gemm::PAD;
+    const int bm = 32 * R;
     nb = std::min(nb, 4096 / blk);                                  // the shift tables hold one chunk of K
-    const size_t fixo = (size_t)(BM + BN) * 4 + (size_t)nb * BM * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
-    size_t area = (size_t)ks * 2 * (blk == 32 ? Est<32>::STAGE : Est<128>::STAGE);
-    const size_t exp_bruto = (size_t)nb * (BM + BN) + 16;
-    const size_t acc = (size_t)ks * BM * (BN + PAD) * 4;
+    const size_t fixo = (size_t)(bm + BN) * 4 + (size_t)nb * bm * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
+    const size_t stage = (size_t)(32 * R + BN) * (blk == 32 ? gemm::Est<32>::LD : gemm::Est<128>::LD);
+    size_t area = (size_t)ks * 2 * stage;
+    const size_t exp_bruto = (size_t)nb * (bm + BN) + 16;
+    const size_t acc = (size_t)ks * bm * (BN + PAD) * 4;
     if (exp_bruto > area) area = exp_bruto;
     if (acc > area) area = acc;
     return fixo + area;

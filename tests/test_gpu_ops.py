@@ -51,20 +51,101 @@ def test_caso_vs_spec(blk, i):
                     f"(flat index, gpu, oracle, count): {difs}")
 
 
-DOMINIO = CS.casos_dominio()
+GEMMS = [i for i, (n, _) in enumerate(CASOS) if n.startswith("gemm")]
+
+
+@pytest.fixture
+def tile_gemm(request):
+    """jt_gemm_bm(bm) for the test, then back to the automatic tile (the reference's tile() helper,
+    teste_ops.py:34-40)."""
+    from jatai_amd import ops as O
+    lib = O.carrega_lib()
+    lib.jt_gemm_bm(request.param)
+    yield request.param
+    lib.jt_gemm_bm(0)
+
+
+@pytest.mark.parametrize("tile_gemm", [64, 128], indirect=True)
+@pytest.mark.parametrize("blk", [128, 32])
+@pytest.mark.parametrize("i", GEMMS, ids=[CASOS[i][0] for i in GEMMS])
+def test_caso_gemm_tile_forcado(blk, i, tile_gemm):
+    """Every GEMM case of the reference suite again with the taller tiles forced through jt_gemm_bm (64 and 128
+    rows: 8 and 16 waves per K-split group), as teste_ops.py:99-103 runs each GEMM at both of its tiles: the same
+    hashes as the spec's."""
+    test_caso_vs_spec(blk, i)
+
+
+@pytest.mark.parametrize("tile_gemm", [64, 128], indirect=True)
+def test_gemm_tile_forcado_k_longo_e_lote(tile_gemm):
+    """Taller tiles on the long-K path (K = 8192: two 4096-value chunks of shift tables), on the transposed
+    ReLU^2-backward copy (two blocks per column of the tile at 64 rows, four at 128) and on a grouped launch, each
+    equal to the oracle (or to the separate launches)."""
+    blk = 32
+    gpu, cpu = GPU(blk), CPU(blk)
+    s = lambda t: R.substream(78, f"{t} {tile_gemm}")
+    for M, N, K in ((128, 256, 8192), (256, 384, 1024)):
+        A = R.bloco(s(f"A{K}"), M, K, blk, espalha=5, e0=-8)
+        B = R.bloco(s(f"B{K}"), N, K, blk, espalha=5, e0=-12)
+        X = R.bloco(s(f"X{K}"), M, N, blk, espalha=3, e0=2)
+        ref = [CS.plano(t) for t in _gemm_modos(cpu.ops, *[tuple(cpu.dev(v) for v in T) for T in (A, B, X)])]
+        out = [CS.plano(t) for t in _gemm_modos(gpu.ops, *[tuple(gpu.dev(v) for v in T) for T in (A, B, X)])]
+        gpu.reg.confere_device()
+        for modo, (a, b) in enumerate(zip(out, ref)):
+            for x, y in zip(a, b):
+                assert np.array_equal(host(x), host(y)), f"K={K} mode {modo}: {primeira_diferenca(host(x), host(y))}"
+        Ag, Bg, Xg = (tuple(gpu.dev(v) for v in T) for T in (A, B, X))
+        Gt, GtT = gpu.ops.gemm_relu2_back_t(Ag, Bg, Xg)
+        refT = cpu.ops.transpoe(cpu.ops.gemm_relu2_back(*[tuple(cpu.dev(v) for v in T) for T in (A, B, X)]))
+        for x, y in zip(GtT, refT):
+            assert np.array_equal(host(x), host(y)), f"K={K} transposed relu2_back: {primeira_diferenca(host(x), host(y))}"
+    pares = [(tuple(gpu.dev(v) for v in R.bloco(s(f"lA{j}"), M, 1024, blk, espalha=6, e0=-20)),
+              tuple(gpu.dev(v) for v in R.bloco(s(f"lB{j}"), N, 1024, blk, espalha=4, e0=-6)), None)
+             for j, (M, N) in enumerate(((256, 512), (512, 128), (128, 256)))]
+    lote = gpu.ops.gemm_cru_lote(pares)
+    for (A, B, _), G in zip(pares, lote):
+        ref = gpu.ops.gemm(A, B, cru=True)
+        for x, y in zip(G, ref):
+            assert np.array_equal(host(x), host(y))
+
+
+ATENCAO4 = [i for i, (n, _) in enumerate(CASOS) if n.startswith("atencao")]
 
 
 @pytest.mark.parametrize("blk", [128, 32])
+@pytest.mark.parametrize("i", ATENCAO4, ids=[CASOS[i][0] for i in ATENCAO4])
+def test_caso_atencao_duas_linhas(blk, i):
+    """The reference suite's attention cases with two query rows per thread (jt_atencao_linhas(2), rows i and
+    T - 1 - i; jatai_cuda.cu:1091): the spec's hashes."""
+    from jatai_amd import ops as O
+    lib = O.carrega_lib()
+    lib.jt_atencao_linhas(2)
+    try:
+        test_caso_vs_spec(blk, i)
+    finally:
+        lib.jt_atencao_linhas(1)
+
+
+DOMINIO = CS.casos_dominio()
+
+
+@pytest.mark.parametrize("linhas", [1, 2])
+@pytest.mark.parametrize("blk", [128, 32])
 @pytest.mark.parametrize("i", range(len(DOMINIO)), ids=[n for n, _ in DOMINIO])
-def test_dominio_vs_spec(blk, i):
+def test_dominio_vs_spec(blk, i, linhas):
     """The rest of the reference's shape domain (rms widths 384-896, softmax V = 384 / 640, head-width-4 attention
     at H = 32 and T = 32 / 96) against the spec's hashes (tests/golden/ops_dominio_blk*.json)."""
     gold = _gold(f"ops_dominio_blk{blk}.json")[i]
     nome, fn = DOMINIO[i]
-    gpu = GPU(blk, vigiar=True)
-    rec = CS.Gravador(gpu.ops, host)
-    saida = fn(rec, CS.Gen(R.substream(1000 + i, nome), blk, gpu.dev), gpu)
-    torch.cuda.synchronize()
+    from jatai_amd import ops as O
+    lib = O.carrega_lib()
+    lib.jt_atencao_linhas(linhas)
+    try:
+        gpu = GPU(blk, vigiar=True)
+        rec = CS.Gravador(gpu.ops, host)
+        saida = fn(rec, CS.Gen(R.substream(1000 + i, nome), blk, gpu.dev), gpu)
+        torch.cuda.synchronize()
+    finally:
+        lib.jt_atencao_linhas(1)
     if [list(x) for x in rec.log] != [list(x) for x in gold["chamadas"]]:
         cpu = CPU(blk)
         ref = fn(cpu.ops, CS.Gen(R.substream(1000 + i, nome), blk, cpu.dev), cpu)
