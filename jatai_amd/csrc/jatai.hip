@@ -52,6 +52,9 @@ static unsigned grade_elem(long long nblocos) { return (unsigned)((nblocos * g_b
 // kernels with 16 values per lane (soma, relu2, relu2_back, peso, otimizador)
 static unsigned grade_u(long long nblocos) { return (unsigned)((nblocos * g_blk + 4095) / 4096); }
 static int ilog2(long long n) { int l = 0; while ((2LL << l) <= n) l++; return l; }
+// attention backward's dS width: 12 bits up to T = 128, one bit less per doubling of T beyond it, rounded up, so
+// that T (2^dsb - 1) (127 << 4) < 2^30 at every T
+static int ds_bits(int T) { return 12 - std::max(0, ilog2(2LL * T - 1) - 7); }
 
 // Dynamic LDS above 64 KiB must be allowed per kernel (gfx950 has 160 KiB per CU): raised once per kernel and
 // size, remembered by kernel address (every k_gemm instantiation has the same function type).
@@ -598,7 +601,7 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
     if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
-    const int dsb = 12 - (ilog2(T) > 7 ? ilog2(T) - 7 : 0);
+    const int dsb = ds_bits(T);
     if (hd == 4) {
         const int nt = (T / g_linhas + 63) & ~63;
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
@@ -669,7 +672,7 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
         return (int)hipErrorInvalidValue;
     const long long BH = (long long)Bt * H;
     const atw::WsB w = atw::parte_b(ws, BH, T);
-    const int dsb = 12 - std::max(0, ilog2(T) - 7);
+    const int dsb = ds_bits(T);
     const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
     const uint8_t* P8 = (const uint8_t*)P;
     const unsigned gp = (unsigned)(BH * (T / 64)), gt = (unsigned)(BH * (T / 16));

@@ -440,9 +440,10 @@ void or_rms_back(const int8_t* gm, const int8_t* gE, const int8_t* ym, const int
 //   score:     u = rnd(q.k, -(eq + ek - log2(hd)/2 + 8))   (the spec's -1 is -log2(4)/2);
 //   ALiBi:     incl = 8 - h // 8 at hd = 4 for every H (the spec, ops.py:208); for hd > 4, incl = 8 - (8 h) / H
 //              (eight slopes 2^0 .. 2^-7 spread evenly over the H heads; at H = 64 the same as the spec's);
-//   dS:        shrunk to 12 - max(0, log2(T) - 7) bits      (12 for T <= 128, keeping |gq|,|gk| < 2^30).
+//   dS:        shrunk to 12 - max(0, ceil(log2 T) - 7) bits (12 for T <= 128, keeping |gq|,|gk| < 2^30).
 static int att_lg(int hd) { return ilog2(hd) / 2; }
-static int att_dsbits(int T) { return 12 - std::max(0, ilog2(T) - 7); }
+static int att_dsbits(int T) { return 12 - std::max(0, ilog2(2 * T - 1) - 7); }
+int or_att_dsbits(int T) { return att_dsbits(T); }
 static i64 att_incl(int h, int H, int hd) { return hd == 4 ? 8 - h / 8 : 8 - (8 * (i64)h) / H; }
 
 // aligned values a[t][d] = rnd(x << GA, emx - e) and the head exponent emx - GA (ops.py:186-192)

@@ -153,6 +153,43 @@ def test_dominio_vs_spec(blk, i, linhas):
         pytest.fail(f"{nome} (BLK={blk}) differs from the spec; first difference per output vs the oracle: {difs}")
 
 
+@pytest.mark.parametrize("linhas", [1, 2])
+@pytest.mark.parametrize("blk", [128, 32])
+@pytest.mark.parametrize("T", [160, 192, 256])
+def test_atencao4_t_longo_vs_oraculo(T, blk, linhas):
+    """Head-width-4 attention past the spec's T <= 128 (this library accepts T % 32 up to 256), forward and both
+    backward variants, against the oracle: the only change from the spec there is dS's width (12 - max(0,
+    ceil(log2 T) - 7) bits: 11 at T = 160 .. 256)."""
+    from jatai_amd import ops as O
+    Bt, H = 2, 64
+    D = 4 * H
+    seed = R.substream(557, f"a4 {T} {blk}")
+    qn = R.bloco(R.substream(seed, "qkv"), Bt * T, 3 * D, blk, espalha=6, e0=-6, zera=0.05)
+    gn = R.bloco(R.substream(seed, "go"), Bt * T, D, blk, espalha=6, e0=-20, zera=0.05)
+    lib = O.carrega_lib()
+    res = {}
+    for nome, be in (("gpu", GPU(blk, vigiar=True)), ("cpu", CPU(blk))):
+        qkv = tuple(be.dev(v) for v in qn)
+        go = tuple(be.dev(v) for v in gn)
+        if nome == "gpu":
+            lib.jt_atencao_linhas(linhas)
+        try:
+            (oacc, oe), P = be.ops.atencao(qkv, Bt, T, H)
+            saida = [oacc, oe, P]
+            for lim in (False, True):
+                old = be.limite(lim)
+                try:
+                    saida += list(be.ops.atencao_back(go, qkv, P, Bt, T, H))
+                finally:
+                    be.limite(old)
+        finally:
+            lib.jt_atencao_linhas(1)
+        res[nome] = [host(x) for x in saida]
+    for nome, a, b in zip(("oacc", "oe", "P", "gacc", "ge", "gacc limite", "ge limite"), res["gpu"], res["cpu"]):
+        d = primeira_diferenca(a, b)
+        assert d is None, f"T={T} {nome}: (flat index, gpu, oracle, count) = {d}"
+
+
 @pytest.mark.parametrize("blk", [32, 128])
 def test_config1(blk):
     gold = _gold("config1.json")[str(blk)]

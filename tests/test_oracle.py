@@ -411,3 +411,25 @@ def test_atencao_hd64_q_zero_so_alibi():
             inv = (1 << 28) // sum(e)
             esperado = [min((v * inv + (1 << 19)) >> 20, 255) for v in e] + [0] * (T - i - 1)
             assert list(P[h, :, i]) == esperado, (h, i)
+
+
+def test_largura_de_ds_por_t():
+    """The attention backward shrinks dS to 12 - max(0, ceil(log2 T) - 7) bits past T = 128 (jatai_oracle.cpp
+    att_dsbits, the kernels' ds_bits). The spec fixes 12 bits for T <= 128 (ops.py:245-247), where its int32 proof
+    bounds |gq|, |gk| = |sum_j dS_ij a_j| by T (2^12 - 1) 2032 < 2^30 (a: aligned values, |a| <= 127 << GA = 2032;
+    RELATORIO_TECNICO.md:897-927). The oracle's rule keeps that bound at every T the kernels accept (T % 32 up to
+    256, T % 64 up to 512), is the spec's 12 bits up to 128, and is the widest width that does so at T = 128, 256
+    and 512: one bit more would break the bound there."""
+    from oracle import ops_oracle as OO
+    largura = OO.lib().or_att_dsbits
+    lim, amax = 1 << 30, 127 << OO.GA
+    for T in range(32, 513, 32):
+        dsb = largura(T)
+        assert 0 < dsb <= 12, T
+        assert T * ((1 << dsb) - 1) * amax < lim, (T, dsb)
+        if T <= 128:
+            assert dsb == 12, T
+        if T in (128, 256, 512):
+            assert T * ((1 << (dsb + 1)) - 1) * amax >= lim, (T, dsb)
+        if T > 32:
+            assert dsb <= largura(T - 32), T                  # never wider for a longer sequence
