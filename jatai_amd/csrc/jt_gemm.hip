@@ -34,6 +34,8 @@ constexpr int BM = 32, BN = 128, PAD = 4;   // BM: rows of the default tile (R =
 // BLK=32: 64-byte rows, unpadded, with the 8-byte chunk c of tile row r stored at chunk c ^ ((r >> 1) & 7): the
 // MFMA fragment reads (16 rows x one chunk per half-wave) and the stage stores (8 rows x 8 chunks per wave) then
 // touch every LDS bank once. BLK=128: 128-byte rows padded by 8 bytes.
+// K-blocks held by the shift tables: all of K up to 4096 values, else chunks of 2048 values
+__host__ __device__ constexpr int bloco_tab(int nb, int blk) { return (nb * blk > 4096 ? 2048 : 4096) / blk; }
 template <int BLK, int R = 1> struct Est {
     static constexpr int SK = BLK == 32 ? 64 : 128;
     static constexpr bool SWZ = BLK == 32;
@@ -65,9 +67,10 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     const int nb = K / BLK, ns = (K + SK - 1) / SK;
     constexpr int BPS = SK / BLK;                                   // blocks per stage
     constexpr int KST = BLK / 32;                                   // MFMA k-steps per block
-    // The shift tables hold at most NBC K-blocks (4096 values of K); a longer K runs in chunks of NBC blocks,
-    // each with its own tables (the row maxima RA, RB are over all of K).
-    constexpr int NBC = 4096 / BLK;
+    // The shift tables hold at most NBC K-blocks: all of K up to 4096 values; a longer K runs in chunks of 2048
+    // values, each with its own tables (the row maxima RA, RB are over all of K). Half-size chunks keep the tables
+    // of a 32-row tile at the LDS size of K = 2048, so four workgroups stay resident per CU.
+    const int NBC = gemm::bloco_tab(nb, BLK);
     const int nbt = min(nb, NBC), nch = (nb + NBC - 1) / NBC;
     // LDS: RA [BM], RB [BN] int32 (live to the end); shift terms na[b][i] = ea_ib + 4 - RA_i (int32) and
     // nb[b][j] = eb_jb - RB_j (int8) of the chunk's blocks, clamped at -100 (n = na + nb <= -22 scales |p| < 2^21
@@ -309,12 +312,13 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         // groups with fewer stages still take part in every barrier of the loop above
         for (int k = nk; k < (s1 - s0 + KS - 1) / KS; k++) __syncthreads();
-        // Past 4096 values of K the int32 accumulator has no a-priori bound: each chunk adds less than 2^30
-        // (NBC blocks of |rnd(p << 4, s)| < 2^23), so a partial sum kept below 2^30 / KS at every chunk end can
-        // neither wrap inside the chunk nor in the sum of the KS partials; one that is not is reported.
+        // Past 4096 values of K the int32 accumulator has no a-priori bound: 4096 values of K add less than 2^30
+        // (4096 / BLK blocks of |rnd(p << 4, s)| < 2^23 BLK / 32), so a partial sum kept below 2^30 / KS at every
+        // multiple of 4096 values (every second chunk) and at the end can neither wrap in between nor in the sum of
+        // the KS partials; one that is not is reported.
         // (the violations are collected as bits and reported after the loop: a call here, with the accumulators
         // and both stage register sets live, would make the compiler keep registers in scratch)
-        if (nch > 1) {
+        if (nch > 1 && ((b0 + nbc) * BLK % 4096 == 0 || c == nch - 1)) {
             constexpr int T = LIM / KS;
 #pragma unroll
             for (int ti = 0; ti < 2; ti++)
@@ -545,7 +549,7 @@ static inline size_t gemm_lds(int nb, int ks, int blk, int R = 1) {
     using gemm::BN;
     using gemm::PAD;
     const int bm = 32 * R;
-    nb = std::min(nb, 4096 / blk);                                  // the shift tables hold one chunk of K
+    nb = std::min(nb, gemm::bloco_tab(nb, blk));                    // the shift tables hold one chunk of K
     const size_t fixo = (size_t)(bm + BN) * 4 + (size_t)nb * bm * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
     const size_t stage = (size_t)(32 * R + BN) * (blk == 32 ? gemm::Est<32>::LD : gemm::Est<128>::LD);
     size_t area = (size_t)ks * 2 * stage;
