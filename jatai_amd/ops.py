@@ -261,6 +261,17 @@ class OpsHip:
         self.reg.depois(kid0, r)
         return Ys
 
+    def de_f32(self, x):
+        """float32 [R, C] to a block tensor: each value split exactly into an integer mantissa and an exponent
+        (frexp: x = v 2^e, |v| < 2^24, an int32 / int16 raw tensor), then the spec's quant of that raw tensor
+        (ops.py:58-72). Integer-only after the exact split; the data path of BASELINE configs 2 and 3 (fp32 N(0, 1)
+        activations, N(0, 0.02) weights). Finite inputs only."""
+        self.reg.exige(x.dtype == torch.float32 and x.dim() == 2 and x.is_cuda, "de_f32: espera float32 [R, C] na GPU")
+        self.reg.exige(bool(torch.isfinite(x).all()), "de_f32: valores nao finitos")
+        m, e = torch.frexp(x)
+        v = (m * float(1 << 24)).to(torch.int32)
+        return self.quant((v.contiguous(), (e - 24).to(torch.int16).contiguous()))
+
     def quant(self, Cc):
         self.reg.confere_cru("C", Cc)
         acc, e = Cc

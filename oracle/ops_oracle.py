@@ -114,6 +114,16 @@ class OpsOraculo:
         lib().or_transpoe(_p(m), _p(E), _i(R), _i(C), _i(self.blk), _p(Y[0]), _p(Y[1]))
         return Y
 
+    def de_f32(self, x):
+        """float32 [R, C] to a block tensor: the exact split x = v 2^e (frexp, |v| < 2^24) as a raw int32 / int16
+        tensor, then the spec's quant (ops.py:58-72)."""
+        x = np.ascontiguousarray(_cpu(x).numpy().astype(np.float32))
+        if not np.isfinite(x).all():
+            raise ValueError("de_f32: non-finite input")
+        m, e = np.frexp(x)
+        v = (m.astype(np.float64) * float(1 << 24)).astype(np.int32)
+        return self.quant((torch.from_numpy(v), torch.from_numpy((e - 24).astype(np.int16))))
+
     def quant(self, Cc):
         acc, e = (_cpu(t) for t in Cc)
         R, C = acc.shape

@@ -44,6 +44,14 @@ def uniform01(seed, shape):
     return (x.astype(np.float64) / float(1 << 53)).reshape(shape)
 
 
+def normal32(seed, shape, sigma=1.0):
+    """float32 samples of N(0, sigma^2) (Box-Muller on two uniform streams, in float64, rounded once)."""
+    u1 = uniform01(substream(seed, "u1"), shape)
+    u2 = uniform01(substream(seed, "u2"), shape)
+    z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
+    return np.ascontiguousarray((sigma * z).astype(np.float32))
+
+
 def bloco(seed, R, C, blk, espalha=4, zera=0.0, e0=-10, mmax=127):
     """Block tensor (m int8 [R,C], E int8 [R,C/blk]): mantissas uniform in [-mmax, mmax], exponents e0 +
     uniform[-espalha, espalha], and each block zeroed (m = 0, E = -127) with probability `zera`.

@@ -77,7 +77,7 @@ def test_caso_gemm_tile_forcado(blk, i, tile_gemm):
 
 @pytest.mark.parametrize("tile_gemm", [64, 128], indirect=True)
 def test_gemm_tile_forcado_k_longo_e_lote(tile_gemm):
-    """Taller tiles on the long-K path (K = 8192: two 4096-value chunks of shift tables), on the transposed
+    """Taller tiles on the long-K path (K = 8192: four 2048-value chunks of shift tables), on the transposed
     ReLU^2-backward copy (two blocks per column of the tile at 64 rows, four at 128) and on a grouped launch, each
     equal to the oracle (or to the separate launches)."""
     blk = 32
@@ -191,6 +191,20 @@ def test_atencao4_t_longo_vs_oraculo(T, blk, linhas):
 
 
 @pytest.mark.parametrize("blk", [32, 128])
+def test_de_f32_vs_oraculo(blk):
+    """The fp32 data path: de_f32 on the GPU (frexp split, then jt_quant) equals the oracle's, bit for bit, on
+    N(0, 1) values with zero blocks, subnormals and large values mixed in."""
+    x = R.normal32(402, (256, 1024))
+    x[0, :blk] = 0.0
+    x[1, :4] = np.array([1e-40, -3e-39, 2.5e-45, 7.0], np.float32)
+    x[2, :blk] *= np.float32(2.0 ** 60)
+    res = [be.ops.de_f32(be.dev(x)) for be in (GPU(blk), CPU(blk))]
+    for nome, a, b in zip(("m", "E"), *res):
+        d = primeira_diferenca(host(a), host(b))
+        assert d is None, f"de_f32 {nome}: {d}"
+
+
+@pytest.mark.parametrize("blk", [32, 128])
 def test_config1(blk):
     gold = _gold("config1.json")[str(blk)]
     gpu = GPU(blk)
@@ -211,16 +225,18 @@ CFG3 = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
 
 @pytest.mark.parametrize("K,N", CFG3, ids=["qkv", "out_proj", "ffn_up", "ffn_down"])
 def test_config3_gemm_shapes(K, N):
-    """fwd Y = X.W^T, dX = dY.(W^T)^T and dW = (dY^T).(X^T)^T (raw) at M = 2048, BLK = 32, vs the oracle."""
+    """fwd Y = X.W^T, dX = dY.(W^T)^T and dW = (dY^T).(X^T)^T (raw) at M = 2048, BLK = 32, vs the oracle. As BASELINE
+    config 3 states them: weights N(0, 0.02) and activations N(0, 1) in fp32, quantized to blocks (de_f32: the exact
+    frexp split, then quant); output gradients N(0, 2^-10)."""
     blk, M = 32, 2048
     gpu, cpu = GPU(blk), CPU(blk)
     seed = R.substream(77, f"cfg3 {K} {N}")
-    Xn = R.bloco(R.substream(seed, "X"), M, K, blk, espalha=3, e0=-8)
-    Wn = R.bloco(R.substream(seed, "W"), N, K, blk, espalha=2, e0=-12)
-    dYn = R.bloco(R.substream(seed, "dY"), M, N, blk, espalha=3, e0=-20)
+    Xf = R.normal32(R.substream(seed, "X"), (M, K))
+    Wf = R.normal32(R.substream(seed, "W"), (N, K), 0.02)
+    dYf = R.normal32(R.substream(seed, "dY"), (M, N), 2.0 ** -10)
     for be in (gpu, cpu):
-        X, W, dY = (tuple(be.dev(v) for v in t) for t in (Xn, Wn, dYn))
         o = be.ops
+        X, W, dY = (o.de_f32(be.dev(v)) for v in (Xf, Wf, dYf))
         be.res = [o.gemm(X, W), o.gemm(dY, o.transpoe(W)), o.gemm(o.transpoe(dY), o.transpoe(X), cru=True)]
     for nome, a, b in zip(("fwd", "dX", "dW"), gpu.res, cpu.res):
         _compara(a, b, f"config3 K={K} N={N} {nome}")
@@ -231,16 +247,19 @@ def test_config2_elementwise():
     blk, M, D, FF, V = 32, 2048, 512, 2048, 256
     gpu, cpu = GPU(blk), CPU(blk)
     s = lambda t: R.substream(88, t)
-    ins = dict(x=R.bloco(s("x"), M, D, blk, espalha=3, e0=-6), y=R.bloco(s("y"), M, D, blk, espalha=3, e0=-9, zera=0.05),
-               g=R.bloco(s("g"), M, D, blk, espalha=4, e0=-20), h=R.bloco(s("h"), M, FF, blk, espalha=3, e0=-5),
-               gh=R.bloco(s("gh"), M, FF, blk, espalha=3, e0=-25), c=R.cru(s("c"), M, D, bits=24, e0=-30),
-               lg=R.cru(s("lg"), M, V, bits=22, e0=-20), w=R.bloco(s("w"), D, FF, blk, e0=-9),
+    # activations fp32 N(0, 1) and weights fp32 N(0, 0.02) through de_f32; gradients fp32 normal
+    # at their training scale; raw inputs, momentum and residual as integer recipes (jatai_cuda/teste_ops.py:18-31)
+    flut = dict(x=R.normal32(s("x"), (M, D)), y=R.normal32(s("y"), (M, D)), h=R.normal32(s("h"), (M, FF)),
+                g=R.normal32(s("g"), (M, D), 2.0 ** -12), gh=R.normal32(s("gh"), (M, FF), 2.0 ** -16),
+                w=R.normal32(s("w"), (D, FF), 0.02))
+    ins = dict(c=R.cru(s("c"), M, D, bits=24, e0=-30), lg=R.cru(s("lg"), M, V, bits=22, e0=-20),
                mom=R.bloco(s("mom"), D, FF, blk, e0=-15), res=R.bloco(s("res"), D, FF, blk, e0=-20, zera=0.3),
                gw=R.cru(s("gw"), D, FF, bits=28, e0=-50))
     alvo = R.tokens(s("alvo"), M, V)
     for be in (gpu, cpu):
-        d = {k: tuple(be.dev(v) for v in t) for k, t in ins.items()}
         o = be.ops
+        d = {k: tuple(be.dev(v) for v in t) for k, t in ins.items()}
+        d.update({k: o.de_f32(be.dev(v)) for k, v in flut.items()})
         Y, cache = o.rms(d["x"])
         w = tuple(t.clone() for t in d["w"])
         mom = tuple(t.clone() for t in d["mom"])

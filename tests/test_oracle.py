@@ -433,3 +433,28 @@ def test_largura_de_ds_por_t():
             assert T * ((1 << (dsb + 1)) - 1) * amax >= lim, (T, dsb)
         if T > 32:
             assert dsb <= largura(T - 32), T                  # never wider for a longer sequence
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_de_f32_exato(blk):
+    """The fp32 data path (BASELINE configs 2 and 3: fp32 N(0, 1) activations quantized to blocks): frexp splits
+    every float32 exactly (v 2^e == x, |v| < 2^24), and the oracle's block tensor is the spec's quantization rule
+    applied to those exact values (_quant_exata, exact integer rounding), including zeros, subnormals and values
+    far apart within a block."""
+    ops = OpsOraculo(blk)
+    Rn, C = 16, 4 * blk
+    x = R.normal32(401, (Rn, C))
+    x[0, :blk] = 0.0                                           # a zero block
+    x[1, :5] = np.array([1e-40, -3e-39, 0.0, 2.5e-45, 7.0], np.float32)   # subnormals beside a normal value
+    x[2, :blk] *= np.float32(2.0 ** 60)                        # a block of large values
+    x[3, ::7] = np.float32(1e-30)                              # tiny values among normal ones
+    m, e = np.frexp(x)
+    v = (m.astype(np.float64) * 2.0 ** 24).astype(np.int64)
+    assert np.array_equal(np.ldexp(v.astype(np.float64), (e - 24).astype(np.int64)), x.astype(np.float64))
+    assert np.all(np.abs(v) < 1 << 24)
+    qm, qE = (host(t).astype(np.int64) for t in ops.de_f32(torch.from_numpy(x)))
+    for r in range(Rn):
+        ms, Es = _quant_exata([int(a) for a in v[r]], [int(a) - 24 for a in e[r]], 7, 127, blk)
+        assert list(qm[r]) == ms and list(qE[r]) == Es, f"row {r}"
+    with pytest.raises(ValueError):
+        ops.de_f32(torch.from_numpy(np.full((1, blk), np.inf, np.float32)))
