@@ -413,6 +413,48 @@ def test_atencao_hd64_q_zero_so_alibi():
             assert list(P[h, :, i]) == esperado, (h, i)
 
 
+def test_atencao_hd64_k_um_quente():
+    """Head width 64 with one-hot keys (token j's k is c_j in dimension j % 64 and 0 elsewhere) and every q, k, v block
+    of a head at one exponent, so alignment is exact (a = m << 4): then q.k_j = 256 q_i[j % 64] c_j, and the score
+    is u_ij = rnd(256 q_i[j % 64] c_j, -(eq + ek - log2(64)/2 + 8)) - ((i - j) << (8 - 8h/H)) with eq, ek the
+    exponents minus GA = 4 (round half even, here as exact Fraction rounding); P follows from u by the spec's softmax
+    (exp_int pinned by primitives.json), and o = sum_j P_ij (v_j << 4) at exponent ev - 8. At e_q + e_k = -7 the
+    shift is 10 bits, so half-even rounding and the -(log2 hd)/2 term both decide bits of u."""
+    from fractions import Fraction
+    Bt, T, H, D, blk, GA = 1, 128, 8, 512, 32, 4
+    eqb, ekb, evb = -3, -4, -6
+    q = R.uniform_int(111, (T, D), -127, 127)
+    c = R.uniform_int(112, (T,), 1, 127) * np.where(R.uniform01(113, (T,)) < 0.5, -1, 1)
+    v = R.uniform_int(114, (T, D), -127, 127)
+    m = np.zeros((Bt * T, 3 * D), np.int64)
+    m[:, :D] = q
+    m[:, 2 * D:] = v
+    for h in range(H):
+        for j in range(T):
+            m[j, D + 64 * h + j % 64] = c[j]
+    E = np.empty((Bt * T, 3 * D // blk), np.int64)
+    E[:, :D // blk], E[:, D // blk:2 * D // blk], E[:, 2 * D // blk:] = eqb, ekb, evb
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    (oacc, oe), P = OpsOraculo(blk).atencao((t(m.astype(np.int8)), t(E.astype(np.int8))), Bt, T, H)
+    P, oacc, oe = host(P).reshape(H, T, T), host(oacc).astype(np.int64), host(oe).astype(np.int64)
+    ex = OpsOraculo.prim("exp_int", np.arange(0, 1 << 17))
+    su = -((eqb - GA) + (ekb - GA) - 3 + 8)
+    assert su == 10
+    for h in range(H):
+        incl = 8 - (8 * h) // H
+        for i in (0, 5, 63, 64, 100, 127):
+            u = [round(Fraction(256 * int(q[i, 64 * h + j % 64]) * int(c[j]), 1 << su)) - ((i - j) << incl)
+                 for j in range(i + 1)]
+            mx = max(u)
+            e = [int(ex[mx - x]) >> 3 for x in u]
+            inv = (1 << 28) // sum(e)
+            p = [min((x * inv + (1 << 19)) >> 20, 255) for x in e]
+            assert list(P[h, :, i]) == p + [0] * (T - i - 1), (h, i)
+            for d in (0, 17, 63):
+                o = sum(p[j] * (int(v[j, 64 * h + d]) << GA) for j in range(i + 1))
+                assert oacc[i, 64 * h + d] == o and oe[i, 64 * h + d] == (evb - GA) - 8, (h, i, d)
+
+
 def test_largura_de_ds_por_t():
     """The attention backward shrinks dS to 12 - max(0, ceil(log2 T) - 7) bits past T = 128 (jatai_oracle.cpp
     att_dsbits, the kernels' ds_bits). The spec fixes 12 bits for T <= 128 (ops.py:245-247), where its int32 proof
