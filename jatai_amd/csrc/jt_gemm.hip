@@ -84,33 +84,41 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     int8_t* st_s = reinterpret_cast<int8_t*>(buf);                 // raw exponent bytes: EA rows [BM][nbc], EB rows [BN][nbc]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control
     const int lr = lane & 15, lg = lane >> 4;                       // fragment row/col, k-group
-    const int g = wave / (4 * R), wq = wave % (4 * R), wr = (wq >> 2) * 32, wc = (wq & 3) * 32, tg = tid & (GT - 1);
+    const int g = KS == 1 ? 0 : wave / (4 * R), wq = wave % (4 * R), wr = (wq >> 2) * 32, wc = (wq & 3) * 32, tg = tid & (GT - 1);
     char* meu = buf + (size_t)g * 2 * STAGE;                        // this group's two stage buffers
 
     // stage loads: thread tg of a group moves VB-byte vector tg % 8 of tile rows tg / 8 + BM i, i = 0 .. NL - 1
-    // (rows 0 .. BM - 1 of A, then 128 of B). Vectors past K (a partial last stage) are not loaded.
-    // Addresses: a workgroup-uniform base per BM-row band (A's rows, then B's in 128 / BM bands) plus one 32-bit
-    // lane offset vr K + vc shared by the NL loads (< 128 * 65536 = 2^23), so the loads take a scalar base.
+    // (rows 0 .. BM - 1 of A, then 128 of B), at lane offset (row) K + vc of its band (< 128 * 65536 = 2^23)
     const int vr = tg >> 3, vc = (tg & 7) * VB;
-    const int8_t* src[NL];
-    src[0] = A + (size_t)row0 * K;
-#pragma unroll
-    for (int i = 1; i < NL; i++) src[i] = B + (size_t)(col0 + BM * (i - 1)) * K;
-    const unsigned vofs = (unsigned)(vr * K + vc);
     int4 reg[NL], reg2[NL];                                         // two register sets: loads run two stages ahead
-    // The last stage may extend past K (nb not a multiple of the blocks per stage): its vectors past K re-read the
-    // row's last vector instead (a uniform test; those bytes land in blocks >= nb, which are never computed).
-    auto busca = [&](int st, int4 (&r)[NL]) {
-        int o = st * SK;
-        if (o + SK > K) o = min(o + vc, K - VB) - vc;
-        const unsigned d = vofs + (unsigned)o;
+    // Stage loads through buffer resources of the tile's A rows and B rows (bounds: the tile's own bytes, so no
+    // access leaves them): the stage offset is the scalar operand, the lane offsets stay fixed, and a stage takes no
+    // vector address arithmetic. The last stage may extend past K (nb not a multiple of the blocks per stage): its
+    // vectors past K re-read the row's last vector instead (those bytes land in blocks >= nb, never computed).
+    const auto rsA = __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)row0 * K), (short)0, BM * K, 0x00020000);
+    const auto rsB = __builtin_amdgcn_make_buffer_rsrc((void*)(B + (size_t)col0 * K), (short)0, BN * K, 0x00020000);
+    int voff[NL];
 #pragma unroll
-        for (int i = 0; i < NL; i++) {
-            if constexpr (VB == 16) r[i] = *reinterpret_cast<const int4*>(src[i] + d);
-            else {
-                const int2 t = *reinterpret_cast<const int2*>(src[i] + d);
-                r[i] = make_int4(t.x, t.y, 0, 0);
-            }
+    for (int i = 0; i < NL; i++) voff[i] = (i == 0 ? vr : BM * (i - 1) + vr) * K + vc;
+    auto carrega = [&](int4& r, int i, int vo, int so) {
+        if constexpr (VB == 16) {
+            const v4i t = __builtin_amdgcn_raw_buffer_load_b128(i == 0 ? rsA : rsB, vo, so, 0);
+            r = make_int4(t[0], t[1], t[2], t[3]);
+        } else {
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            const v2i t = __builtin_amdgcn_raw_buffer_load_b64(i == 0 ? rsA : rsB, vo, so, 0);
+            r = make_int4(t[0], t[1], 0, 0);
+        }
+    };
+    auto busca = [&](int st, int4 (&r)[NL]) {
+        const int o = __builtin_amdgcn_readfirstlane(st * SK);
+        if (o + SK <= K) {
+#pragma unroll
+            for (int i = 0; i < NL; i++) carrega(r[i], i, voff[i], o);
+        } else {
+            const int d = min(o + vc, K - VB) - vc;
+#pragma unroll
+            for (int i = 0; i < NL; i++) carrega(r[i], i, voff[i] + d, 0);
         }
     };
     auto guarda = [&](int par, const int4 (&r)[NL]) {
@@ -300,14 +308,14 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         for (int k = 0; k < nk; k += 2) {
             // even k: new loads into reg (its stage is stored), the pending stage k + 1 sits in reg2
             if (k + 2 < nk) busca(gs + (k + 2) * KS, reg);
-            calcula(meu + (k % 2) * STAGE, gs + k * KS);
-            if (k + 1 < nk) guarda((k + 1) % 2, reg2);
+            calcula(meu, gs + k * KS);
+            if (k + 1 < nk) guarda(1, reg2);
             __syncthreads();
             if (k + 1 >= nk) break;
             // odd k + 1: the stage k + 2 loads sit in reg; new loads into reg2
             if (k + 3 < nk) busca(gs + (k + 3) * KS, reg2);
-            calcula(meu + ((k + 1) % 2) * STAGE, gs + (k + 1) * KS);
-            if (k + 2 < nk) guarda((k + 2) % 2, reg);
+            calcula(meu + STAGE, gs + (k + 1) * KS);
+            if (k + 2 < nk) guarda(0, reg);
             __syncthreads();
         }
         // groups with fewer stages still take part in every barrier of the loop above
