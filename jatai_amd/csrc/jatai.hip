@@ -39,7 +39,7 @@ static hipStream_t g_stream = 0;
 static int g_blk = 128;                 // block size of every tensor: 32 or 128
 static int g_alvo_wg = 1024;            // GEMM K-split target: tiles x K-splits per launch
 static int g_gemm_bm = 0;               // GEMM tile rows: 0 = automatic, or 32, 64, 128 forced (jt_gemm_bm)
-static int g_linhas = 1;                // attention query rows per thread at head width 4: 1 or 2 (jt_atencao_linhas)
+static int g_linhas = 0;                // head-width-4 attention layout (jt_atencao_linhas): 1 or 2 query rows per thread, 0 automatic
 static int g_atencao_mfma = 1;          // head width 64: matrix-core attention (1) or the dot2 kernels (0)
 
 static int fim() { return (int)hipGetLastError(); }
@@ -130,7 +130,7 @@ void jt_gemm_split(int alvo) { g_alvo_wg = alvo > 0 ? alvo : 1024; }
 void jt_gemm_bm(int bm) { g_gemm_bm = bm; }
 // jatai_cuda.cu:1091: query rows per thread of the head-width-4 attention, 1 (default) or 2 (rows i and T - 1 - i,
 // which balances the causal work); same bits.
-void jt_atencao_linhas(int n) { g_linhas = n == 2 ? 2 : 1; }
+void jt_atencao_linhas(int n) { g_linhas = n == 1 || n == 2 ? n : 0; }
 // No reference counterpart: selects the matrix-core (1, default) or dot2 (0) attention kernels at head width 64.
 void jt_atencao_mfma(int ligado) { g_atencao_mfma = ligado ? 1 : 0; }
 // jatai_cuda.cu:1087: stochastic rounding of gemm_soma's residual add. A synchronous copy into the device global
@@ -533,11 +533,17 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd == 4) {
-        const int nt = (T / g_linhas + 63) & ~63;        // whole waves; threads without a row only join the reductions
+        if (g_linhas == 0 && T <= 128) {                 // automatic: 4 lanes per query row
+            k_atencao4l<128, 4><<<Bt * H, 512, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P,
+                                                              T, H, D, g_blk, GA, kid);
+            return fim();
+        }
+        const int nl = g_linhas == 2 ? 2 : 1;
+        const int nt = (T / nl + 63) & ~63;              // whole waves; threads without a row only join the reductions
 #define A4(TM, NR) k_atencao4<TM, NR><<<Bt * H, nt, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, \
                                                                     (uint8_t*)P, T, H, D, g_blk, GA, kid)
-        if (T <= 128) { if (g_linhas == 2) A4(128, 2); else A4(128, 1); }
-        else { if (g_linhas == 2) A4(256, 2); else A4(256, 1); }
+        if (T <= 128) { if (nl == 2) A4(128, 2); else A4(128, 1); }
+        else { if (nl == 2) A4(256, 2); else A4(256, 1); }
 #undef A4
         return fim();
     }
@@ -603,9 +609,15 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     const int hd = D / H;
     const int dsb = ds_bits(T);
     if (hd == 4) {
-        const int nt = (T / g_linhas + 63) & ~63;
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
-#define B4(TM, LM) { if (g_linhas == 2) k_atencao4_back<TM, LM, 2><<<Bt * H, nt, 0, g_stream>>>(ARGS); \
+        if (g_linhas == 0 && T <= 128) {                 // automatic: 4 lanes per query row
+            if (limite) k_atencao4l_back<128, 1, 4><<<Bt * H, 512, 0, g_stream>>>(ARGS);
+            else k_atencao4l_back<128, 0, 4><<<Bt * H, 512, 0, g_stream>>>(ARGS);
+            return fim();
+        }
+        const int nl = g_linhas == 2 ? 2 : 1;
+        const int nt = (T / nl + 63) & ~63;
+#define B4(TM, LM) { if (nl == 2) k_atencao4_back<TM, LM, 2><<<Bt * H, nt, 0, g_stream>>>(ARGS); \
                      else k_atencao4_back<TM, LM, 1><<<Bt * H, nt, 0, g_stream>>>(ARGS); }
         if (T <= 128) { if (limite) B4(128, 1) else B4(128, 0) }
         else { if (limite) B4(256, 1) else B4(256, 0) }

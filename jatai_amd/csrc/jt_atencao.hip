@@ -217,3 +217,247 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         }
     }
 }
+
+// ---------------------------------------------------------------------------------------------- LPR lanes per row
+// The same arithmetic with LPR consecutive lanes per query row (T <= TMAX = 128): lane l of row i takes the keys
+// j = l, l + LPR, ... <= i and keeps their per-pair values in registers, so each score, exponential, gP and dS is
+// computed once instead of once per pass; the row's maxima and sums combine across its LPR lanes (integer max and
+// sum: exact in any order). 4 x the threads of one-row-per-thread, and the work of a row split four ways. A wave
+// holds 64 / LPR consecutive rows, so the number of key steps it needs is known per wave (kr rows, kc columns):
+// the unrolled steps past it are skipped by a scalar branch, and the causal half of the pairs costs nothing.
+// NS head slices of 4 columns aligned at once (the alignment of alinha4<1>): thread t < T loads token t's 4 bytes
+// and block exponent of every slice before anything waits, and one workgroup reduction gives all NS head maxima
+struct Fatia4 { const int8_t *m, *E; int ld, col; };
+template <int NS, int NW>
+__device__ __forceinline__ void alinha4n(const Fatia4 (&f)[NS], int blk, int b0, int T, int GA, int (&red)[NS][NW], int (*const (&al)[NS])[4],
+                                         int (&eo)[NS]) {
+    const int t = threadIdx.x;
+    int e[NS], w[NS], mx[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        e[s] = t < T ? (int)f[s].E[(size_t)(b0 + t) * (f[s].ld / blk) + f[s].col / blk] : SEM_TOPO;
+        w[s] = t < T ? *reinterpret_cast<const int*>(f[s].m + (size_t)(b0 + t) * f[s].ld + f[s].col) : 0;
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) mx[s] = g_max<64>(e[s]);
+    if ((t & 63) == 0)
+#pragma unroll
+        for (int s = 0; s < NS; s++) red[s][t >> 6] = mx[s];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        int r = SEM_TOPO;
+#pragma unroll
+        for (int x = 0; x < NW; x++) r = max(r, red[s][x]);
+        if (t < T)
+#pragma unroll
+            for (int d = 0; d < 4; d++) al[s][t][d] = rnd_d(((w[s] << (24 - 8 * d)) >> 24) << GA, r - e[s]);
+        eo[s] = r - GA;
+    }
+}
+
+template <int TMAX, int LPR>
+__global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, int* __restrict__ Oacc,
+                                                          int16_t* __restrict__ Oe, uint8_t* __restrict__ P, int T, int H, int D, int blk,
+                                                          int GA, int kid) {
+    constexpr int NJ = TMAX / LPR, NW = TMAX * LPR / 64;
+    __shared__ int qa[TMAX][4], ka[TMAX][4], va[TMAX][4];
+    __shared__ int red[3][NW];
+    const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
+    int eo[3];
+    {
+        const Fatia4 f[3] = {{qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
+        int (*const al[3])[4] = {qa, ka, va};
+        alinha4n<3, NW>(f, blk, b0, T, GA, red, al, eo);
+    }
+    const int eq = eo[0], ek = eo[1], ev = eo[2];
+    __syncthreads();
+    const int su = -(eq + ek - 1 + 8), incl = 8 - h / 8;
+    const int i = threadIdx.x / LPR, l = threadIdx.x % LPR;
+    const bool ativo = i < T;
+    const int ii = ativo ? i : 0, row = b0 + ii;
+    const long long idx = (long long)row * D + h * 4;
+    const int q0 = qa[ii][0], q1 = qa[ii][1], q2 = qa[ii][2], q3 = qa[ii][3];
+    // key steps of this wave: its last row is min(T, 64 / LPR (w + 1)) - 1
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kr = __builtin_amdgcn_readfirstlane((min(T, (64 / LPR) * (w + 1)) - 1) / LPR + 1);
+    int u[NJ], mx = U_MIN;
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        if (k < kr && ativo && j <= i) {
+            const int sc = q0 * ka[j][0] + q1 * ka[j][1] + q2 * ka[j][2] + q3 * ka[j][3];
+            u[k] = rnd(sc, su, kid, idx) - ((i - j) << incl);
+            mx = max(mx, u[k]);
+        }
+    }
+    mx = g_max<LPR>(mx);
+    int soma = 0;
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        if (k < kr && ativo && j <= i) { u[k] = exp_dif(mx, u[k]) >> 3; soma += u[k]; }
+    }
+    soma = g_sum<LPR>(soma);
+    if (ativo && soma <= 0) {
+        if (l == 0) reporta(E_DIV, kid, idx, soma, mx);
+        soma = 1;
+    }
+    const int inv = (1 << 28) / max(soma, 1);
+    uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
+    int o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        int p = 0;
+        if (k < kr && ativo && j <= i) {
+            p = min((u[k] * inv + (1 << 19)) >> 20, 255);
+#pragma unroll
+            for (int d = 0; d < 4; d++) o[d] += p * va[j][d];
+        }
+        if (ativo && j < T) Pb[(size_t)j * T + i] = (uint8_t)p;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++) o[d] = g_sum<LPR>(o[d]);
+    if (!ativo || l != 0) return;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const size_t x = (size_t)row * D + h * 4 + d;
+        if (o[d] >= LIM || o[d] <= -LIM) reporta(E_ACUM, kid, x, o[d], -3);
+        Oacc[x] = o[d];
+        Oe[x] = (int16_t)(ev - 8);
+    }
+}
+
+// Backward with LPR lanes per row. Rows: lane l of row i keeps gP'_ij, P_ij and then dS_ij for its keys in
+// registers and writes dS to LDS ([i][j], int16: |dS| < 2^DSB <= 2^12). Columns: lane l of column j sums over the
+// rows i = j + l, j + l + LPR, ... < T, reading dS from LDS and P from its contiguous stored row.
+template <int TMAX, int LIMITE, int LPR>
+__global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE,
+                                                               const int8_t* __restrict__ qm, const int8_t* __restrict__ qE,
+                                                               const uint8_t* __restrict__ P, int* __restrict__ Gacc, int16_t* __restrict__ Ge,
+                                                               int T, int H, int D, int blk, int GA, int DSB, int kid) {
+    constexpr int NJ = TMAX / LPR, LDS_ = TMAX + 2, NW = TMAX * LPR / 64;
+    __shared__ int goa[TMAX][4], qa[TMAX][4], ka[TMAX][4], va[TMAX][4];
+    __shared__ int16_t dsm[TMAX][LDS_];
+    __shared__ int red[TMAX * LPR / 64];
+    __shared__ int red4[4][NW];
+    const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
+    const uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
+    int eo[4];
+    {
+        const Fatia4 f[4] = {{gom, goE, D, h * 4}, {qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
+        int (*const al[4])[4] = {goa, qa, ka, va};
+        alinha4n<4, NW>(f, blk, b0, T, GA, red4, al, eo);
+    }
+    const int ego = eo[0], eq = eo[1], ek = eo[2], ev = eo[3];
+    __syncthreads();
+    const int i = threadIdx.x / LPR, l = threadIdx.x % LPR;
+    const bool ativo = i < T;
+    const int ii = ativo ? i : 0;
+    const int g0 = goa[ii][0], g1 = goa[ii][1], g2 = goa[ii][2], g3 = goa[ii][3];
+    // key steps of this wave as rows (its last row is min(T, 64 / LPR (w + 1)) - 1) and as columns (its first
+    // column is 64 / LPR w)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kr = __builtin_amdgcn_readfirstlane((min(T, (64 / LPR) * (w + 1)) - 1) / LPR + 1);
+    const int kc = __builtin_amdgcn_readfirstlane(max(T - (64 / LPR) * w, 0) / LPR + 1);
+    // gP_ij = dO_i . v_j and P_ij of the lane's keys
+    int gp[NJ], pp[NJ];
+    int mg = 0;
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        if (k < kr && ativo && j <= i) {
+            gp[k] = g0 * va[j][0] + g1 * va[j][1] + g2 * va[j][2] + g3 * va[j][3];
+            pp[k] = Pb[(size_t)j * T + i];
+            if constexpr (!LIMITE) mg = max(mg, abs(gp[k]));
+        }
+    }
+    // shift of gP: exact causal maximum, or max_i ||dO_i||_inf * max_j ||v_j||_1
+    if constexpr (LIMITE) {
+        const int b1 = ativo ? max(max(abs(g0), abs(g1)), max(abs(g2), abs(g3))) : 0;
+        const int b2 = ativo ? abs(va[i][0]) + abs(va[i][1]) + abs(va[i][2]) + abs(va[i][3]) : 0;
+        mg = bloco_max(b1, red) * bloco_max(b2, red);
+    } else {
+        mg = bloco_max(mg, red);
+    }
+    const int sh = max(bitlen(mg) - 15, 0), egp = ego + ev + sh;
+    // s_i = rnd(sum_j P_ij gP'_ij, 8)
+    int s = 0, pm = 0, gm = 0;
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        if (k < kr && ativo && j <= i) {
+            gp[k] = rnd_d(gp[k], sh);
+            s += pp[k] * gp[k];
+            if constexpr (LIMITE) { pm = max(pm, pp[k]); gm = max(gm, abs(gp[k])); }
+        }
+    }
+    s = g_sum<LPR>(s);
+    if (ativo && l == 0 && (s >= LIM || s <= -LIM)) reporta(E_ACUM, kid, (long long)(b0 + i) * ld + h * 4, s, -4);
+    const int sl = rnd_d(s, 8);
+    // shift of dS: exact maximum of |P (gP' - s)|, or max P * (max |gP'| + max |s|)
+    int md = 0;
+    if constexpr (LIMITE) {
+        const int pmb = bloco_max(pm, red), gmb = bloco_max(gm, red), smb = bloco_max(ativo ? abs(sl) : 0, red);
+        md = pmb * (gmb + smb);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NJ; k++) {
+            const int j = l + LPR * k;
+            if (k < kr && ativo && j <= i) md = max(md, abs(pp[k] * (gp[k] - sl)));
+        }
+        md = bloco_max(md, red);
+    }
+    const int sh2 = max(bitlen(md) - DSB, 0), eds = egp - 9 + sh2;
+    // row i: dS_ij to LDS, gq_i = sum_j dS_ij k_j
+    int gq[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int j = l + LPR * k;
+        if (k < kr && ativo && j <= i) {
+            const int ds = rnd_d(pp[k] * (gp[k] - sl), sh2);
+            dsm[i][j] = (int16_t)ds;
+#pragma unroll
+            for (int d = 0; d < 4; d++) gq[d] += ds * ka[j][d];
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++) gq[d] = g_sum<LPR>(gq[d]);
+    if (ativo && l == 0) {
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const size_t o = (size_t)(b0 + i) * ld + h * 4 + d;
+            if (gq[d] >= LIM || gq[d] <= -LIM) reporta(E_ACUM, kid, o, gq[d], -5);
+            Gacc[o] = gq[d];
+            Ge[o] = (int16_t)(eds + ek);
+        }
+    }
+    __syncthreads();                                                 // every dS of the head in LDS
+    // column j = i: gk_j = sum_{r >= j} dS_rj q_r, gv_j = sum_{r >= j} P_rj dO_r (row j of the stored P is contiguous)
+    const int j = ii;
+    const uint8_t* Pr = Pb + (size_t)j * T;
+    int gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < NJ; k++) {
+        const int r = j + l + LPR * k;
+        if (k < kc && ativo && r < T) {
+            const int ds = dsm[r][j], p = Pr[r];
+#pragma unroll
+            for (int d = 0; d < 4; d++) { gk[d] += ds * qa[r][d]; gv[d] += p * goa[r][d]; }
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++) { gk[d] = g_sum<LPR>(gk[d]); gv[d] = g_sum<LPR>(gv[d]); }
+    if (!ativo || l != 0) return;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const size_t o = (size_t)(b0 + j) * ld + h * 4 + d;
+        if (gk[d] >= LIM || gk[d] <= -LIM) reporta(E_ACUM, kid, o + D, gk[d], -5);
+        if (gv[d] >= LIM || gv[d] <= -LIM) reporta(E_ACUM, kid, o + 2 * D, gv[d], -5);
+        Gacc[o + D] = gk[d];
+        Ge[o + D] = (int16_t)(eds + eq);
+        Gacc[o + 2 * D] = gv[d];
+        Ge[o + 2 * D] = (int16_t)(ego - 8);
+    }
+}

@@ -111,24 +111,25 @@ def test_gemm_tile_forcado_k_longo_e_lote(tile_gemm):
 ATENCAO4 = [i for i, (n, _) in enumerate(CASOS) if n.startswith("atencao")]
 
 
+@pytest.mark.parametrize("linhas", [1, 2])
 @pytest.mark.parametrize("blk", [128, 32])
 @pytest.mark.parametrize("i", ATENCAO4, ids=[CASOS[i][0] for i in ATENCAO4])
-def test_caso_atencao_duas_linhas(blk, i):
-    """The reference suite's attention cases with two query rows per thread (jt_atencao_linhas(2), rows i and
-    T - 1 - i; jatai_cuda.cu:1091): the spec's hashes."""
+def test_caso_atencao_duas_linhas(blk, i, linhas):
+    """The reference suite's attention cases with the layouts jt_atencao_linhas forces (jatai_cuda.cu:1091): one
+    query row per thread, and two (rows i and T - 1 - i); the default runs 4 lanes per row. The spec's hashes."""
     from jatai_amd import ops as O
     lib = O.carrega_lib()
-    lib.jt_atencao_linhas(2)
+    lib.jt_atencao_linhas(linhas)
     try:
         test_caso_vs_spec(blk, i)
     finally:
-        lib.jt_atencao_linhas(1)
+        lib.jt_atencao_linhas(0)
 
 
 DOMINIO = CS.casos_dominio()
 
 
-@pytest.mark.parametrize("linhas", [1, 2])
+@pytest.mark.parametrize("linhas", [0, 1, 2])
 @pytest.mark.parametrize("blk", [128, 32])
 @pytest.mark.parametrize("i", range(len(DOMINIO)), ids=[n for n, _ in DOMINIO])
 def test_dominio_vs_spec(blk, i, linhas):
@@ -145,7 +146,7 @@ def test_dominio_vs_spec(blk, i, linhas):
         saida = fn(rec, CS.Gen(R.substream(1000 + i, nome), blk, gpu.dev), gpu)
         torch.cuda.synchronize()
     finally:
-        lib.jt_atencao_linhas(1)
+        lib.jt_atencao_linhas(0)
     if [list(x) for x in rec.log] != [list(x) for x in gold["chamadas"]]:
         cpu = CPU(blk)
         ref = fn(cpu.ops, CS.Gen(R.substream(1000 + i, nome), blk, cpu.dev), cpu)
@@ -153,7 +154,7 @@ def test_dominio_vs_spec(blk, i, linhas):
         pytest.fail(f"{nome} (BLK={blk}) differs from the spec; first difference per output vs the oracle: {difs}")
 
 
-@pytest.mark.parametrize("linhas", [1, 2])
+@pytest.mark.parametrize("linhas", [0, 1, 2])
 @pytest.mark.parametrize("blk", [128, 32])
 @pytest.mark.parametrize("T", [160, 192, 256])
 def test_atencao4_t_longo_vs_oraculo(T, blk, linhas):
@@ -183,7 +184,7 @@ def test_atencao4_t_longo_vs_oraculo(T, blk, linhas):
                 finally:
                     be.limite(old)
         finally:
-            lib.jt_atencao_linhas(1)
+            lib.jt_atencao_linhas(0)
         res[nome] = [host(x) for x in saida]
     for nome, a, b in zip(("oacc", "oe", "P", "gacc", "ge", "gacc limite", "ge limite"), res["gpu"], res["cpu"]):
         d = primeira_diferenca(a, b)
