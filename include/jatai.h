@@ -29,7 +29,7 @@ void jt_gemm_split(int alvo_wg);       /* split-K target workgroup count for raw
 void jt_gemm_bm(int bm);               /* jatai_cuda.cu:1090: GEMM tile rows: 0 automatic (32), 64 or 128 forced (32 forces the
                                         * default); a forced tile that does not divide M falls back to one that does; same bits */
 void jt_atencao_linhas(int n);         /* jatai_cuda.cu:1091: query rows per thread of the head-width-4 attention: 1 or 2 (rows
-                                        * i and T - 1 - i); any other value (0, the default) is automatic: 4 lanes per query row
+                                        * i and T - 1 - i); any other value (0, the default) is automatic: 8 lanes per query row
                                         * up to T = 128, one row per thread beyond; same bits */
 int jt_res_estocastico(int ligado);    /* jatai_cuda.cu:1087: 1 = gemm_soma's residual add rounds stochastically (0 = off, the default) */
 

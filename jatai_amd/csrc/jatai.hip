@@ -533,8 +533,8 @@ int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, in
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd == 4) {
-        if (g_linhas == 0 && T <= 128) {                 // automatic: 4 lanes per query row
-            k_atencao4l<128, 4><<<Bt * H, 512, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P,
+        if (g_linhas == 0 && T <= 128) {                 // automatic: 8 lanes per query row
+            k_atencao4l<128, 8><<<Bt * H, 1024, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, (int*)Oacc, (int16_t*)Oe, (uint8_t*)P,
                                                               T, H, D, g_blk, GA, kid);
             return fim();
         }
@@ -610,9 +610,9 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
     const int dsb = ds_bits(T);
     if (hd == 4) {
 #define ARGS (const int8_t*)gom, (const int8_t*)goE, (const int8_t*)qm, (const int8_t*)qE, (const uint8_t*)P, (int*)Gacc, (int16_t*)Ge, T, H, D, g_blk, GA, dsb, kid
-        if (g_linhas == 0 && T <= 128) {                 // automatic: 4 lanes per query row
-            if (limite) k_atencao4l_back<128, 1, 4><<<Bt * H, 512, 0, g_stream>>>(ARGS);
-            else k_atencao4l_back<128, 0, 4><<<Bt * H, 512, 0, g_stream>>>(ARGS);
+        if (g_linhas == 0 && T <= 128) {                 // automatic: 8 lanes per query row
+            if (limite) k_atencao4l_back<128, 1, 8><<<Bt * H, 1024, 0, g_stream>>>(ARGS);
+            else k_atencao4l_back<128, 0, 8><<<Bt * H, 1024, 0, g_stream>>>(ARGS);
             return fim();
         }
         const int nl = g_linhas == 2 ? 2 : 1;

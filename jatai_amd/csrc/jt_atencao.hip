@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
 // The same arithmetic with LPR consecutive lanes per query row (T <= TMAX = 128): lane l of row i takes the keys
 // j = l, l + LPR, ... <= i and keeps their per-pair values in registers, so each score, exponential, gP and dS is
 // computed once instead of once per pass; the row's maxima and sums combine across its LPR lanes (integer max and
-// sum: exact in any order). 4 x the threads of one-row-per-thread, and the work of a row split four ways. A wave
+// sum: exact in any order). LPR x the threads of one-row-per-thread, and the work of a row split LPR ways. A wave
 // holds 64 / LPR consecutive rows, so the number of key steps it needs is known per wave (kr rows, kc columns):
 // the unrolled steps past it are skipped by a scalar branch, and the causal half of the pairs costs nothing.
 // NS head slices of 4 columns aligned at once (the alignment of alinha4<1>): thread t < T loads token t's 4 bytes

@@ -116,7 +116,7 @@ ATENCAO4 = [i for i, (n, _) in enumerate(CASOS) if n.startswith("atencao")]
 @pytest.mark.parametrize("i", ATENCAO4, ids=[CASOS[i][0] for i in ATENCAO4])
 def test_caso_atencao_duas_linhas(blk, i, linhas):
     """The reference suite's attention cases with the layouts jt_atencao_linhas forces (jatai_cuda.cu:1091): one
-    query row per thread, and two (rows i and T - 1 - i); the default runs 4 lanes per row. The spec's hashes."""
+    query row per thread, and two (rows i and T - 1 - i); the default runs 8 lanes per row. The spec's hashes."""
     from jatai_amd import ops as O
     lib = O.carrega_lib()
     lib.jt_atencao_linhas(linhas)
