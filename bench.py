@@ -727,8 +727,9 @@ def mede_passo(ops, reg, c, steps, warmup, grafo=True):
 def main():
     a = args()
     if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the multi-GPU path is a design "
-              f"(DESIGN.md), not a measured configuration.", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); sharding the step over GPUs is "
+              f"designed (token-parallel, an exact int32 sum of the weight-gradient partials) but not built or measured.",
+              file=sys.stderr)
         sys.exit(2)
     from jatai_amd import ops as O
     from jatai_amd.registro import Registro
