@@ -225,6 +225,19 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
 // sum: exact in any order). LPR x the threads of one-row-per-thread, and the work of a row split LPR ways. A wave
 // holds 64 / LPR consecutive rows, so the number of key steps it needs is known per wave (kr rows, kc columns):
 // the unrolled steps past it are skipped by a scalar branch, and the causal half of the pairs costs nothing.
+// The backward loads the head's whole P ([j][i] as stored) into LDS first with 16-byte accesses (rows 144 bytes
+// apart: 16-byte aligned, and the 8 keys a wave touches at once fall on different banks) instead of reading one
+// byte per pair twice. (The forward stores P a byte per pair: gathering a wave's rows into 8-byte pieces first, or
+// the head's P into LDS behind a workgroup barrier, measured slower.)
+constexpr int PLD = 144;
+// the T x T bytes of global P ([j][i], rows of T) into the LDS copy (rows of PLD), 16 bytes per thread and step
+__device__ __forceinline__ void carrega_p(const uint8_t* __restrict__ Pg, uint8_t (*ps)[PLD], int T) {
+    const int porl = T / 16, n = T * porl;
+    for (int c = threadIdx.x; c < n; c += blockDim.x) {
+        const int r = c / porl, col = (c - r * porl) * 16;
+        *reinterpret_cast<int4*>(&ps[r][col]) = *reinterpret_cast<const int4*>(Pg + (size_t)r * T + col);
+    }
+}
 // NS head slices of 4 columns aligned at once (the alignment of alinha4<1>): thread t < T loads token t's 4 bytes
 // and block exponent of every slice before anything waits, and one workgroup reduction gives all NS head maxima
 struct Fatia4 { const int8_t *m, *E; int ld, col; };
@@ -342,12 +355,14 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
     __shared__ int16_t dsm[TMAX][LDS_];
     __shared__ int red[TMAX * LPR / 64];
     __shared__ int red4[4][NW];
+    __shared__ __align__(16) uint8_t ps[TMAX][PLD];
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     const uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
     int eo[4];
     {
         const Fatia4 f[4] = {{gom, goE, D, h * 4}, {qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
         int (*const al[4])[4] = {goa, qa, ka, va};
+        carrega_p(Pb, ps, T);
         alinha4n<4, NW>(f, blk, b0, T, GA, red4, al, eo);
     }
     const int ego = eo[0], eq = eo[1], ek = eo[2], ev = eo[3];
@@ -369,7 +384,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
             gp[k] = g0 * va[j][0] + g1 * va[j][1] + g2 * va[j][2] + g3 * va[j][3];
-            pp[k] = Pb[(size_t)j * T + i];
+            pp[k] = ps[j][i];
             if constexpr (!LIMITE) mg = max(mg, abs(gp[k]));
         }
     }
@@ -436,7 +451,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
     __syncthreads();                                                 // every dS of the head in LDS
     // column j = i: gk_j = sum_{r >= j} dS_rj q_r, gv_j = sum_{r >= j} P_rj dO_r (row j of the stored P is contiguous)
     const int j = ii;
-    const uint8_t* Pr = Pb + (size_t)j * T;
+    const uint8_t* Pr = ps[j];
     int gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < NJ; k++) {
