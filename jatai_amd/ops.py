@@ -102,8 +102,8 @@ class OpsHip:
         M, K = a.shape
         N = b.shape[0]
         self.reg.exige(b.shape[1] == K, f"{op}: K diferente, A {tuple(a.shape)} x B {tuple(b.shape)}")
-        # K <= 4096 as the reference (ops.py:336-337); beyond it (up to 65536) the kernel walks K in chunks of 4096
-        # and needs K / BLK to be a multiple of 16
+        # K <= 4096 as the reference (ops.py:336-337); beyond it (up to 65536) the kernel walks K in chunks of 2048
+        # values of shift tables, reads the exponent rows with 16-byte loads and so needs K / BLK to be a multiple of 16
         self.reg.exige(M % 32 == 0 and N % 128 == 0 and K % BLK == 0 and 0 < K and (K <= 4096 or (K <= 65536 and (K // BLK) % 16 == 0)),
                        f"{op}: M multiplo de 32, N de 128, K de {BLK} e K <= 4096 (ou K <= 65536 com K/{BLK} multiplo de 16) "
                        f"(M={M}, N={N}, K={K})")

@@ -416,7 +416,7 @@ def test_gemm_k_longo_vs_oraculo(blk, K):
 
 def test_gemm_cru_lote_config5_dw():
     """The weight-gradient GEMMs of a BASELINE config-5 step (K = 16384 tokens) as the step runs them: one grouped
-    launch (gemm_cru_lote -> k_gemm_lote, one K-split, four 4096-value chunks of shift tables) of the layer's five
+    launch (gemm_cru_lote -> k_gemm_lote, one K-split, eight 2048-value chunks of shift tables) of the layer's five
     shapes plus the output and embedding gradients, each equal to the CPU oracle's raw GEMM (ops.py:95-108)."""
     blk, K, D, FF, V = 32, 16384, 512, 2048, 256
     gpu, cpu = GPU(blk), CPU(blk)
