@@ -491,13 +491,24 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 // runs, so a captured graph follows the value set before each replay.
 __device__ int g_res_est = 0;
 
+// Tile of workgroup id in a grid of n workgroups. The dispatcher deals workgroups to the 8 XCDs in turn (id mod 8),
+// each XCD with its own L2. A grid of at most 1024 workgroups is resident at once; there XCD x takes the x-th
+// eighth of the tiles in row-major order, so the column tiles of a row band (which read the same A rows) share one
+// L2 instead of four (at config 4: ReLU^2 GEMM 19.8 -> 18.8 us, residual-add GEMM 16.8 -> 16.4). Larger grids
+// keep the plain order, which measured as fast or faster there. A bijection whenever n is a multiple of 8.
+__device__ __forceinline__ int tile_xcd(int id, int n) {
+    if (n > 1024 || (n & 7)) return id;
+    return (id & 7) * (n >> 3) + (id >> 3);
+}
+
 template <int BLK, int MODO, int KS, int R = 1>
 __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_eu(4))) k_gemm(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                                    const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                                    int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                                    const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M,
                                                    int N, int K, int kid) {
-    gemm_corpo<BLK, MODO, KS, R>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, blockIdx.y * 32 * R, blockIdx.x * gemm::BN,
+    const int nx = gridDim.x, t = tile_xcd(blockIdx.y * nx + blockIdx.x, nx * gridDim.y);
+    gemm_corpo<BLK, MODO, KS, R>(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, kid, (t / nx) * 32 * R, (t % nx) * gemm::BN,
                               Otim{}, 0, 0, MODO == 2 ? g_res_est : 0);
 }
 
