@@ -112,7 +112,8 @@ int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid);
 
 /* ---- causal ALiBi attention (jatai_cuda.cu:1177-1194). Head width D / H = 4, the reference's: T % 32 == 0,
  * T <= 256 (the reference: T <= 128), H <= 64, ALiBi slope 8 - h / 8 (ops.py:208, 475). No reference counterpart:
- * head widths 16, 32, 64 with T % 64 == 0, T <= 512 and slope 8 - 8h / H. */
+ * head widths 16, 32, 64 with T % 64 == 0, T <= 512 and slope 8 - 8h / H. Every attention entry point takes GA, the
+ * guard bits of the aligned values, from 0 to 4 (the spec's is 4, ops.py:20), else hipErrorInvalidValue. */
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid);
 /* no reference counterpart: jt_atencao with a caller workspace of jt_atencao_ws_bytes(Bt, T, H, D) bytes (16-byte
  * aligned); same outputs. At head width 64 on matrix cores (T <= 512) k and v are converted once per (sequence,

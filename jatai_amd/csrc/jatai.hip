@@ -522,14 +522,16 @@ int jt_perda(const void* d_alvo, const void* soma, void* out, int M, int kid) {
 // ---------------------------------------------------------------------------------------------- attention
 // Shapes: head width 4 (the reference's, jatai_cuda.cu:1176-1187 with ops.py:475) takes T a multiple of 32 up to
 // 256 and H <= 64 (the ALiBi schedule 8 - h // 8 of ops.py:208); head widths 16, 32, 64 (no reference
-// counterpart) take T a multiple of 64 up to 512.
-static bool atencao_forma(int Bt, int T, int H, int D) {
-    if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return false;
+// counterpart) take T a multiple of 64 up to 512. GA, the guard bits of the aligned values, is the spec's 4
+// (ops.py:20) or less: every bound the kernels rest on assumes |aligned value| <= 127 << 4 = 2032 (int32 sums,
+// exact f16 values, the 24-bit products, the dS width), as the reference's own int32 bounds do at T <= 128.
+static bool atencao_forma(int Bt, int T, int H, int D, int GA) {
+    if (Bt <= 0 || H <= 0 || T <= 0 || D % H || GA < 0 || GA > 4) return false;
     if (D / H == 4) return T % 32 == 0 && T <= 256 && H <= 64;
     return T % 64 == 0 && T <= 512;
 }
 int jt_atencao(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, int kid) {
-    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA)) return (int)hipErrorInvalidValue;
     if (!alinhados(qm, qE, Oacc, Oe, P)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     if (hd == 4) {
@@ -589,7 +591,7 @@ static int atencao_ws(const void* qm, const void* qE, void* O1, void* O2, void* 
 }
 int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P, int Bt, int T, int H, int D, int GA, void* ws,
                   long long ws_bytes, int kid) {
-    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA)) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, kid);
     return atencao_ws(qm, qE, Oacc, Oe, P, Bt, T, H, D, GA, ws, ws_bytes, false, kid);
 }
@@ -598,13 +600,13 @@ int jt_atencao_ws(const void* qm, const void* qE, void* Oacc, void* Oe, void* P,
 // half a head); hipErrorNotSupported otherwise.
 int jt_atencao_ws_q(const void* qm, const void* qE, void* Om, void* OE, void* P, int Bt, int T, int H, int D, int GA, void* ws,
                     long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
     return atencao_ws(qm, qE, Om, OE, P, Bt, T, H, D, GA, ws, ws_bytes, true, kid);
 }
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
-    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA)) return (int)hipErrorInvalidValue;
     if (!alinhados(gom, goE, qm, qE, P, Gacc, Ge)) return (int)hipErrorInvalidValue;
     const int hd = D / H;
     const int dsb = ds_bits(T);
@@ -703,7 +705,7 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
 }
 int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T,
                        int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
-    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA)) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
     return atencao_back_ws(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, ws, ws_bytes, false, kid);
 }
@@ -738,7 +740,7 @@ extern "C" {
 long long jt_scratch_bytes() { return (long long)SCRATCH_BYTES; }
 int jt_atencao_back_sem_alocar(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt,
                                int T, int H, int D, int GA, int limite, int kid) {
-    if (!atencao_forma(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA)) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma) return jt_atencao_back(gom, goE, qm, qE, P, Gacc, Ge, Bt, T, H, D, GA, limite, kid);
     const long long n = jt_atencao_back_ws_bytes(Bt, T, H, D);
     if (n <= 0 || n > (long long)SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
@@ -752,7 +754,7 @@ int jt_atencao_back_sem_alocar(const void* gom, const void* goE, const void* qm,
 // hipErrorNotSupported otherwise.
 int jt_atencao_back_ws_q(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
                          int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid) {
-    if (Bt <= 0 || H <= 0 || D % H || T % 64 || T <= 0) return (int)hipErrorInvalidValue;
+    if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
     return atencao_back_ws(gom, goE, qm, qE, P, Gm, GE, Bt, T, H, D, GA, limite, ws, ws_bytes, true, kid);
 }

@@ -10,6 +10,9 @@
 // Backward: gP = dO . v^T shrunk to 15 bits by its causal maximum (or an upper bound in the LIMITE variant),
 // s_i = rnd(sum_j P gP, 8), dS = P (gP - s) shrunk to DSB bits, then gq = dS k, gk = dS^T q, gv = P^T dO
 // as raw outputs [M, 3D].
+// Every product is a 24-bit one (mul24): aligned values |a| <= 128 << GA <= 2048 (GA <= 4), P <= 255, ex <= 4095,
+// 2^28 / sum ex <= 2^16 (the row maximum alone adds 4095 to the sum), |gP'| <= 2^15, |gP' - s| < 2^17 (a row of P
+// sums to at most 256 + T / 2), |dS| <= 2^12.
 #include "jt_comum.h"
 
 __device__ __forceinline__ int bloco_max(int v, int* red) {
@@ -75,7 +78,7 @@ __global__ void __launch_bounds__(TMAX) k_atencao4(const int8_t* __restrict__ qm
         const int q0 = qa[i][0], q1 = qa[i][1], q2 = qa[i][2], q3 = qa[i][3];
         const long long idx = (long long)row * D + h * 4;
         auto sc = [&](int j) {
-            const int s = q0 * ka[j][0] + q1 * ka[j][1] + q2 * ka[j][2] + q3 * ka[j][3];
+            const int s = mul24(q0, ka[j][0]) + mul24(q1, ka[j][1]) + mul24(q2, ka[j][2]) + mul24(q3, ka[j][3]);
             return rnd(s, su, kid, idx) - ((i - j) << incl);
         };
         int mx = U_MIN;
@@ -89,9 +92,9 @@ __global__ void __launch_bounds__(TMAX) k_atencao4(const int8_t* __restrict__ qm
             int p = 0;
             if (j <= i) {
                 const int ex = exp_dif(mx, sc(j)) >> 3;
-                p = min((ex * inv + (1 << 19)) >> 20, 255);
+                p = min((mul24(ex, inv) + (1 << 19)) >> 20, 255);
 #pragma unroll
-                for (int d = 0; d < 4; d++) o[d] += p * va[j][d];
+                for (int d = 0; d < 4; d++) o[d] += mul24(p, va[j][d]);
             }
             Pb[(size_t)j * T + i] = (uint8_t)p;
         }
@@ -124,7 +127,9 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
     int lin[NR];
 #pragma unroll
     for (int k = 0; k < NR; k++) lin[k] = linha_de<NR>(threadIdx.x, k, T);
-    auto gp_ij = [&](int i, int j) { return goa[i][0] * va[j][0] + goa[i][1] * va[j][1] + goa[i][2] * va[j][2] + goa[i][3] * va[j][3]; };
+    auto gp_ij = [&](int i, int j) {
+        return mul24(goa[i][0], va[j][0]) + mul24(goa[i][1], va[j][1]) + mul24(goa[i][2], va[j][2]) + mul24(goa[i][3], va[j][3]);
+    };
     // shift of gP: exact causal maximum, or max_i ||dO_i||_inf * max_j ||v_j||_1
     int mg = 0;
     if constexpr (LIMITE) {
@@ -152,7 +157,7 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         int s = 0;
         for (int j = 0; j <= i; j++) {
             const int p = Pb[(size_t)j * T + i], gp = rnd_d(gp_ij(i, j), sh);
-            s += p * gp;
+            s += mul24(p, gp);
             if constexpr (LIMITE) { pm = max(pm, p); gm = max(gm, abs(gp)); }
         }
         if (s >= LIM || s <= -LIM) reporta(E_ACUM, kid, (long long)(b0 + i) * ld + h * 4, s, -4);
@@ -170,7 +175,7 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
     } else {
 #pragma unroll
         for (int k = 0; k < NR; k++)
-            for (int j = 0; j <= lin[k]; j++) md = max(md, abs((int)Pb[(size_t)j * T + lin[k]] * (rnd_d(gp_ij(lin[k], j), sh) - sl[k])));
+            for (int j = 0; j <= lin[k]; j++) md = max(md, abs(mul24((int)Pb[(size_t)j * T + lin[k]], rnd_d(gp_ij(lin[k], j), sh) - sl[k])));
         md = bloco_max(md, red);                                   // also publishes slin
     }
     const int sh2 = max(bitlen(md) - DSB, 0), eds = egp - 9 + sh2;
@@ -182,9 +187,9 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         // row i: gq_i = sum_j dS_ij k_j
         int gq[4] = {0, 0, 0, 0};
         for (int j = 0; j <= i; j++) {
-            const int ds = rnd_d((int)Pb[(size_t)j * T + i] * (rnd_d(gp_ij(i, j), sh) - sl[k]), sh2);
+            const int ds = rnd_d(mul24((int)Pb[(size_t)j * T + i], rnd_d(gp_ij(i, j), sh) - sl[k]), sh2);
 #pragma unroll
-            for (int d = 0; d < 4; d++) gq[d] += ds * ka[j][d];
+            for (int d = 0; d < 4; d++) gq[d] += mul24(ds, ka[j][d]);
         }
 #pragma unroll
         for (int d = 0; d < 4; d++) {
@@ -200,10 +205,10 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
         int gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0};
         for (int ii = jj; ii < T; ii++) {
             const int p = Pr[ii];
-            const int gp = goa[ii][0] * v0 + goa[ii][1] * v1 + goa[ii][2] * v2 + goa[ii][3] * v3;
-            const int ds = rnd_d(p * (rnd_d(gp, sh) - slin[ii]), sh2);
+            const int gp = mul24(goa[ii][0], v0) + mul24(goa[ii][1], v1) + mul24(goa[ii][2], v2) + mul24(goa[ii][3], v3);
+            const int ds = rnd_d(mul24(p, rnd_d(gp, sh) - slin[ii]), sh2);
 #pragma unroll
-            for (int d = 0; d < 4; d++) { gk[d] += ds * qa[ii][d]; gv[d] += p * goa[ii][d]; }
+            for (int d = 0; d < 4; d++) { gk[d] += mul24(ds, qa[ii][d]); gv[d] += mul24(p, goa[ii][d]); }
         }
 #pragma unroll
         for (int d = 0; d < 4; d++) {
@@ -299,7 +304,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     for (int k = 0; k < NJ; k++) {
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
-            const int sc = q0 * ka[j][0] + q1 * ka[j][1] + q2 * ka[j][2] + q3 * ka[j][3];
+            const int sc = mul24(q0, ka[j][0]) + mul24(q1, ka[j][1]) + mul24(q2, ka[j][2]) + mul24(q3, ka[j][3]);
             u[k] = rnd(sc, su, kid, idx) - ((i - j) << incl);
             mx = max(mx, u[k]);
         }
@@ -324,9 +329,9 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
         const int j = l + LPR * k;
         int p = 0;
         if (k < kr && ativo && j <= i) {
-            p = min((u[k] * inv + (1 << 19)) >> 20, 255);
+            p = min((mul24(u[k], inv) + (1 << 19)) >> 20, 255);
 #pragma unroll
-            for (int d = 0; d < 4; d++) o[d] += p * va[j][d];
+            for (int d = 0; d < 4; d++) o[d] += mul24(p, va[j][d]);
         }
         if (ativo && j < T) Pb[(size_t)j * T + i] = (uint8_t)p;
     }
@@ -383,7 +388,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
     for (int k = 0; k < NJ; k++) {
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
-            gp[k] = g0 * va[j][0] + g1 * va[j][1] + g2 * va[j][2] + g3 * va[j][3];
+            gp[k] = mul24(g0, va[j][0]) + mul24(g1, va[j][1]) + mul24(g2, va[j][2]) + mul24(g3, va[j][3]);
             pp[k] = ps[j][i];
             if constexpr (!LIMITE) mg = max(mg, abs(gp[k]));
         }
@@ -404,7 +409,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
             gp[k] = rnd_d(gp[k], sh);
-            s += pp[k] * gp[k];
+            s += mul24(pp[k], gp[k]);
             if constexpr (LIMITE) { pm = max(pm, pp[k]); gm = max(gm, abs(gp[k])); }
         }
     }
@@ -420,7 +425,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
 #pragma unroll
         for (int k = 0; k < NJ; k++) {
             const int j = l + LPR * k;
-            if (k < kr && ativo && j <= i) md = max(md, abs(pp[k] * (gp[k] - sl)));
+            if (k < kr && ativo && j <= i) md = max(md, abs(mul24(pp[k], gp[k] - sl)));
         }
         md = bloco_max(md, red);
     }
@@ -431,10 +436,10 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
     for (int k = 0; k < NJ; k++) {
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
-            const int ds = rnd_d(pp[k] * (gp[k] - sl), sh2);
+            const int ds = rnd_d(mul24(pp[k], gp[k] - sl), sh2);
             dsm[i][j] = (int16_t)ds;
 #pragma unroll
-            for (int d = 0; d < 4; d++) gq[d] += ds * ka[j][d];
+            for (int d = 0; d < 4; d++) gq[d] += mul24(ds, ka[j][d]);
         }
     }
 #pragma unroll
@@ -459,7 +464,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
         if (k < kc && ativo && r < T) {
             const int ds = dsm[r][j], p = Pr[r];
 #pragma unroll
-            for (int d = 0; d < 4; d++) { gk[d] += ds * qa[r][d]; gv[d] += p * goa[r][d]; }
+            for (int d = 0; d < 4; d++) { gk[d] += mul24(ds, qa[r][d]); gv[d] += mul24(p, goa[r][d]); }
         }
     }
 #pragma unroll

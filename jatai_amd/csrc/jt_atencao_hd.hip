@@ -17,6 +17,8 @@
 // (2) s_i = rnd(sum_j P gP', 8) and partial maxima of |dS| (or its bound terms), (3) gq for the block's query
 // rows and gk, gv for its key rows, (4) the exponent columns. The partial maxima and s_i live, between
 // launches, in the op's own output: the exponent area of the gv columns, which launch (4) writes last.
+// The scalar products are 24-bit ones (mul24): P <= 255, ex <= 4095 and 2^28 / sum ex <= 2^16 (the row maximum
+// alone adds 4095 to the sum), |gP' - s| < 2^17 (|gP'| <= 2^15, a row of P sums to at most 256 + T / 2).
 #include "jt_comum.h"
 
 typedef short s2_t __attribute__((ext_vector_type(2)));
@@ -131,7 +133,7 @@ __global__ void __launch_bounds__(hd::NT) k_atencao_hd(const int8_t* __restrict_
     for (int k = 0; k < DL; k++) o[k] = 0;
     uint8_t* Pb = P + (size_t)bh * T * T;
     for (int j = 0; j <= i; j++) {
-        const int p = min(((exp_dif(mx, u_ij(j)) >> 3) * inv + (1 << 19)) >> 20, 255);
+        const int p = min((mul24(exp_dif(mx, u_ij(j)) >> 3, inv) + (1 << 19)) >> 20, 255);
         if (r == 0) Pb[(size_t)j * T + i] = (uint8_t)p;
         const int* vr = va + j * (HD / 2) + r * W;
 #pragma unroll
@@ -390,7 +392,7 @@ __global__ void __launch_bounds__(hd::NT) k_atb_grad(const int8_t* __restrict__ 
 #pragma unroll
             for (int k = 0; k < W; k++) s = dot2(gi[k], vreg[k], s);
             const int p = Pr[i];
-            const int ds = rnd_d(p * (rnd_d(quad_soma(s), sh) - slin[il]), sh2);
+            const int ds = rnd_d(mul24(p, rnd_d(quad_soma(s), sh) - slin[il]), sh2);
             const int* qi = qa + il * (HD / 2) + r * W;
 #pragma unroll
             for (int k = 0; k < W; k++) {
@@ -565,7 +567,7 @@ __global__ void __launch_bounds__(256) k_atencao_mf(const int8_t* __restrict__ q
         unsigned pk = 0;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int p = min((uu[t][v] * inv[v] + (1 << 19)) >> 20, 255);
+            const int p = min((mul24(uu[t][v], inv[v]) + (1 << 19)) >> 20, 255);
             pk |= (unsigned)p << (8 * v);
             pw[(size_t)(4 * lg + v) * Tk + j] = (_Float16)p;
         }
@@ -764,7 +766,7 @@ __global__ void __launch_bounds__(256) k_atb_mf_linhas(const int8_t* __restrict_
         for (int t = 0; t < NTT; t++) {
             if (t >= ntk) continue;
 #pragma unroll
-            for (int v = 0; v < 4; v++) md = max(md, abs((int)((pr[t] >> (8 * v)) & 255) * (g[t][v] - sl[v])));
+            for (int v = 0; v < 4; v++) md = max(md, abs(mul24((int)((pr[t] >> (8 * v)) & 255), g[t][v] - sl[v])));
         }
         md = wg_max(md, red);
         if (tid == 0) slq[3] = md;
@@ -820,7 +822,7 @@ __global__ void __launch_bounds__(256) k_atb_mf_gq(const int8_t* __restrict__ go
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int p = (pr >> (8 * v)) & 255;
-            const int ds = j <= i0 + v ? rnd_d(p * (rnd_d(o[v], sh) - sl[v]), sh2) : 0;
+            const int ds = j <= i0 + v ? rnd_d(mul24(p, rnd_d(o[v], sh) - sl[v]), sh2) : 0;
             dw[(size_t)(4 * lg + v) * Tk + j] = (short)ds;
         }
     }
@@ -910,7 +912,7 @@ __global__ void __launch_bounds__(256) k_atb_mf_gkv(const int8_t* __restrict__ g
         for (int v = 0; v < 4; v++) {
             const int j = jr + v;
             const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
-            const int ds = i >= j ? rnd_d(p * (rnd_d(o[v], sh) - sl), sh2) : 0;
+            const int ds = i >= j ? rnd_d(mul24(p, rnd_d(o[v], sh) - sl), sh2) : 0;
             dw[(size_t)(4 * lg + v) * nq + il] = (short)ds;
             pww[(size_t)(4 * lg + v) * nq + il] = (uint8_t)p;
         }

@@ -11,6 +11,8 @@
 //       four partial outputs are added in fp32: every partial and their sum are integers below 2^20 (P <= 255,
 //       |v| <= 2032, a row of P sums to at most 256 + T/2), so the sum is exact and equals the one-pass result.
 // 4096 waves at config 4 (4 per SIMD) instead of 1024, each with a quarter of the serial score/softmax chain.
+// The scalar products are 24-bit ones (mul24): P <= 255, ex <= 4095 and 2^28 / sum ex <= 2^16 (the row maximum
+// alone adds 4095 to the sum), |gP'| <= 2^15 and |gP' - s| < 2^17 (a row of P sums to at most 256 + T / 2).
 #include "jt_comum.h"
 
 constexpr size_t cmax_(size_t a, size_t b) { return a > b ? a : b; }
@@ -249,7 +251,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
         unsigned pk = 0;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int p = min((uu[n][v] * inv[v] + (1 << 19)) >> 20, 255);
+            const int p = min((mul24(uu[n][v], inv[v]) + (1 << 19)) >> 20, 255);
             pk |= (unsigned)p << (8 * v);
             pw[wv][4 * lg + v][16 * n + lr] = (_Float16)p;
         }
@@ -543,7 +545,7 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
             const int xv = j <= i0 + v ? dsh(o[v]) : 0;
             const int p = (pr[n] >> (8 * v)) & 255;
             x[n][v] = xv;
-            s[v] += p * xv;
+            s[v] += mul24(p, xv);
             if (LIMITE) { pm = max(pm, p); gm = max(gm, abs(xv)); }
         }
     }
@@ -572,7 +574,7 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
         for (int n = 0; n < NTW; n++) {
             if (n >= nv) continue;
 #pragma unroll
-            for (int v = 0; v < 4; v++) md = max(md, abs((int)((pr[n] >> (8 * v)) & 255) * (x[n][v] - sl[v])));
+            for (int v = 0; v < 4; v++) md = max(md, abs(mul24((int)((pr[n] >> (8 * v)) & 255), x[n][v] - sl[v])));
         }
         md = wg_max4(md, red);
         if (tid == 0) w.p2a[bh * atw::SLOTS + qt] = md;
@@ -639,7 +641,7 @@ __device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __r
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int p = (pr >> (8 * v)) & 255;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? dsh2(p * (dsh(o[v]) - sl[v])) : 0);
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? dsh2(mul24(p, dsh(o[v]) - sl[v])) : 0);
         }
     }
     if (nv & 1)
@@ -735,7 +737,7 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
         for (int v = 0; v < 4; v++) {
             const int j = jr + v;
             const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? dsh2(p * (dsh(o[v]) - sl)) : 0);
+            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? dsh2(mul24(p, dsh(o[v]) - sl)) : 0);
             pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)p;
         }
     }

@@ -58,14 +58,20 @@ __device__ __forceinline__ int shl(int x, int s) { return (int)((unsigned)x << s
 // x * 2^-s for either sign of s where a left shift provably keeps every bit (no check)
 __device__ __forceinline__ int desloca(int x, int s) { return s >= 0 ? rnd_d(x, s) : shl(x, min(-s, 31)); }
 
-// exp(-d/256) in Q15 for d >= 0: shift plus a cubic (ops.py:75-81)
+// a * b for -2^23 <= a, b < 2^23: the low 32 bits of the product, which is what a * b gives, from the full-rate
+// 24-bit multiply (v_mul_i32_i24, and v_mad_i32_i24 when added) instead of the quarter-rate 32-bit one the
+// compiler emits when it cannot bound the operands. Each use states why its operands lie in that range.
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+
+// exp(-d/256) in Q15 for d >= 0: shift plus a cubic (ops.py:75-81). Every product is a 24-bit one: min(d, 6000)
+// and 23637 are below 2^15, f < 2^15, and p stays within (-2^15, 2^15) through the three steps.
 __device__ __forceinline__ int exp_int(int d) {
-    int t = min(d, 6000) * 23637;
+    int t = mul24(min(d, 6000), 23637);
     int n = t >> 22, f = (t & ((1 << 22) - 1)) >> 7;
     int p = -1295;
-    p = ((p * f) >> 15) + 7556;
-    p = ((p * f) >> 15) - 22645;
-    p = ((p * f) >> 15) + 32765;
+    p = (mul24(p, f) >> 15) + 7556;
+    p = (mul24(p, f) >> 15) - 22645;
+    p = (mul24(p, f) >> 15) + 32765;
     return n > 30 ? 0 : p >> n;
 }
 // exp(-(mx - u)/256) with the difference clamped before subtracting (mx - u may exceed 2^31)

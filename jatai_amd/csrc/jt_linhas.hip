@@ -36,7 +36,7 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
     const int r = isqrt_i(ss >> log2D), k = bitlen(r) + 10, inv = div_exata(1 << k, r);
     int v[VPR], q[VPR];
 #pragma unroll
-    for (int i = 0; i < VPR; i++) v[i] = x[i] * inv;            // |v| < 2^18, one exponent per block
+    for (int i = 0; i < VPR; i++) v[i] = mul24(x[i], inv);      // |v| < 2^18, one exponent per block
     const int Eo = quant8_u<VPR, LPB>(v, eb - k - emax + G / 2, q, kid, o);
     if (!ativo) return;
     grava_q8(Ym + o, q);
@@ -100,11 +100,11 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
     int v[VPR], ee[VPR];
 #pragma unroll
     for (int i = 0; i < VPR; i++) {
-        int dentro = dg(g[i]) - dy(y[i] * S);
+        int dentro = dg(g[i]) - dy(mul24(y[i], S));                  // |S| <= 2^15
         const unsigned ad = (unsigned)(dentro < 0 ? -dentro : dentro);
         const int sh2 = max(32 - (int)__clz((int)ad) - 18, 0);     // bitlen(dentro) - 18
         dentro = desl_f(dentro, sh2);
-        v[i] = dentro * inv;
+        v[i] = mul24(dentro, inv);                                  // |dentro| < 2^18, inv <= 2^11
         ee[i] = ec + sh2 - k - (emax - G / 2);
     }
     int8_t q[VPR];
