@@ -53,6 +53,11 @@ int jt_gemm_tile(int M, int N, int modo);              /* no reference counterpa
                                                         * uses for a shape and mode */
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
             int M, int N, int K, int modo, int kid);
+/* no reference counterpart: Z16 = soma16(X16, A.B^T) (R16, int16 mantissas) and Y8 = para8(Z16) in one launch, the
+ * bits of jt_gemm (modo 0), jt_soma16 and jt_para8 in turn (the R16 step's residual add, modelo.py:67-72, 78-84).
+ * X16, Z16 int16 [M,N]; XE, ZE, YE8 int8 [M,N/BLK]; Y8 int8 [M,N]. Shapes as jt_gemm_f. */
+int jt_gemm_soma16(const void* A, const void* EA, const void* B, const void* EB, const void* X16, const void* XE, void* Z16,
+                   void* ZE, void* Y8, void* YE8, int M, int N, int K, int kid);
 
 /* ---- no reference counterpart: n raw-output GEMMs sharing K, in launches of up to 64. `entradas` is a HOST array of
  * n entries {const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad;} (device pointers inside); entry i
@@ -104,6 +109,12 @@ int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, 
 /* no reference counterpart: om = soma(x, rms_back(g, y, cache)) in one launch (kid: rms_back part, kid + 1: soma) */
 int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, const void* xm,
                      const void* xE, void* om, void* oE, int M, int D, int log2D, int G, int GB, int kid);
+/* no reference counterpart: z16 = soma16(x16, rms_back(g, y, cache)) and y8 = para8(z16) in one launch (the R16
+ * backward's residual update, modelo.py:114-130), the bits of jt_rms_back, jt_soma16 and jt_para8 in turn (launch
+ * ids kid, kid + 1, kid + 2). x16, z16 int16 [M,D]; xE, zE, yE8 int8 [M,D/BLK]; y8 int8 [M,D]. */
+int jt_rms_back_soma16(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax,
+                       const void* x16, const void* xE, void* z16, void* zE, void* y8, void* yE8, int M, int D, int log2D, int G,
+                       int GB, int kid);
 int jt_softmax_ce(const void* acc, const void* e, const void* alvo, void* gm, void* gE, void* d_alvo, void* soma, int M, int V,
                   int log2M, int kid);
 /* no reference counterpart: the loss of modelo.py:93, mean over M rows of d_alvo / 256 + ln(soma / 4096) (int32 rows from

@@ -152,10 +152,12 @@ int jt_bloco_atual() { return g_blk; }
 int jt_gemm_divisoes(int M, int N, int K, int modo) { return gemm_divisoes(M, N, K, modo); }
 // No reference counterpart: the tile rows (32, 64 or 128) jt_gemm_f uses for a shape and mode.
 int jt_gemm_tile(int M, int N, int modo) { return 32 * gemm_r(M, N, modo); }
-int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
-              const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
+}  // extern "C"
+// modes 0-4 (jt_gemm_f) and 6 (jt_gemm_soma16)
+static int gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
+                  const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
     using namespace gemm;
-    if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || !k_ok(K) || modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || !k_ok(K)) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk, r = gemm_r(M, N, modo);
     // mode 4 with Om2: the transposed copy needs a single K-split (BLK = 32 only)
@@ -177,6 +179,7 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
         case 2: LB2(2); break;
         case 3: LB2(3); break;
         case 4: LB2(4); break;
+        case 6: LB2(6); break;
     }
 #undef LB2
 #undef LB4
@@ -186,6 +189,20 @@ int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void
 #undef L
 #undef ARGS
     return fim();
+}
+extern "C" {
+int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, const void* Xm,
+              const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid) {
+    if (modo < 0 || modo > 4) return (int)hipErrorInvalidValue;
+    return gemm_f(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2, M, N, K, modo, kid);
+}
+// No reference counterpart: Z16 = soma16(X16, gemm(A, B)) and Y8 = para8(Z16) in one launch -- the 16-bit residual
+// stream's add (modelo.py:67-72, 78-84) and the INT8 copy the next RMSNorm reads -- with the bits of jt_gemm
+// (mode 0), jt_soma16 and jt_para8 in turn. X16, Z16 int16 [M, N]; XE, ZE, YE8 int8 [M, N / BLK]; Y8 int8 [M, N].
+int jt_gemm_soma16(const void* A, const void* EA, const void* B, const void* EB, const void* X16, const void* XE, void* Z16, void* ZE,
+                   void* Y8, void* YE8, int M, int N, int K, int kid) {
+    if (!X16 || !XE || !Z16 || !ZE || !Y8 || !YE8) return (int)hipErrorInvalidValue;
+    return gemm_f(A, EA, B, EB, Z16, ZE, nullptr, nullptr, X16, XE, Y8, YE8, M, N, K, 6, kid);
 }
 int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce, int M, int N, int K,
             int modo, int kid) {
@@ -479,7 +496,7 @@ int jt_rms_back(const void* gm, const void* gE, const void* ym, const void* yE, 
     if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE)) return (int)hipErrorInvalidValue;
     const bool ok = por_linha(D, [&](auto fm, auto bl) {
         using FM = decltype(fm);
-        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, false, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, 0, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
             (const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym, (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om,
             (int8_t*)oE, M, log2D, G, GB, kid, nullptr, nullptr, 0, D);
     });
@@ -493,9 +510,25 @@ int jt_rms_back_soma(const void* gm, const void* gE, const void* ym, const void*
     if (!alinhados(gm, gE, ym, yE, cr, cemax, om, oE) || !alinhados(xm, xE)) return (int)hipErrorInvalidValue;
     const bool ok = por_linha(D, [&](auto fm, auto bl) {
         using FM = decltype(fm);
-        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, true, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, 1, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
             (const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym, (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)om,
             (int8_t*)oE, M, log2D, G, GB, kid, (const int8_t*)xm, (const int8_t*)xE, kid + 1, D);
+    });
+    return ok ? fim() : (int)hipErrorInvalidValue;
+}
+// No reference counterpart: z16 = soma16(x16, rms_back(g, y, cache)) and y8 = para8(z16) in one launch (the
+// backward's update of the 16-bit residual stream, modelo.py:114-130, and the INT8 copy the next GEMMs read);
+// equals jt_rms_back, jt_soma16 and jt_para8 in turn (launch ids kid, kid + 1, kid + 2). x16, z16 int16 [M, D];
+// xE, zE, yE8 int8 [M, D / BLK]; y8 int8 [M, D].
+int jt_rms_back_soma16(const void* gm, const void* gE, const void* ym, const void* yE, const void* cr, const void* cemax, const void* x16,
+                       const void* xE, void* z16, void* zE, void* y8, void* yE8, int M, int D, int log2D, int G, int GB, int kid) {
+    if (M <= 0 || !x16 || !xE || !z16 || !zE || !y8 || !yE8) return (int)hipErrorInvalidValue;
+    if (!alinhados(gm, gE, ym, yE, cr, cemax, z16, zE) || !alinhados(x16, xE, y8, yE8)) return (int)hipErrorInvalidValue;
+    const bool ok = por_linha(D, [&](auto fm, auto bl) {
+        using FM = decltype(fm);
+        k_rms_back<FM::VP, FM::LP, decltype(bl)::value, 2, FM::CH><<<grade_linhas(M, FM::LP), 256, 0, g_stream>>>(
+            (const int8_t*)gm, (const int8_t*)gE, (const int8_t*)ym, (const int8_t*)yE, (const int*)cr, (const int*)cemax, (int8_t*)z16,
+            (int8_t*)zE, M, log2D, G, GB, kid, (const int8_t*)x16, (const int8_t*)xE, kid + 1, D, (int8_t*)y8, (int8_t*)yE8);
     });
     return ok ? fim() : (int)hipErrorInvalidValue;
 }

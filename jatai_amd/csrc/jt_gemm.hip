@@ -22,7 +22,7 @@
 // order). The summed tile is then read in a row-block layout (16 consecutive columns per lane) where the block
 // quantization and the fused epilogues run:
 //   MODO 0 block output | 1 raw output | 2 + residual add (soma) | 3 + ReLU^2 second output
-//   4 ReLU^2 backward with H
+//   4 ReLU^2 backward with H | 6 + 16-bit residual add (soma16) and its INT8 copy (para8)
 // The fused epilogues compute exactly the separate ops on the quantized GEMM output (jatai_cuda.cu:195-200).
 #include "jt_comum.h"
 
@@ -346,6 +346,9 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     if constexpr (MODO == 2 || MODO == 4) {
         if (tid < GT) { le_i8(Xm + o, xin); exin = XE[oe]; }
     }
+    if constexpr (MODO == 6) {                                     // the R16 residual (int16 mantissas)
+        if (tid < GT) { le_i16(reinterpret_cast<const int16_t*>(Xm) + o, xin); exin = XE[oe]; }
+    }
     int base[16];
     if (tid < GT) {
         const int ra = ra_s[orow];
@@ -421,6 +424,28 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             if (Ea > 126 && lider) reporta(E_EXP, kid, (long long)o, Ea, -7);
             grava_i8(Om2 + o, q);
             if (lider) OE2[oe] = (int8_t)Ea;
+        }
+        if constexpr (MODO == 6) {
+            // z16 = soma16(X16, C) (jatai_cuda.cu:514-531: ec = max(xE + 15, E + 7) - 28, zero blocks add 0, a
+            // 15-bit block quantization) into Cm (int16 mantissas) and CE, then y8 = para8(z16) (jatai_cuda.cu:
+            // 501-513) into Om2, OE2: what jt_soma16 and jt_para8 compute from the stored tensors. The exponents
+            // are taken as stored (int8), so even an out-of-range one gives the separate launches' bits.
+            const int ey = (int)(int8_t)E, ec = max(exin + 15, ey + 7) - 28;
+            const Desl dx(ec - exin), dm(ec - ey);                 // left shifts keep |values| below 2^28
+            const int mx = exin == E_ZERO ? 0 : -1, mm = ey == E_ZERO ? 0 : -1;
+            int s[16], q[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) s[j] = (dx(xin[j]) & mx) + (dm((int)m[j]) & mm);
+            const int Ez = quant_u<16, LPB, true, 15, 32767>(s, ec, q, kid, (long long)o);
+            int16_t z[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) z[j] = (int16_t)q[j];
+            grava_i16(reinterpret_cast<int16_t*>(Cm) + o, z);
+            if (lider) CE[oe] = (int8_t)Ez;
+            int8_t y[16];
+            const int Ey = quant8_u8<16, LPB>(q, (int)(int8_t)Ez, y, kid, (long long)o);
+            grava_i8(Om2 + o, y);
+            if (lider) OE2[oe] = (int8_t)Ey;
         }
         if constexpr (MODO == 2) {                                 // z = soma(X, C): ec = max(xE, E) - 21
             int s[16];

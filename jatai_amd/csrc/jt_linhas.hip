@@ -49,12 +49,14 @@ __global__ void __launch_bounds__(256) k_rms(const int8_t* __restrict__ Xm, cons
 // The block-uniform alignments run through Desl: |g y| << GB < 2^21 shifts right, g shifts left by at most 21
 // (ec >= eg + 7 - 28) and y S by at most 6 (|S| <= 2^15, ec >= ey + eS + 22 - 28), so every value stays below 2^28
 // and the spec's left-shift checks cannot fire. Every load (x included) is issued before the first reduction.
-template <int VPR, int LPR, int BLK, bool SOMA = false, bool CHEIO = true>
+// SOMA = 2: x is the 16-bit residual stream (int16 mantissas): om (int16), oE get z16 = soma16(x16, dx)
+// (jatai_cuda.cu:514-531) and om2, oE2 its INT8 copy para8(z16) (jatai_cuda.cu:501-513), launch ids kid2, kid2 + 1.
+template <int VPR, int LPR, int BLK, int SOMA = 0, bool CHEIO = true>
 __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm, const int8_t* __restrict__ gE, const int8_t* __restrict__ ym,
                                                   const int8_t* __restrict__ yE, const int* __restrict__ cr, const int* __restrict__ cemax,
                                                   int8_t* __restrict__ om, int8_t* __restrict__ oE, int M, int log2D, int G, int GB, int kid,
                                                   const int8_t* __restrict__ xm = nullptr, const int8_t* __restrict__ xE = nullptr, int kid2 = 0,
-                                                  int Dr = 0) {
+                                                  int Dr = 0, int8_t* __restrict__ om2 = nullptr, int8_t* __restrict__ oE2 = nullptr) {
     constexpr int LPB = BLK / VPR;
     const int D = CHEIO ? VPR * LPR : Dr, nb = D / BLK;
     const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, lr = threadIdx.x % LPR;
@@ -74,9 +76,10 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
         for (int i = 0; i < VPR; i++) g[i] = y[i] = 0;
     }
     const int r = cr[row], emax = cemax[row];
-    if constexpr (SOMA) {
+    if constexpr (SOMA != 0) {
         if (ativo) {
-            le_i8(xm + o, a);
+            if constexpr (SOMA == 2) le_i16(reinterpret_cast<const int16_t*>(xm) + o, a);
+            else le_i8(xm + o, a);
             ex = xE[(long long)row * nb + b];
         } else {
 #pragma unroll
@@ -109,7 +112,26 @@ __global__ void __launch_bounds__(256) k_rms_back(const int8_t* __restrict__ gm,
     }
     int8_t q[VPR];
     const int Eo = quant8_d<VPR, LPB>(v, ee, q, kid, o);            // |ee| < 600
-    if constexpr (SOMA) {                                            // z = soma(x, dx): ec = max(xE, E) - 21
+    if constexpr (SOMA == 2) {      // z16 = soma16(x16, dx): ec = max(xE + 15, E + 7) - 28; exponents as stored (int8)
+        const int ey = (int)(int8_t)Eo, ec2 = max(ex + 15, ey + 7) - 28;
+        const Desl da(ec2 - ex), dq(ec2 - ey);                       // left shifts keep |values| below 2^28
+        const int ma = ex == E_ZERO ? 0 : -1, mq = ey == E_ZERO ? 0 : -1;
+        int zs[VPR], qz[VPR];
+#pragma unroll
+        for (int i = 0; i < VPR; i++) zs[i] = (da(a[i]) & ma) + (dq((int)q[i]) & mq);
+        const int Ez = quant_u<VPR, LPB, true, 15, 32767>(zs, ec2, qz, kid2, o);
+        int8_t y8[VPR];
+        const int Ey = quant8_u8<VPR, LPB>(qz, (int)(int8_t)Ez, y8, kid2 + 1, o);
+        if (!ativo) return;
+        int16_t z16[VPR];
+#pragma unroll
+        for (int i = 0; i < VPR; i++) z16[i] = (int16_t)qz[i];
+        grava_i16(reinterpret_cast<int16_t*>(om) + o, z16);
+        grava_i8(om2 + o, y8);
+        if ((lr & (LPB - 1)) == 0) { oE[(long long)row * nb + b] = (int8_t)Ez; oE2[(long long)row * nb + b] = (int8_t)Ey; }
+        return;
+    }
+    if constexpr (SOMA == 1) {                                       // z = soma(x, dx): ec = max(xE, E) - 21
         const int ec2 = max(ex, Eo) - 21;
         const Desl da(ec2 - ex), dq(ec2 - Eo);
         int zs[VPR], qz[VPR];

@@ -78,6 +78,9 @@ class Modelo:
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
         # the residual update of the backward, soma(gx, rms_back(...)), in one launch
         self.rms_soma = hasattr(ops, "rms_back_soma")
+        # the R16 step's residual adds, soma16(x16, gemm(...)) and soma16(gx16, rms_back(...)), each with the INT8
+        # copy para8 of its result (what the next RMSNorm or GEMMs read) in one launch
+        self.soma16_fundida = hasattr(ops, "gemm_soma16") and hasattr(ops, "rms_back_soma16")
         # the loss in one launch of the library (float64 sums in another order than torch's mean: equal to 1e-15)
         self.perda_fundida = hasattr(ops, "perda")
         # measurement hook: stage name -> (before, after) callables run around that stage of the step
@@ -105,7 +108,12 @@ class Modelo:
     def passo(self, tok, alvo, k_lr=None):
         """Forward (+ backward and update when k_lr is given). Returns the loss as a tensor on the device."""
         ops, reg, p, r16 = self.ops, self.reg, self.p, self.r16
+        s16 = r16 and self.soma16_fundida
         Bt, T = tok.shape
+        x8 = None                   # R16: the INT8 copy of x16 when a fused launch wrote it
+
+        def oito(x16):              # para8(x16), or the copy already written
+            return x8 if x8 is not None else ops.para8(x16)
         tok, alvo = tok.reshape(-1).to(torch.int32).contiguous(), alvo.reshape(-1).to(torch.int32).contiguous()
         with reg.trecho("forward"):
             with reg.trecho("embedding"):
@@ -116,23 +124,29 @@ class Modelo:
             for l in range(self.L):
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("atencao"):
-                        n1, c1 = ops.rms(ops.para8(x16) if r16 else x)
+                        n1, c1 = ops.rms(oito(x16) if r16 else x)
                         qkv = ops.gemm(n1, p[f"Wqkv{l}"])
                         if self.quant_na_atencao:
                             om, P = ops.atencao_q(qkv, Bt, T, self.H)
                         else:
                             oc, P = ops.atencao(qkv, Bt, T, self.H)
                             om = ops.quant(oc)
-                        if r16:
+                        if s16:
+                            x16, x8 = ops.gemm_soma16(om, p[f"Wo{l}"], x16)
+                            x = x8 if self.estatisticas else None
+                        elif r16:
                             x16 = ops.soma16(x16, ops.gemm(om, p[f"Wo{l}"]))
                             x = ops.para8(x16) if self.estatisticas else None
                         else:
                             x = ops.gemm_soma(om, p[f"Wo{l}"], x)
                         self._st(f"c{l}.qkv", qkv); self._st(f"c{l}.atencao_saida", om); self._st(f"c{l}.residuo1", x)
                     with reg.trecho("mlp"):
-                        n2, c2 = ops.rms(ops.para8(x16) if r16 else x)
+                        n2, c2 = ops.rms(oito(x16) if r16 else x)
                         h, a = ops.gemm_relu2(n2, p[f"Wup{l}"])
-                        if r16:
+                        if s16:
+                            x16, x8 = ops.gemm_soma16(a, p[f"Wd{l}"], x16)
+                            x = x8 if self.estatisticas else None
+                        elif r16:
                             x16 = ops.soma16(x16, ops.gemm(a, p[f"Wd{l}"]))
                             x = ops.para8(x16) if self.estatisticas else None
                         else:
@@ -140,7 +154,7 @@ class Modelo:
                         self._st(f"c{l}.relu2", a, zeros_normais=True); self._st(f"c{l}.residuo2", x)
                 caches.append((n1, c1, qkv, P, om, n2, c2, h, a))
             with reg.trecho("saida"):
-                nf, cf = ops.rms(ops.para8(x16) if r16 else x)
+                nf, cf = ops.rms(oito(x16) if r16 else x)
                 logits = ops.gemm(nf, p["out"], cru=True)
                 g, d_alvo, soma = ops.softmax_ce(logits, alvo)
         perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma, ops if self.perda_fundida else None)
@@ -188,7 +202,9 @@ class Modelo:
                             gh = ops.gemm_relu2_back(gx, T_(p[f"Wd{l}"]), h)
                         grads[f"Wup{l}"] = grad_w(f"Wup{l}", gh, n2)
                         gn = ops.gemm(gh, T_(p[f"Wup{l}"]))
-                        if r16:
+                        if s16:
+                            gx16, gx = ops.rms_back_soma16(gn, n2, c2, gx16)
+                        elif r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n2, c2))
                             gx = ops.para8(gx16)
                         else:
@@ -203,7 +219,9 @@ class Modelo:
                             gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))
                         grads[f"Wqkv{l}"] = grad_w(f"Wqkv{l}", gq, n1)
                         gn = ops.gemm(gq, T_(p[f"Wqkv{l}"]))
-                        if r16:
+                        if s16:
+                            gx16, gx = ops.rms_back_soma16(gn, n1, c1, gx16)
+                        elif r16:
                             gx16 = ops.soma16(gx16, ops.rms_back(gn, n1, c1))
                             gx = ops.para8(gx16)
                         else:

@@ -33,7 +33,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
            "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
-           "jt_rms_back_soma", "jt_perda", "jt_gemm_tile")
+           "jt_rms_back_soma", "jt_perda", "jt_gemm_tile", "jt_gemm_soma16", "jt_rms_back_soma16")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -320,6 +320,20 @@ class OpsHip:
         self.reg.exige(tuple(Y[0].shape) == tuple(X16[0].shape), f"soma16: formas {tuple(X16[0].shape)} e {tuple(Y[0].shape)}")
         return self._r16("soma16", "jt_soma16", (*X16, *Y), dict(x16=X16[0], y=Y[0]), tuple(X16[0].shape), True)
 
+    # no reference counterpart: (soma16(X16, gemm(A, B)), para8 of it) from one launch -- the R16 step's residual add
+    # and the INT8 copy its next RMSNorm reads; the same bits as the three ops in turn
+    def gemm_soma16(self, A, B, X16):
+        reg = self.reg
+        reg.confere_bloco("A", A); reg.confere_bloco("B", B); reg.confere_r16("x16", X16)
+        (a, ea), (b, eb) = A, B
+        M, N, K = self._formas_gemm("gemm_soma16", a, b)
+        reg.exige(tuple(X16[0].shape) == (M, N), f"gemm_soma16: x16 com forma {tuple(X16[0].shape)}, esperado {(M, N)}")
+        Z = (torch.empty(M, N, dtype=torch.int16, device=a.device), torch.empty(M, N // BLK, dtype=torch.int8, device=a.device))
+        Y = self._novo_bloco(M, N, a.device)
+        self._lanca("gemm_soma16", "jt_gemm_soma16", (a, ea, b, eb, X16[0], X16[1], Z[0], Z[1], Y[0], Y[1], M, N, K),
+                    dict(A=a, EA=ea, B=b, EB=eb, x16=X16[0], xE=X16[1]), (M, N))
+        return Z, Y
+
     def relu2(self, Hh):
         return self._elem("relu2", "jt_relu2", (Hh,), ("h",))
 
@@ -382,6 +396,27 @@ class OpsHip:
                                       G, GB, ctypes.c_int(kid))
         self.reg.depois(kid, r)
         return O
+
+    # no reference counterpart: (soma16(X16, rms_back(g, y, cache)), para8 of it) in one launch -- the R16 backward's
+    # residual update and the INT8 copy the next GEMMs read; launch ids: rms_back, soma16, para8
+    def rms_back_soma16(self, Gg, Y, cache, X16):
+        self.reg.confere_bloco("g", Gg); self.reg.confere_bloco("y", Y); self.reg.confere_r16("x16", X16)
+        (g, gE), (y, yE), (x, xE) = Gg, Y, X16
+        M, D = g.shape
+        self.reg.exige(tuple(x.shape) == (M, D), f"rms_back_soma16: x16 com forma {tuple(x.shape)}, esperado {(M, D)}")
+        G, GB = g_rms(D)
+        Z = (torch.empty(M, D, dtype=torch.int16, device=g.device), torch.empty(M, D // BLK, dtype=torch.int8, device=g.device))
+        O = self._novo_bloco(M, D, g.device)
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        kid = self.reg.registra("rms_back", dict(g=g, gE=gE, y=y, yE=yE, r=cache[0], emax=cache[1]), (M, D))
+        self.reg.registra("soma16", dict(x16=x, xE=xE), (M, D), tempo=False)
+        self.reg.registra("para8", dict(), (M, D), tempo=False)
+        r = self.lib.jt_rms_back_soma16(*[self._a(t) for t in (g, gE, y, yE, cache[0], cache[1], x, xE, Z[0], Z[1], O[0], O[1])], M, D,
+                                        int(math.log2(D)), G, GB, ctypes.c_int(kid))
+        self.reg.depois(kid, r)
+        return Z, O
 
     def atencao(self, QKV, Bt, T, H):
         self.reg.confere_bloco("qkv", QKV)

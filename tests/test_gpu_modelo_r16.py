@@ -1,7 +1,8 @@
 """The config-5 architecture at test scale: the training step with the 16-bit residual stream (R16: para16 /
 soma16 / para8 carry the residual, modelo.py:60-130) at the BASELINE widths (D=512, 8 heads x 64, FF=2048, V=256,
 T=256, BLK=32), with 2 layers and 2 sequences. Every op output of the HIP path equals the CPU oracle's; the fused
-step (batched transposes, grouped weight-gradient GEMMs, fused optimizer) leaves the same weights, momenta and
+step (batched transposes, grouped weight-gradient GEMMs, fused optimizer, the residual adds with their INT8 copies
+in the GEMM and rms_back launches) leaves the same weights, momenta and
 residuals; a third step replayed from a captured hipGraph equals the eager op-by-op step.
 
 The R16 ops have no counterpart in the reference's spec (their oracle restates the CUDA kernels,
@@ -31,7 +32,9 @@ def test_passo_r16_vs_oraculo():
         mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg, r16=True)
         mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub(), r16=True)
         mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.rms_soma = mg.perda_fundida = False
+        mg.soma16_fundida = False
         mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg, r16=True)
+        assert mf.soma16_fundida
         for p in range(2):
             x = R.tokens(R.substream(37, f"r16 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
             tok = torch.from_numpy(x[:, :-1].copy()).long()

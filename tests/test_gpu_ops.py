@@ -360,6 +360,51 @@ def test_rms_back_soma(blk, D):
     _compara(o.rms_back_soma(G, Y, cache, X), o.soma(X, o.rms_back(G, Y, cache)), "rms_back_soma")
 
 
+@pytest.mark.parametrize("blk,M,N,K,alvo,bm", [(32, 512, 512, 512, 1024, 0), (32, 512, 512, 512, 1, 0), (32, 256, 512, 2048, 1024, 128),
+                                                 (128, 256, 256, 512, 1024, 0), (32, 2048, 512, 1536, 1024, 64)])
+def test_gemm_soma16(blk, M, N, K, alvo, bm):
+    """soma16(x16, gemm(A, B)) and para8 of the sum in one launch (the R16 step's residual add) equal gemm, soma16
+    and para8 in turn, at one and two K-splits and at forced tiles of 64 and 128 rows; zero blocks on both sides."""
+    gpu = GPU(blk, vigiar=True)
+    s = lambda t: R.substream(94, f"{blk} {M} {N} {K} {t}")
+    A = tuple(gpu.dev(v) for v in R.bloco(s("A"), M, K, blk, espalha=4, e0=-6, zera=0.05))
+    B = tuple(gpu.dev(v) for v in R.bloco(s("B"), N, K, blk, espalha=4, e0=-9))
+    X0 = tuple(gpu.dev(v) for v in R.bloco(s("x0"), M, N, blk, espalha=3, e0=-4, zera=0.05))
+    Y0 = tuple(gpu.dev(v) for v in R.bloco(s("y0"), M, N, blk, espalha=3, e0=-12, zera=0.05))
+    o = gpu.ops
+    X16 = o.soma16(o.para16(X0), Y0)                                 # 15-bit mantissas, zero blocks included
+    try:
+        gpu.ops.lib.jt_gemm_split(alvo)
+        gpu.ops.lib.jt_gemm_bm(bm)
+        Z, Y8 = o.gemm_soma16(A, B, X16)
+        Zr = o.soma16(X16, o.gemm(A, B))
+    finally:
+        gpu.ops.lib.jt_gemm_split(1024)
+        gpu.ops.lib.jt_gemm_bm(0)
+    _compara(Z, Zr, "gemm_soma16: soma16")
+    _compara(Y8, o.para8(Zr), "gemm_soma16: para8")
+
+
+@pytest.mark.parametrize("blk,D", [(32, 512), (128, 256), (32, 768)])
+def test_rms_back_soma16(blk, D):
+    """soma16(x16, rms_back(g, y, cache)) and para8 of the sum in one launch (the R16 backward's residual update)
+    equal rms_back, soma16 and para8 in turn, also at a width that is not a power of two."""
+    gpu = GPU(blk, vigiar=True)
+    M = 512
+    s = lambda t: R.substream(95, f"{blk} {D} {t}")
+    X0 = tuple(gpu.dev(v) for v in R.bloco(s("x0"), M, D, blk, espalha=3, e0=-6))
+    G = tuple(gpu.dev(v) for v in R.bloco(s("g"), M, D, blk, espalha=4, e0=-20))
+    X1 = tuple(gpu.dev(v) for v in R.bloco(s("x1"), M, D, blk, espalha=3, e0=-18, zera=0.05))
+    Y1 = tuple(gpu.dev(v) for v in R.bloco(s("y1"), M, D, blk, espalha=3, e0=-26, zera=0.05))
+    o = gpu.ops
+    Y, cache = o.rms(X0)
+    X16 = o.soma16(o.para16(X1), Y1)
+    Z, Y8 = o.rms_back_soma16(G, Y, cache, X16)
+    Zr = o.soma16(X16, o.rms_back(G, Y, cache))
+    _compara(Z, Zr, "rms_back_soma16: soma16")
+    _compara(Y8, o.para8(Zr), "rms_back_soma16: para8")
+
+
 def test_tabela_otimizador_mantem_tensores():
     """The fused optimizer's device table keeps alive every tensor whose address it holds: built from tensors the
     caller then drops, with torch's allocator cache emptied (as entering graph capture does), the update still

@@ -46,6 +46,7 @@ def roda(ops, reg, dev, passos, host):
     m.quant_na_atencao = False
     m.transposta_na_gemm = False
     m.rms_soma = False
+    m.soma16_fundida = False
     m.perda_fundida = False
     init = {n: [R.sha(host(t[0])), R.sha(host(t[1]))] for n, t in m.p.items()}
     out = []
