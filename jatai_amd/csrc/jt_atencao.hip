@@ -281,16 +281,18 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     constexpr int NJ = TMAX / LPR, NW = TMAX * LPR / 64;
     __shared__ int qa[TMAX][4], ka[TMAX][4], va[TMAX][4];
     __shared__ int red[3][NW];
+    __shared__ __align__(16) unsigned short texp[EXP_N];
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     int eo[3];
     {
         const Fatia4 f[3] = {{qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
         int (*const al[3])[4] = {qa, ka, va};
+        exp_tab_lds(texp);                                           // published by the barriers below
         alinha4n<3, NW>(f, blk, b0, T, GA, red, al, eo);
     }
     const int eq = eo[0], ek = eo[1], ev = eo[2];
     __syncthreads();
-    const int su = -(eq + ek - 1 + 8), incl = 8 - h / 8;
+    const int su = __builtin_amdgcn_readfirstlane(-(eq + ek - 1 + 8)), incl = 8 - h / 8;   // one per head
     const int i = threadIdx.x / LPR, l = threadIdx.x % LPR;
     const bool ativo = i < T;
     const int ii = ativo ? i : 0, row = b0 + ii;
@@ -299,13 +301,19 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     // key steps of this wave: its last row is min(T, 64 / LPR (w + 1)) - 1
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kr = __builtin_amdgcn_readfirstlane((min(T, (64 / LPR) * (w + 1)) - 1) / LPR + 1);
+    // the ALiBi term (i - j) << incl of key j = l + LPR k is ab - k (LPR << incl) (shifts distribute over the
+    // subtraction in 32-bit arithmetic); the score's rounding shift su is one per head: for su >= 0 one FMA (Desl,
+    // exact for |score| < 2^26), a left shift (checked) otherwise
+    const int ab = (ii - l) << incl, pa = LPR << incl;
+    const bool direita = su >= 0;
+    const Desl dsu(su);
     int u[NJ], mx = U_MIN;
 #pragma unroll
     for (int k = 0; k < NJ; k++) {
         const int j = l + LPR * k;
         if (k < kr && ativo && j <= i) {
             const int sc = mul24(q0, ka[j][0]) + mul24(q1, ka[j][1]) + mul24(q2, ka[j][2]) + mul24(q3, ka[j][3]);
-            u[k] = rnd(sc, su, kid, idx) - ((i - j) << incl);
+            u[k] = (direita ? dsu(sc) : rnd(sc, su, kid, idx)) - ab + k * pa;
             mx = max(mx, u[k]);
         }
     }
@@ -314,14 +322,15 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
 #pragma unroll
     for (int k = 0; k < NJ; k++) {
         const int j = l + LPR * k;
-        if (k < kr && ativo && j <= i) { u[k] = exp_dif(mx, u[k]) >> 3; soma += u[k]; }
+        if (k < kr && ativo && j <= i) { u[k] = exp_tab(texp, mx, u[k]); soma += u[k]; }
     }
     soma = g_sum<LPR>(soma);
     if (ativo && soma <= 0) {
         if (l == 0) reporta(E_DIV, kid, idx, soma, mx);
         soma = 1;
     }
-    const int inv = (1 << 28) / max(soma, 1);
+    // a row's sum is at least 4095 (its maximum contributes exp(0) >> 3), so 2^28 / sum < 2^20: div_exata's bound
+    const int inv = soma > 256 ? div_exata(1 << 28, soma) : (1 << 28) / max(soma, 1);
     uint8_t* Pb = P + (size_t)blockIdx.x * T * T;
     int o[4] = {0, 0, 0, 0};
 #pragma unroll

@@ -141,6 +141,8 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     __shared__ int sred[4][16];
     __shared__ __align__(16) _Float16 pw[4][16][LP];
     __shared__ float so[4][16][64];
+    __shared__ __align__(16) unsigned short texp[EXP_N];
+    exp_tab_lds(texp);                                               // published by the first barrier below
     // workgroups in decreasing work across all heads (the query tile qt costs qt + 1 key tiles): the ones resident
     // together on a CU then mix long and short rows
     const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, qt = nqt - 1 - (int)(blockIdx.x / BH);
@@ -224,7 +226,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
         if (n >= nv) continue;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int ex = uu[n][v] == U_MIN ? 0 : exp_dif(mx[v], uu[n][v]) >> 3;
+            const int ex = exp_tab(texp, mx[v], uu[n][v]);          // a masked pair (U_MIN) reads the final 0
             uu[n][v] = ex;
             soma[v] += ex;
         }

@@ -77,6 +77,52 @@ __device__ __forceinline__ int exp_int(int d) {
 // exp(-(mx - u)/256) with the difference clamped before subtracting (mx - u may exceed 2^31)
 __device__ __forceinline__ int exp_dif(int mx, int u) { return exp_int(u <= mx - 6000 ? 6000 : mx - u); }
 
+// The softmax numerator exp_int(d) >> 3 (ops.py:203) as a table: d takes at most 6001 values, and from EXP_D0 on
+// the numerator is 0, so EXP_D0 + 1 entries (the last 0) hold it exactly. Built at compile time by the same integer
+// arithmetic; the compiler checks that every d in [EXP_D0, 6000] gives 0 and that EXP_D0 is the first such d.
+// A kernel copies it into LDS (exp_tab_lds) and reads one 16-bit entry per score instead of the cubic's ~16
+// instructions.
+namespace tabexp {
+constexpr int exp_int_c(int d) {
+    const int t = (d < 6000 ? d : 6000) * 23637;
+    const int n = t >> 22, f = (t & ((1 << 22) - 1)) >> 7;
+    int p = -1295;
+    p = ((p * f) >> 15) + 7556;
+    p = ((p * f) >> 15) - 22645;
+    p = ((p * f) >> 15) + 32765;
+    return n > 30 ? 0 : p >> n;
+}
+constexpr int primeiro_zero() {
+    int d = 6000;
+    while (d > 0 && (exp_int_c(d - 1) >> 3) == 0) d--;
+    return d;
+}
+}  // namespace tabexp
+constexpr int EXP_D0 = tabexp::primeiro_zero();
+constexpr int EXP_N = (EXP_D0 + 1 + 7) & ~7;                        // entries, padded to whole 16-byte chunks
+static_assert(EXP_D0 > 0 && (tabexp::exp_int_c(EXP_D0 - 1) >> 3) != 0, "exp table: EXP_D0 is the first zero");
+struct TabExp { unsigned short v[EXP_N]; };
+constexpr TabExp faz_tab_exp() {
+    TabExp t{};
+    for (int d = 0; d < EXP_N; d++) t.v[d] = (unsigned short)(d < EXP_D0 ? tabexp::exp_int_c(d) >> 3 : 0);
+    return t;
+}
+constexpr bool tab_exp_zero_depois() {
+    for (int d = EXP_D0; d <= 6000; d++)
+        if ((tabexp::exp_int_c(d) >> 3) != 0) return false;
+    return true;
+}
+static_assert(tab_exp_zero_depois(), "exp table: the numerator is 0 for every d >= EXP_D0");
+__constant__ const TabExp TAB_EXP = faz_tab_exp();
+// copy the table into a workgroup's LDS (EXP_N / 8 chunks of 16 bytes); the caller's barrier publishes it
+__device__ __forceinline__ void exp_tab_lds(unsigned short* t) {
+    for (int c = threadIdx.x; c < EXP_N / 8; c += blockDim.x)
+        reinterpret_cast<int4*>(t)[c] = reinterpret_cast<const int4*>(TAB_EXP.v)[c];
+}
+// exp_dif(mx, u) >> 3 from the table for u <= mx: the difference as unsigned is exact (below 2^32) however far
+// apart mx and u are, and every difference from EXP_D0 on reads the final 0 (an index never leaves the table)
+__device__ __forceinline__ int exp_tab(const unsigned short* t, int mx, int u) { return t[min((unsigned)(mx - u), (unsigned)EXP_D0)]; }
+
 // The spec's isqrt (ops.py:84-89: 10 Newton steps from 2^ceil(bitlen(n)/2)) is floor(sqrt(n)) for every
 // 1 <= n < 2^31 (checked over all of them) and 1 for n <= 0. Here: a float square root, within 0.01 of sqrt(n) for
 // these n, whose floor is off by at most one and is corrected by one exact integer step either way.
