@@ -232,8 +232,8 @@ __global__ void __launch_bounds__(TMAX) k_atencao4_back(const int8_t* __restrict
 // the unrolled steps past it are skipped by a scalar branch, and the causal half of the pairs costs nothing.
 // The backward loads the head's whole P ([j][i] as stored) into LDS first with 16-byte accesses (rows 144 bytes
 // apart: 16-byte aligned, and the 8 keys a wave touches at once fall on different banks) instead of reading one
-// byte per pair twice. (The forward stores P a byte per pair: gathering a wave's rows into 8-byte pieces first, or
-// the head's P into LDS behind a workgroup barrier, measured slower.)
+// byte per pair twice. The forward writes P the same way round: a byte per pair into the head's transposed P in
+// LDS, then 16-byte stores of whole rows.
 constexpr int PLD = 144;
 // the T x T bytes of global P ([j][i], rows of T) into the LDS copy (rows of PLD), 16 bytes per thread and step
 __device__ __forceinline__ void carrega_p(const uint8_t* __restrict__ Pg, uint8_t (*ps)[PLD], int T) {
@@ -282,6 +282,8 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     __shared__ int qa[TMAX][4], ka[TMAX][4], va[TMAX][4];
     __shared__ int red[3][NW];
     __shared__ __align__(16) unsigned short texp[EXP_N];
+    __shared__ __align__(16) uint8_t pt[TMAX][PLD];                // P of the head, transposed ([j][i])
+    static_assert(PLD >= TMAX && PLD % 16 == 0, "P rows in LDS");
     const int b = blockIdx.x / H, h = blockIdx.x % H, ld = 3 * D, b0 = b * T;
     int eo[3];
     {
@@ -342,10 +344,20 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
 #pragma unroll
             for (int d = 0; d < 4; d++) o[d] += mul24(p, va[j][d]);
         }
-        if (ativo && j < T) Pb[(size_t)j * T + i] = (uint8_t)p;
+        if (ativo && j < T) pt[j][i] = (uint8_t)p;
     }
 #pragma unroll
     for (int d = 0; d < 4; d++) o[d] = g_sum<LPR>(o[d]);
+    // the head's P, transposed in LDS, goes out as 16-byte pieces of whole rows: byte stores scattered over rows T
+    // apart cost 7.7 of this kernel's 27 us at the reference shape, these 2.5
+    __syncthreads();
+    {
+        const int porl = T / 16, n = T * porl;
+        for (int c = threadIdx.x; c < n; c += blockDim.x) {
+            const int r = c / porl, col = (c - r * porl) * 16;
+            *reinterpret_cast<int4*>(Pb + (size_t)r * T + col) = *reinterpret_cast<const int4*>(&pt[r][col]);
+        }
+    }
     if (!ativo || l != 0) return;
 #pragma unroll
     for (int d = 0; d < 4; d++) {
