@@ -238,7 +238,7 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
         const int nb = L.K / g_blk, ksmax = std::min(g_blk == 32 ? 4 : 2, 4 / r);
         int ks = 1;
         while (ks < ksmax && tot * 2 * ks <= g_alvo_wg && nb >= 8 * ks) ks *= 2;
-        const size_t lds = gemm_lds(nb, ks, g_blk, r);
+        const size_t lds = gemm_lds(nb, ks, g_blk, r, gemm::CTAB_LOTE);
 #define L_(BL, S, RR) (lds_max(k_gemm_lote<BL, S, RR>, lds), k_gemm_lote<BL, S, RR><<<(unsigned)tot, 256 * RR * S, lds, g_stream>>>(L, kid + base))
         if (r == 4) { if (g_blk == 32) L_(32, 1, 4); else L_(128, 1, 4); }
         else if (r == 2) { if (g_blk == 32) { if (ks == 1) L_(32, 1, 2); else L_(32, 2, 2); } else { if (ks == 1) L_(128, 1, 2); else L_(128, 2, 2); } }

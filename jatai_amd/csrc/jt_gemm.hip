@@ -35,7 +35,15 @@ constexpr int BM = 32, BN = 128, PAD = 4;   // BM: rows of the default tile (R =
 // MFMA fragment reads (16 rows x one chunk per half-wave) and the stage stores (8 rows x 8 chunks per wave) then
 // touch every LDS bank once. BLK=128: 128-byte rows padded by 8 bytes.
 // K-blocks held by the shift tables: all of K up to 4096 values, else chunks of 2048 values
-__host__ __device__ constexpr int bloco_tab(int nb, int blk) { return (nb * blk > 4096 ? 2048 : 4096) / blk; }
+// (ctab > 0: chunks of ctab values instead of 2048 when K is chunked anyway and ctab / blk is a multiple of 16,
+// the chunked path's 16-byte exponent loads)
+__host__ __device__ constexpr int bloco_tab(int nb, int blk, int ctab = 0) {
+    return (nb * blk > 4096 ? (ctab > 0 && ctab < 2048 && (ctab / blk) % 16 == 0 ? ctab : 2048) : 4096) / blk;
+}
+// Chunk of the grouped weight-gradient launch (k_gemm_lote) past K = 4096: 1024 values, so a 32-row tile's LDS is
+// 28.7 KB and five workgroups fit per CU instead of four (config 5, K = 16384: 3532 -> 3447 us; at K <= 4096 the
+// single chunk of all of K measured as fast, 448 against 450 us at config 4, and is kept)
+constexpr int CTAB_LOTE = 1024;
 template <int BLK, int R = 1> struct Est {
     static constexpr int SK = BLK == 32 ? 64 : 128;
     static constexpr bool SWZ = BLK == 32;
@@ -54,7 +62,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                            const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
                                            int K, int kid, const int row0, const int col0, const Otim ot = Otim{}, int k_lr = 0,
-                                           int ef = 0, int est = 0) {
+                                           int ef = 0, int est = 0, int ctab = 0) {
     using gemm::BN;
     using gemm::PAD;
     using E = gemm::Est<BLK, R>;
@@ -70,7 +78,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // The shift tables hold at most NBC K-blocks: all of K up to 4096 values; a longer K runs in chunks of 2048
     // values, each with its own tables (the row maxima RA, RB are over all of K). Half-size chunks keep the tables
     // of a 32-row tile at the LDS size of K = 2048, so four workgroups stay resident per CU.
-    const int NBC = gemm::bloco_tab(nb, BLK);
+    const int NBC = gemm::bloco_tab(nb, BLK, ctab);
     const int nbt = min(nb, NBC), nch = (nb + NBC - 1) / NBC;
     // LDS: RA [BM], RB [BN] int32 (live to the end); shift terms na[b][i] = ea_ib + 4 - RA_i (int32) and
     // nb[b][j] = eb_jb - RB_j (int8) of the chunk's blocks, clamped at -100 (n = na + nb <= -22 scales |p| < 2^21
@@ -561,7 +569,7 @@ __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_
         if (i + s < L.n && L.ini[i + s] <= t) i += s;
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
     gemm_corpo<BLK, 1, KS, R>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i],
-                              L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN);
+                              L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN, Otim{}, 0, 0, 0, gemm::CTAB_LOTE);
 }
 
 // The weight gradients of a step with the optimizer in the epilogue (mode 5): GEMM i's tile goes through
@@ -589,11 +597,11 @@ __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_
 }
 
 // dynamic LDS bytes for nb K-blocks, KS K-splits and tiles of 32 R rows
-static inline size_t gemm_lds(int nb, int ks, int blk, int R = 1) {
+static inline size_t gemm_lds(int nb, int ks, int blk, int R = 1, int ctab = 0) {
     using gemm::BN;
     using gemm::PAD;
     const int bm = 32 * R;
-    nb = std::min(nb, gemm::bloco_tab(nb, blk));                    // the shift tables hold one chunk of K
+    nb = std::min(nb, gemm::bloco_tab(nb, blk, ctab));              // the shift tables hold one chunk of K
     const size_t fixo = (size_t)(bm + BN) * 4 + (size_t)nb * bm * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
     const size_t stage = (size_t)(32 * R + BN) * (blk == 32 ? gemm::Est<32>::LD : gemm::Est<128>::LD);
     size_t area = (size_t)ks * 2 * stage;

@@ -55,10 +55,11 @@ def test_modelo_transpostas_em_lote():
     assert est(a) == est(b)
 
 
-@pytest.mark.parametrize("blk", [32, 128])
-def test_gemm_cru_lote_igual_a_gemm(blk):
+@pytest.mark.parametrize("blk,K", [(32, 512), (128, 512), (32, 2048), (128, 2048), (32, 8192), (128, 8192)])
+def test_gemm_cru_lote_igual_a_gemm(blk, K):
+    """70 GEMMs in two grouped launches equal one raw gemm each: K = 512 and 2048 in one chunk of shift tables,
+    K = 8192 in chunks (1024 values at BLK 32, 2048 at BLK 128)."""
     gpu = GPU(blk, vigiar=True)
-    K = 512
     formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(70)]
     pares, ref = [], []
     for i, (M, N) in enumerate(formas):
