@@ -382,19 +382,25 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     }
     __syncthreads();
     if constexpr (MODO == 1) {
-        // raw output, coalesced: thread t writes column t % 128 of rows 16 (t / 128) .. +15 (64 consecutive ints per wave)
+        // raw output in 16-byte pieces: thread t writes columns 4 (t % 32) .. + 3 of rows t / 32 + 8 R k, k = 0 .. 3
+        // (a wave: two rows of 512 contiguous bytes of C32 and 256 of Ce)
+        typedef short s4_t __attribute__((ext_vector_type(4)));
         if (tid < GT) {
-            const int c = tid & 127, r0 = (tid >> 7) * 16;
-            const int rbc = rb_s[c] - 4;
-#pragma unroll 4
-            for (int rr = 0; rr < 16; rr++) {
-                const int r = r0 + rr;
-                int v = 0;
+            const int c = (tid & 31) * 4;
+            int rbc[4];
 #pragma unroll
-                for (int q = 0; q < KS; q++) v += acc_s[q * TILE + r * (BN + PAD) + c];
+            for (int x = 0; x < 4; x++) rbc[x] = rb_s[c + x] - 4;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int r = (tid >> 5) + 8 * R * k;
+                v4i t = *reinterpret_cast<const v4i*>(acc_s + r * (BN + PAD) + c);
+#pragma unroll
+                for (int q = 1; q < KS; q++) t += *reinterpret_cast<const v4i*>(acc_s + q * TILE + r * (BN + PAD) + c);
                 const size_t oo = (size_t)(row0 + r) * N + col0 + c;
-                C32[oo] = v;
-                Ce[oo] = (int16_t)max(-30000, ra_s[r] + rbc);
+                *reinterpret_cast<v4i*>(C32 + oo) = t;
+                const int ra = ra_s[r];
+                *reinterpret_cast<s4_t*>(Ce + oo) = s4_t{(short)max(-30000, ra + rbc[0]), (short)max(-30000, ra + rbc[1]),
+                                                         (short)max(-30000, ra + rbc[2]), (short)max(-30000, ra + rbc[3])};
             }
         }
         return;
