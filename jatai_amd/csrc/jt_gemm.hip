@@ -56,7 +56,9 @@ template <int BLK, int R = 1> struct Est {
 }
 
 // The body of one workgroup's tile (rows row0 .., columns col0 ..), shared by k_gemm and the grouped k_gemm_lote.
-template <int BLK, int MODO, int KS, int R = 1>
+// PADT: exponent rows staged with padding (below); on for the K-split and grouped kernels, where it measured faster
+// (grouped launch 445 -> 435 us at config 4), off for the single-split ones, whose code it made 3-6% slower.
+template <int BLK, int MODO, int KS, int R = 1, bool PADT = (KS > 1)>
 __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const int8_t* __restrict__ EA, const int8_t* __restrict__ B,
                                            const int8_t* __restrict__ EB, int8_t* __restrict__ Cm, int8_t* __restrict__ CE,
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
@@ -164,11 +166,14 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // A thread's row r = tid % 32 and column c = tid % 128 are the same in every iteration, so their maxima are read
     // once; the exponent bytes of U iterations are read before any table entry is written (the writes could alias
     // the reads for the compiler, which would otherwise wait on every read).
-    auto desloca_tab = [&](int nbc) {
+    // The staged rows are sst bytes apart: with PADT, nbc + 4 when nbc is a multiple of 16, an odd number of 4-byte words, so
+    // the byte reads below (consecutive threads, consecutive rows) fall in different LDS banks; rows nbc bytes
+    // apart (a multiple of 64 at K >= 2048) put a wave's reads in two banks.
+    auto desloca_tab = [&](int nbc, int sst) {
         const int r = tid & (BM - 1), c = tid & (BN - 1);
         const int ra4 = 4 - ra_s[r], rbn = -rb_s[c];
-        const int8_t* ea = st_s + r * nbc;
-        const int8_t* eb = st_s + (BM + c) * nbc;
+        const int8_t* ea = st_s + r * sst;
+        const int8_t* eb = st_s + (BM + c) * sst;
         constexpr int U = 4, SA = GT * KS / BM, SB = GT * KS / BN;   // SA = 8 KS, SB = 2 R KS
         for (int b0 = tid / BM; b0 < nbc; b0 += U * SA) {           // entries b * BM + r
             int e[U];
@@ -196,6 +201,10 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         const int nva = BM * nb / 16, nvt = (BM + BN) * nb / 16;
         const int4* ga = reinterpret_cast<const int4*>(EA + (size_t)row0 * nb);
         const int4* gb = reinterpret_cast<const int4*>(EB + (size_t)col0 * nb);
+        // rows of whole vectors, 32 bytes or more (the ones that fall in 4 or fewer banks): staged sst1 bytes apart;
+        // at 16 bytes (8 banks) the padding's split stores cost more than the conflicts (K = 512: 2-5% slower)
+        const bool pad = PADT && nb % 16 == 0 && nb >= 32;
+        const int q = pad ? nb / 16 : 1, sst1 = pad ? nb + 4 : nb;
         for (int v0 = tid; v0 < nvt; v0 += 4 * GT * KS) {
             int4 t[4];
 #pragma unroll
@@ -206,15 +215,23 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const int v = min(v0 + k * GT * KS, nvt);
-                *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
+                if (pad) {                                            // v = nvt: the junk row BM + BN
+                    const int r = v / q;
+                    int* d = reinterpret_cast<int*>(st_s + (size_t)r * sst1 + 16 * (v - r * q));
+                    d[0] = t[k].x; d[1] = t[k].y; d[2] = t[k].z; d[3] = t[k].w;
+                } else {
+                    *reinterpret_cast<int4*>(st_s + (size_t)v * 16) = t[k];
+                }
             }
         }
         __syncthreads();
-        // RA, RB: 16 exponent bytes per LDS read when the rows are 16-byte aligned (nb a multiple of 16)
-        const int8_t* er = tid < BM ? st_s + tid * nb : (tid >= OB && tid < OB + BN) ? st_s + (BM + tid - OB) * nb : nullptr;
+        // RA, RB: 4 exponent bytes per LDS read from padded rows, 16 from unpadded rows of whole vectors, else 1
+        const int8_t* er = tid < BM ? st_s + tid * sst1 : (tid >= OB && tid < OB + BN) ? st_s + (BM + tid - OB) * sst1 : nullptr;
         if (er) {
             int m = -128;
-            if (nb % 16 == 0) {
+            if (pad) {
+                for (int b = 0; b < nb; b += 4) m = max(m, max_i8x4(*reinterpret_cast<const int*>(er + b)));
+            } else if (nb % 16 == 0) {
                 for (int b = 0; b < nb; b += 16) {
                     const int4 t = *reinterpret_cast<const int4*>(er + b);
                     m = max(m, max(max(max_i8x4(t.x), max_i8x4(t.y)), max(max_i8x4(t.z), max_i8x4(t.w))));
@@ -226,19 +243,25 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             else rb_s[tid - OB] = m;
         }
         __syncthreads();
-        desloca_tab(nb);
+        desloca_tab(nb, sst1);
     };
     // several chunks: 160 row segments of nbc bytes (a multiple of 16) at column b0 of rows of nb bytes, one
     // 16-byte vector at a time (this runs between chunks, with the accumulators live)
     auto tabelas_parte = [&](int b0, int nbc) {
-        const int vpr = nbc / 16;
+        const int vpr = nbc / 16, sst = PADT ? nbc + 4 : nbc;
         for (int v = tid; v < (BM + BN) * vpr; v += GT * KS) {
             const int r = v / vpr, k = v - r * vpr;
             const int8_t* e = r < BM ? EA + (size_t)(row0 + r) * nb : EB + (size_t)(col0 + r - BM) * nb;
-            *reinterpret_cast<int4*>(st_s + (size_t)r * nbc + 16 * k) = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
+            const int4 t = *reinterpret_cast<const int4*>(e + b0 + 16 * k);
+            if constexpr (PADT) {
+                int* d = reinterpret_cast<int*>(st_s + (size_t)r * sst + 16 * k);
+                d[0] = t.x; d[1] = t.y; d[2] = t.z; d[3] = t.w;
+            } else {
+                *reinterpret_cast<int4*>(st_s + (size_t)r * sst + 16 * k) = t;
+            }
         }
         __syncthreads();
-        desloca_tab(nbc);
+        desloca_tab(nbc, sst);
     };
     int b0 = 0;                                                     // first K-block of the current chunk
     // chunk 0, before the accumulators are live: its first two stages in flight during the exponent staging
@@ -574,8 +597,9 @@ __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_
     for (int s = 32; s; s >>= 1)
         if (i + s < L.n && L.ini[i + s] <= t) i += s;
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
-    gemm_corpo<BLK, 1, KS, R>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr, L.M[i],
-                              L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN, Otim{}, 0, 0, 0, gemm::CTAB_LOTE);
+    gemm_corpo<BLK, 1, KS, R, true>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr,
+                                    L.M[i], L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN, Otim{}, 0, 0, 0,
+                                    gemm::CTAB_LOTE);
 }
 
 // The weight gradients of a step with the optimizer in the epilogue (mode 5): GEMM i's tile goes through
@@ -611,7 +635,7 @@ static inline size_t gemm_lds(int nb, int ks, int blk, int R = 1, int ctab = 0) 
     const size_t fixo = (size_t)(bm + BN) * 4 + (size_t)nb * bm * 4 + (((size_t)nb * BN + 15) & ~(size_t)15);
     const size_t stage = (size_t)(32 * R + BN) * (blk == 32 ? gemm::Est<32>::LD : gemm::Est<128>::LD);
     size_t area = (size_t)ks * 2 * stage;
-    const size_t exp_bruto = (size_t)nb * (bm + BN) + 16;
+    const size_t exp_bruto = (size_t)(nb + 4) * (bm + BN + 1) + 16;   // staged rows nb + 4 bytes apart, and a junk row
     const size_t acc = (size_t)ks * bm * (BN + PAD) * 4;
     if (exp_bruto > area) area = exp_bruto;
     if (acc > area) area = acc;
