@@ -69,8 +69,9 @@ class Modelo:
         # launches (~10k tiles instead of 50 launches of 64-256 tiles); same results.
         self.dw_em_lote = hasattr(ops, "gemm_cru_lote")
         # momento + peso inside the grouped weight-gradient GEMM's epilogue, no gradient buffers (226 MB at config
-        # 4). Off by default: the optimizer is bound by its own arithmetic, so the separate pass is as fast
-        # (measured 0.80 ms vs 0.82 ms per step at config 4).
+        # 4). Off by default: the optimizer is bound by its own arithmetic, so the fusion saves little (a config-4
+        # step 3.183 -> 3.162 ms, a config-5 step 34.49 -> 34.69 ms), and the separate launch keeps the GEMM's
+        # own time measurable.
         self.otim_no_gemm = False
         # attention kernels that write their outputs quantized (quant(atencao), quant(atencao_back)): same results
         self.quant_na_atencao = hasattr(ops, "atencao_q")
