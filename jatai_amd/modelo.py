@@ -3,11 +3,10 @@
 byte vocabulary, Q/K/V in one matrix, SGD with momentum 7/8, lr = 2^-k and error feedback -- run on any backend
 with the reference operator surface (OpsHip on the GPU; a CPU oracle in the tests and the CPU baseline).
 
-`PassoGravado` captures one whole training step (forward, backward, optimizer: ~522 launches at L=12) as one
-hipGraph through torch.cuda.graph (reference: modelo.py:143-180). Weights, momentum and residuals are updated in
-place by the kernels, every temporary lives in the graph's pool at a fixed address, and the loss is computed on
-the host side of the replay from the captured per-row integers (d_alvo, soma), so no library reduction is
-recorded inside the graph.
+`PassoGravado` captures one whole training step (forward, backward, optimizer: 522 launches op by op at L=12,
+about 230 with the fusions below) as one hipGraph through torch.cuda.graph (reference: modelo.py:143-180).
+Weights, momentum and residuals are updated in place by the kernels, every temporary lives in the graph's pool at
+a fixed address, and the loss is computed inside the graph from the per-row integers (d_alvo, soma).
 """
 import math
 import os
@@ -75,8 +74,13 @@ class Modelo:
         self.otim_no_gemm = False
         # attention kernels that write their outputs quantized (quant(atencao), quant(atencao_back)): same results
         self.quant_na_atencao = hasattr(ops, "atencao_q")
-        # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand)
+        # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand), on
+        # launches of at least 4 workgroups per CU: the epilogue's transposed write is a serial tail of each
+        # workgroup, hidden by the other resident workgroups of a large grid and exposed at one per CU, where the
+        # batched transpose is faster (config 4, 256 workgroups: step 3.183 ms fused, 3.162 batched; config 5, 8192
+        # workgroups: 34.62 fused, 34.76 batched)
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
+        self.t_na_gemm_min_wg = None    # the workgroup threshold (None: 4 per CU of the device; 0: always)
         # the residual update of the backward, soma(gx, rms_back(...)), in one launch
         self.rms_soma = hasattr(ops, "rms_back_soma")
         # the R16 step's residual adds, soma16(x16, gemm(...)) and soma16(gx16, rms_back(...)), each with the INT8
@@ -89,6 +93,17 @@ class Modelo:
         # so the stage can be timed between replays as the step runs it
         self.marcas = {}
         self._gbuf, self._tabela = None, None
+
+    def _t_na_gemm(self, M, N):
+        """Whether the ReLU^2-backward GEMM of M tokens x N columns writes its transpose too (see transposta_na_gemm)."""
+        if not self.transposta_na_gemm:
+            return False
+        lib = getattr(self.ops, "lib", None)
+        if self.t_na_gemm_min_wg == 0 or lib is None:
+            return True
+        if self.t_na_gemm_min_wg is None:
+            self.t_na_gemm_min_wg = 4 * torch.cuda.get_device_properties(self.dev).multi_processor_count
+        return (M // lib.jt_gemm_tile(M, N, 4)) * (N // 128) >= self.t_na_gemm_min_wg
 
     def _otim_no_gemm(self):
         """Weight gradients straight into momento + peso in the grouped GEMM's epilogue (no gradient buffers)."""
@@ -196,7 +211,7 @@ class Modelo:
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("mlp"):
                         grads[f"Wd{l}"] = grad_w(f"Wd{l}", gx, a)
-                        if self.transposta_na_gemm:
+                        if self._t_na_gemm(h[0].shape[0], h[0].shape[1]):
                             gh, tgh = ops.gemm_relu2_back_t(gx, T_(p[f"Wd{l}"]), h)
                             prontas[id(gh[0])] = tgh
                         else:
