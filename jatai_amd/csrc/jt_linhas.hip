@@ -277,8 +277,11 @@ __global__ void __launch_bounds__(2 * TR) k_transpoe_lote(const LoteT L, int kid
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
         const int t = min(blockIdx.x * TPW + j, L.ini[L.n] - 1);   // past the list's end: a copy of the last tile, not stored
-        int i = 0;                                                  // uniform: kernel arguments, scalar loads
-        while (i + 1 < L.n && L.ini[i + 1] <= t) i++;
+        // the last tensor whose first tile is at most t (a binary search: 6 dependent scalar loads instead of up to
+        // 63 in a scan, which cost the step's three launches 140 -> 126 us at config 4); uniform, kernel arguments
+        int i = 0;
+        for (int s = 32; s; s >>= 1)
+            if (i + s < L.n && L.ini[i + s] <= t) i += s;
         const int local = t - L.ini[i], ntx = L.C[i] / 64;
         ti[j] = i; bx[j] = local % ntx; by[j] = local / ntx;
         c[j] = transpoe_carga<BLK, TR>(L.X[i], L.EX[i], L.C[i], bx[j], by[j]);

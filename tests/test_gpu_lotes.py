@@ -1,7 +1,8 @@
 """Batched launches that have no reference counterpart, against the per-tensor ops they replace (bit-exact):
 
 * transpoe_lote over 70 tensors of mixed shapes (two launches: 64 tensors per launch) equals transpoe of each,
-  at BLK 32 and 128, and each result equals the CPU oracle's transpose;
+  at BLK 32 and 128, and each result equals the CPU oracle's transpose; and so does one launch of ~8.4k tiles
+  (4 tiles per workgroup, a partial last workgroup);
 * the model step with batched transposes leaves weights, momenta and residuals identical to one transpoe per use;
 * gemm_cru_lote over 70 GEMMs (two launches) equals one raw gemm each, at BLK 32 and 128, and a model step
   with the deferred grouped weight-gradient GEMMs equals the step with one GEMM per gradient.
@@ -29,6 +30,27 @@ def test_transpoe_lote_igual_a_transpoe(blk):
     for i, (a, b) in enumerate(zip(lote, um)):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"tensor {i} {formas[i]}"
     for i in (0, 33, 69):
+        ref = cpu.ops.transpoe(tuple(cpu.dev(a) for a in xs_h[i]))
+        assert np.array_equal(host(lote[i][0]), host(ref[0])) and np.array_equal(host(lote[i][1]), host(ref[1]))
+
+
+@pytest.mark.parametrize("blk", [32, 128])
+def test_transpoe_lote_grande_igual_a_transpoe(blk):
+    """64 tensors, ~8.4k tiles in one launch: the launch with 4 tiles per workgroup (from 8192 tiles), whose last
+    workgroup holds a partial set of tiles (the total is not a multiple of 4)."""
+    gpu, cpu = GPU(blk, vigiar=True), CPU(blk)
+    formas = [(128 * (3 + i % 7), 64 * (10 + (7 * i) % 27)) for i in range(64)]
+    formas = [(r, c - c % blk if c % blk else c) for r, c in formas]
+    tiles = sum((r // 128) * (c // 64) for r, c in formas)
+    assert tiles >= 8192 and tiles % 4 != 0
+    xs_h = [R.bloco(R.substream(8, f"lote grande {i}"), r, c, blk, espalha=6, e0=-6) for i, (r, c) in enumerate(formas)]
+    xs = [tuple(gpu.dev(a) for a in x) for x in xs_h]
+    lote = gpu.ops.transpoe_lote(xs)
+    um = [gpu.ops.transpoe(x) for x in xs]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(lote, um)):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"tensor {i} {formas[i]}"
+    for i in (0, 31, 63):
         ref = cpu.ops.transpoe(tuple(cpu.dev(a) for a in xs_h[i]))
         assert np.array_equal(host(lote[i][0]), host(ref[0])) and np.array_equal(host(lote[i][1]), host(ref[1]))
 
