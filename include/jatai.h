@@ -159,6 +159,17 @@ long long jt_scratch_bytes(void);
  * [M, 3D/32]), equal to jt_quant of the raw gradient; same support as jt_atencao_ws_q. */
 int jt_atencao_back_ws_q(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
                          int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid);
+/* no reference counterpart: the forward/backward pair that converts q, k, v once for both. jt_atencao_ws_qs is
+ * jt_atencao_ws_q that also saves, in salvo (jt_atencao_salvo_bytes(Bt, T, H, D) bytes, 16-byte aligned), the
+ * backward's conversions of q, k, v; jt_atencao_back_ws_qs is jt_atencao_back_ws_q reading them from salvo, so it
+ * converts only dO. The caller keeps salvo and qkv unchanged from the one call to the other. The bound variant
+ * (limite = 1) converts q, k, v itself and leaves salvo unread. Same outputs as jt_atencao_ws_q and
+ * jt_atencao_back_ws_q. */
+long long jt_atencao_salvo_bytes(int Bt, int T, int H, int D);
+int jt_atencao_ws_qs(const void* qm, const void* qE, void* Om, void* OE, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                     long long ws_bytes, void* salvo, long long salvo_bytes, int kid);
+int jt_atencao_back_ws_qs(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
+                          int H, int D, int GA, int limite, void* ws, long long ws_bytes, const void* salvo, long long salvo_bytes, int kid);
 
 #ifdef __cplusplus
 }

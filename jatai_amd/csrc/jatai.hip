@@ -617,13 +617,16 @@ long long jt_atencao_ws_bytes(int Bt, int T, int H, int D) {
     if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
     return (long long)atw::bytes_fwd((long long)Bt * H, T);
 }
+// salvo (optional): the backward's conversions of q, k, v are written there too (atw::Salvo)
 static int atencao_ws(const void* qm, const void* qE, void* O1, void* O2, void* P, int Bt, int T, int H, int D, int GA, void* ws, long long ws_bytes,
-                      bool bloco, int kid) {
-    if (!alinhados(qm, qE, O1, O2, P, ws) || !ws || ws_bytes < jt_atencao_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+                      bool bloco, int kid, void* salvo = nullptr) {
+    if (!alinhados(qm, qE, O1, O2, P, ws, salvo) || !ws || ws_bytes < jt_atencao_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
         return (int)hipErrorInvalidValue;
     const long long BH = (long long)Bt * H;
     const atw::Ws w = atw::parte(ws, BH, T);
-    k_atf_prep<<<(unsigned)(BH * (T / 64)), 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, T, H, D, g_blk, GA);
+    if (salvo) k_atf_prep<true><<<(unsigned)(BH * (T / 64)), 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, atw::parte_s(salvo, BH, T),
+                                                                                  T, H, D, g_blk, GA);
+    else k_atf_prep<false><<<(unsigned)(BH * (T / 64)), 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, atw::Salvo{}, T, H, D, g_blk, GA);
     const unsigned g = (unsigned)(BH * (T / 16));
 #define L(NTW, B) k_atf<NTW, B><<<g, 256, 0, g_stream>>>((const int8_t*)qm, (const int8_t*)qE, w, O1, O2, (uint8_t*)P, T, H, D, g_blk, GA, kid)
     if (bloco) { if (T <= 256) L(4, true); else L(8, true); }
@@ -645,6 +648,22 @@ int jt_atencao_ws_q(const void* qm, const void* qE, void* Om, void* OE, void* P,
     if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
     return atencao_ws(qm, qE, Om, OE, P, Bt, T, H, D, GA, ws, ws_bytes, true, kid);
+}
+// No reference counterpart: bytes of the buffer in which jt_atencao_ws_qs saves the backward's conversions of q, k, v
+// for jt_atencao_back_ws_qs (0 for an invalid shape).
+long long jt_atencao_salvo_bytes(int Bt, int T, int H, int D) {
+    if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
+    return (long long)atw::bytes_salvo((long long)Bt * H, T);
+}
+// No reference counterpart: jt_atencao_ws_q that also writes into salvo (jt_atencao_salvo_bytes bytes, 16-byte
+// aligned) the conversions of q, k, v that the backward of the same qkv reads (jt_atencao_back_ws_qs), from the pass
+// that converts k and v for the forward anyway. Same outputs as jt_atencao_ws_q.
+int jt_atencao_ws_qs(const void* qm, const void* qE, void* Om, void* OE, void* P, int Bt, int T, int H, int D, int GA, void* ws,
+                     long long ws_bytes, void* salvo, long long salvo_bytes, int kid) {
+    if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
+    if (!salvo || salvo_bytes < jt_atencao_salvo_bytes(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    return atencao_ws(qm, qE, Om, OE, P, Bt, T, H, D, GA, ws, ws_bytes, true, kid, salvo);
 }
 int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge, int Bt, int T, int H,
                     int D, int GA, int limite, int kid) {
@@ -722,19 +741,27 @@ long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D) {
     if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
     return (long long)atw::bytes_back((long long)Bt * H, T);
 }
+// salvo (optional, exact variant): the conversions of q, k, v saved by jt_atencao_ws_qs for the same qkv
 static int atencao_back_ws(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* G1, void* G2, int Bt, int T,
-                           int H, int D, int GA, int limite, void* ws, long long ws_bytes, bool bloco, int kid) {
-    if (!alinhados(gom, goE, qm, qE, P, G1, G2, ws) || !ws || ws_bytes < jt_atencao_back_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
+                           int H, int D, int GA, int limite, void* ws, long long ws_bytes, bool bloco, int kid, const void* salvo = nullptr) {
+    if (!alinhados(gom, goE, qm, qE, P, G1, G2, ws, salvo) || !ws || ws_bytes < jt_atencao_back_ws_bytes(Bt, T, H, D) || 64 % g_blk && g_blk % 64)
         return (int)hipErrorInvalidValue;
     const long long BH = (long long)Bt * H;
-    const atw::WsB w = atw::parte_b(ws, BH, T);
+    atw::WsB w = atw::parte_b(ws, BH, T);
+    const int* smx = nullptr;
+    if (salvo && !limite) {                              // q, k, v read from the saved conversions
+        const atw::Salvo s = atw::parte_s(const_cast<void*>(salvo), BH, T);
+        w.vm8 = s.vm8; w.vL = s.vL; w.kt = s.kt; w.qt = s.qt;
+        smx = s.mx;
+    }
     const int dsb = ds_bits(T);
     const int8_t *go8 = (const int8_t*)gom, *goE8 = (const int8_t*)goE, *q8 = (const int8_t*)qm, *qE8 = (const int8_t*)qE;
     const uint8_t* P8 = (const uint8_t*)P;
     const unsigned gp = (unsigned)(BH * (T / 64)), gt = (unsigned)(BH * (T / 16));
 #define FASES(NTW, LM, B)                                                                                                 \
     {                                                                                                                     \
-        k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                              \
+        if (!LM && smx) k_atb_prep_s<<<gp, 256, 0, g_stream>>>(go8, goE8, w, smx, T, H, D, g_blk, GA);                     \
+        else k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                         \
         if (!LM) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                                          \
         k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \
         k_atbqkv<NTW, LM, B><<<2 * gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);              \
@@ -799,6 +826,17 @@ int jt_atencao_back_ws_q(const void* gom, const void* goE, const void* qm, const
     if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
     if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
     return atencao_back_ws(gom, goE, qm, qE, P, Gm, GE, Bt, T, H, D, GA, limite, ws, ws_bytes, true, kid);
+}
+// No reference counterpart: jt_atencao_back_ws_q reading the conversions of q, k, v that jt_atencao_ws_qs saved in
+// salvo for this qkv (the caller keeps salvo and qkv unchanged in between), so that only dO is converted. The bound
+// variant (limite = 1) also needs per-64-token norms of v, which the forward does not save: it converts q, k, v
+// itself and leaves salvo unread. Same outputs as jt_atencao_back_ws_q.
+int jt_atencao_back_ws_qs(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gm, void* GE, int Bt, int T,
+                          int H, int D, int GA, int limite, void* ws, long long ws_bytes, const void* salvo, long long salvo_bytes, int kid) {
+    if (!atencao_forma(Bt, T, H, D, GA) || T % 64) return (int)hipErrorInvalidValue;
+    if (D / H != 64 || !g_atencao_mfma || T > 512 || g_blk != 32) return (int)hipErrorNotSupported;
+    if (!salvo || salvo_bytes < jt_atencao_salvo_bytes(Bt, T, H, D)) return (int)hipErrorInvalidValue;
+    return atencao_back_ws(gom, goE, qm, qE, P, Gm, GE, Bt, T, H, D, GA, limite, ws, ws_bytes, true, kid, salvo);
 }
 
 }  // extern "C"

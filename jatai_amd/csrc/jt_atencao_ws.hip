@@ -40,6 +40,29 @@ inline Ws parte(void* base, long long BH, int T) {
     w.mx = (int*)p;
     return w;
 }
+// The backward's conversions of q, k, v, written by the forward's conversion pass, which has those values loaded
+// (kept by the caller from the forward to the backward of the same qkv): vm8 int8 [BH][T][64]; vL int8 [BH][T][2];
+// kt, qt f16 [BH][64][T]; mx int [BH][4] (emq, emk, emv: the head maxima, before - GA)
+struct Salvo {
+    int8_t *vm8, *vL;
+    _Float16 *kt, *qt;
+    int* mx;
+};
+inline size_t bytes_salvo(long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    return alinha256(n * 64) + alinha256(n * 2) + 2 * alinha256(n * 64 * 2) + alinha256((size_t)BH * 16);
+}
+inline Salvo parte_s(void* base, long long BH, int T) {
+    const size_t n = (size_t)BH * T;
+    char* p = (char*)base;
+    Salvo s;
+    s.vm8 = (int8_t*)p; p += alinha256(n * 64);
+    s.vL = (int8_t*)p; p += alinha256(n * 2);
+    s.kt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    s.qt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    s.mx = (int*)p;
+    return s;
+}
 }
 
 // Largest block exponent of the 64 / blk blocks of a head slice in one token's exponent row e (column c0): at
@@ -82,23 +105,36 @@ __device__ __forceinline__ void grava_t64(const TileT& tile, _Float16* __restric
     }
 }
 
-__global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, int T, int H, int D,
-                                                  int blk, int GA) {
+// SALVA: also the backward's conversions of q, k, v into s (the arithmetic of k_atb_prep's: v as m8 << L
+// fragments, q and k aligned as f16 [64][T], the head maxima), so the backward converts only dO.
+template <bool SALVA = false>
+__global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm, const int8_t* __restrict__ qE, atw::Ws w, atw::Salvo s, int T,
+                                                  int H, int D, int blk, int GA) {
     constexpr int HD = 64;
     __shared__ int red[3][4];
     __shared__ __align__(16) TileT tv;
+    __shared__ __align__(16) TileT tqk[SALVA ? 2 : 1];              // SALVA: q and k aligned, for the backward
     const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, nbl = ld / blk, tid = threadIdx.x;
-    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t; its k and v values are loaded before the head
-    // maxima's barrier, so their latency overlaps it
+    // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t; its k and v values (and q with SALVA) are loaded
+    // before the head maxima's barrier, so their latency overlaps it
     const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
     const size_t base = (size_t)(b0 + t) * ld, tt = (size_t)bh * T + t;
-    const int colk = D + h * HD + 16 * c4, colv = 2 * D + h * HD + 16 * c4;
+    const int colq = h * HD + 16 * c4, colk = D + colq, colv = 2 * D + colq;
     const int4 rk = ld16(qm + base + colk), rv = ld16(qm + base + colv);
     const int ekt = qE[(size_t)(b0 + t) * nbl + colk / blk], evt = qE[(size_t)(b0 + t) * nbl + colv / blk];
+    int4 rq = make_int4(0, 0, 0, 0);
+    int eqt = 0;
+    if constexpr (SALVA) {
+        rq = ld16(qm + base + colq);
+        eqt = qE[(size_t)(b0 + t) * nbl + colq / blk];
+    }
     int emq, emk, emv;
     emx3(qE, ld, h * HD, D + h * HD, 2 * D + h * HD, blk, b0, T, red, emq, emk, emv);
-    if (part == 0 && tid == 0) { w.mx[bh * 4] = emq; w.mx[bh * 4 + 1] = emk; w.mx[bh * 4 + 2] = emv; }
+    if (part == 0 && tid == 0) {
+        w.mx[bh * 4] = emq; w.mx[bh * 4 + 1] = emk; w.mx[bh * 4 + 2] = emv;
+        if constexpr (SALVA) { s.mx[bh * 4] = emq; s.mx[bh * 4 + 1] = emk; s.mx[bh * 4 + 2] = emv; }
+    }
     {
         int v[16];
         abre_i8(rk, v);
@@ -109,6 +145,11 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
         grava_i8(w.km8 + tt * 64 + 16 * c4, m8);
         if ((c4 & 1) == 0) w.kl[tt * 2 + half] = (int8_t)L;
+        if constexpr (SALVA) {
+            const Desl dk(emk - ekt);
+#pragma unroll
+            for (int k = 0; k < 16; k++) tqk[SALVA ? 1 : 0][16 * c4 + k][tid >> 2] = (_Float16)dk(shl(v[k], GA));
+        }
     }
     {
         int v[16];
@@ -116,9 +157,29 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         const Desl dv(emv - evt);                                    // rnd(v << GA, emv - evt), one shift per block
 #pragma unroll
         for (int k = 0; k < 16; k++) tv[16 * c4 + k][tid >> 2] = (_Float16)dv(shl(v[k], GA));
+        if constexpr (SALVA) {
+            const int sh = emv - evt;
+            int8_t m8[16];
+            int L = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
+            grava_i8(s.vm8 + tt * 64 + 16 * c4, m8);
+            if ((c4 & 1) == 0) s.vL[tt * 2 + half] = (int8_t)L;
+        }
+    }
+    if constexpr (SALVA) {
+        int v[16];
+        abre_i8(rq, v);
+        const Desl dq(emq - eqt);
+#pragma unroll
+        for (int k = 0; k < 16; k++) tqk[0][16 * c4 + k][tid >> 2] = (_Float16)dq(shl(v[k], GA));
     }
     __syncthreads();
     grava_t64(tv, w.vt + (size_t)bh * 64 * T, T, part * 64);
+    if constexpr (SALVA) {
+        grava_t64(tqk[0], s.qt + (size_t)bh * 64 * T, T, part * 64);
+        grava_t64(tqk[SALVA ? 1 : 0], s.kt + (size_t)bh * 64 * T, T, part * 64);
+    }
 }
 
 // NTW = key tiles a wave can own (T / 64)
@@ -308,7 +369,8 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 // The arithmetic of k_atb_mf_linhas / _gq / _gkv / k_atb_exp, in launches that read converted operands from the
 // workspace and split each 16-row tile's partner tiles over four waves:
 //   (0) k_atb_prep: head maxima of dO, q, k, v; dO, v as m8 << L fragments; k, q, dO aligned as f16 [64][T];
-//       for the bound variant (LIMITE), per 64 tokens max |dO| and max ||v||_1 (ops.py:231-235);
+//       for the bound variant (LIMITE), per 64 tokens max |dO| and max ||v||_1 (ops.py:231-235); or k_atb_prep_s,
+//       the same for dO alone when the forward's conversion pass saved those of q, k, v (exact variant);
 //   (1) k_atb1 (exact variant): per query tile, max |gP| over its causal pairs;
 //   (2) k_atb2: s_i = rnd(sum_j P_ij rnd(gP_ij, sh), 8) per row, and per query tile the maxima that set dS's
 //       shrink (max |P (gP' - s)|, or max P, max |gP'|, max |s| for LIMITE);
@@ -473,6 +535,50 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
         if (tid == 0) { w.p1a[bh * atw::SLOTS + part] = a; w.p1b[bh * atw::SLOTS + part] = c; }
     }
+}
+
+// k_atb_prep of the exact variant when the forward's conversion pass saved q, k, v (atw::Salvo, the same qkv): the
+// workspace's vm8, vL, kt, qt point into the saved buffer, so only dO is converted here; the head maxima of q, k, v
+// come from the saved ones (smx), that of dO from one reduction.
+__global__ void __launch_bounds__(256) k_atb_prep_s(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, atw::WsB w,
+                                                    const int* __restrict__ smx, int T, int H, int D, int blk, int GA) {
+    constexpr int HD = 64;
+    __shared__ int red[4];
+    __shared__ __align__(16) TileT tg;
+    const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
+    const int b0 = b * T, tid = threadIdx.x, nbg = D / blk;
+    const int t = part * 64 + (tid >> 2), c4 = tid & 3, half = c4 >> 1;
+    const size_t tt = (size_t)bh * T + t;
+    const int colg = h * HD + 16 * c4;
+    const int4 rg = ld16(gom + (size_t)(b0 + t) * D + colg);
+    const int egt = goE[(size_t)(b0 + t) * nbg + colg / blk];
+    int m = SEM_TOPO;
+    for (int tk = tid; tk < T; tk += 256) m = max(m, emx_fatia(goE + (size_t)(b0 + tk) * nbg, h * HD, blk));   // T <= 512
+    m = g_max<64>(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const int emg = max(max(red[0], red[1]), max(red[2], red[3]));
+    if (part == 0 && tid == 0) {
+        w.mx[bh * 4] = emg - GA;
+        w.mx[bh * 4 + 1] = smx[bh * 4] - GA; w.mx[bh * 4 + 2] = smx[bh * 4 + 1] - GA; w.mx[bh * 4 + 3] = smx[bh * 4 + 2] - GA;
+    }
+    {   // dO: m8 << L fragments and aligned f16, as k_atb_prep
+        int v[16];
+        abre_i8(rg, v);
+        const int s = emg - egt;
+        const Desl ds(s);
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
+            tg[16 * c4 + k][tid >> 2] = (_Float16)ds(shl(v[k], GA));
+        }
+        grava_i8(w.gm8 + tt * 64 + 16 * c4, m8);
+        if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
+    }
+    __syncthreads();
+    grava_t64(tg, w.gt + (size_t)bh * 64 * T, T, part * 64);
 }
 
 // gP tile of query rows i0 .. i0 + 3 (this lane) x key j = 16 t + lr from the workspace fragments

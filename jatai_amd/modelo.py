@@ -74,6 +74,12 @@ class Modelo:
         self.otim_no_gemm = False
         # attention kernels that write their outputs quantized (quant(atencao), quant(atencao_back)): same results
         self.quant_na_atencao = hasattr(ops, "atencao_q")
+        # in a training step, the forward attention's conversion pass also writes the backward's conversions of q, k,
+        # v (a buffer per layer kept to the backward), whose conversion pass then reads only dO: same results. Off by
+        # default: the backward's pass gets 2.6 us shorter and the forward's 1.95 us longer, and the backward kernels
+        # that read those conversions lose 2.2 us, which they now fetch from HBM instead of from the cache the
+        # backward's pass just wrote them to (config-4 step 3.132 -> 3.157 ms; config 5 34.23 either way)
+        self.conversoes_salvas = False
         # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand), on
         # launches of at least 4 workgroups per CU: the epilogue's transposed write is a serial tail of each
         # workgroup, hidden by the other resident workgroups of a large grid and exposed at one per CU, where the
@@ -142,7 +148,10 @@ class Modelo:
                     with reg.trecho("atencao"):
                         n1, c1 = ops.rms(oito(x16) if r16 else x)
                         qkv = ops.gemm(n1, p[f"Wqkv{l}"])
-                        if self.quant_na_atencao:
+                        sv = None
+                        if self.quant_na_atencao and self.conversoes_salvas and k_lr is not None:
+                            om, P, sv = ops.atencao_qs(qkv, Bt, T, self.H)
+                        elif self.quant_na_atencao:
                             om, P = ops.atencao_q(qkv, Bt, T, self.H)
                         else:
                             oc, P = ops.atencao(qkv, Bt, T, self.H)
@@ -168,7 +177,7 @@ class Modelo:
                         else:
                             x = ops.gemm_soma(a, p[f"Wd{l}"], x)
                         self._st(f"c{l}.relu2", a, zeros_normais=True); self._st(f"c{l}.residuo2", x)
-                caches.append((n1, c1, qkv, P, om, n2, c2, h, a))
+                caches.append((n1, c1, qkv, P, om, n2, c2, h, a, sv))
             with reg.trecho("saida"):
                 nf, cf = ops.rms(oito(x16) if r16 else x)
                 logits = ops.gemm(nf, p["out"], cru=True)
@@ -207,7 +216,7 @@ class Modelo:
                 if r16:
                     gx16 = ops.para16(gx)
             for l in reversed(range(self.L)):
-                n1, c1, qkv, P, om, n2, c2, h, a = caches[l]
+                n1, c1, qkv, P, om, n2, c2, h, a, sv = caches[l]
                 with reg.trecho(f"camada {l}"):
                     with reg.trecho("mlp"):
                         grads[f"Wd{l}"] = grad_w(f"Wd{l}", gx, a)
@@ -229,7 +238,9 @@ class Modelo:
                     with reg.trecho("atencao"):
                         grads[f"Wo{l}"] = grad_w(f"Wo{l}", gx, om)
                         go = ops.gemm(gx, T_(p[f"Wo{l}"]))
-                        if self.quant_na_atencao:
+                        if sv is not None:
+                            gq = ops.atencao_back_qs(go, qkv, P, sv, Bt, T, self.H)
+                        elif self.quant_na_atencao:
                             gq = ops.atencao_back_q(go, qkv, P, Bt, T, self.H)
                         else:
                             gq = ops.quant(ops.atencao_back(go, qkv, P, Bt, T, self.H))

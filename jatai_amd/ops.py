@@ -33,7 +33,8 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_bloco_atual", "jt_otimizador", "jt_tab_otim_bytes", "jt_transpoe_lote", "jt_entrada_t_bytes", "jt_gemm_divisoes",
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
            "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
-           "jt_rms_back_soma", "jt_perda", "jt_gemm_tile", "jt_gemm_soma16", "jt_rms_back_soma16")
+           "jt_rms_back_soma", "jt_perda", "jt_gemm_tile", "jt_gemm_soma16", "jt_rms_back_soma16", "jt_atencao_ws_qs",
+           "jt_atencao_back_ws_qs")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -57,6 +58,7 @@ def carrega_lib(caminho=LIB):
     lib.jt_erro_le.argtypes = [ctypes.c_void_p]
     lib.jt_atencao_ws_bytes.restype = ctypes.c_longlong
     lib.jt_atencao_back_ws_bytes.restype = ctypes.c_longlong
+    lib.jt_atencao_salvo_bytes.restype = ctypes.c_longlong
     return lib
 
 
@@ -472,6 +474,47 @@ class OpsHip:
         ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
         self._lanca("atencao_back+quant", "jt_atencao_back_ws_q", (gm, gE, m, E, P, G[0], G[1], Bt, T, H, D, GA, int(ATENCAO_LIMITE), ws, nws),
                     dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D), longos=(14,))
+        return G
+
+    # no reference counterpart: atencao_q / atencao_back_q converting q, k, v once for both. atencao_qs also returns a
+    # buffer with the backward's conversions of q, k, v (None where the kernels do not run: then atencao_back_qs is
+    # atencao_back_q); atencao_back_qs(GO, QKV, P, salvo, ...) reads them, for the same QKV, unchanged in between.
+    def atencao_qs(self, QKV, Bt, T, H):
+        """(quant(O), P, salvo) for (O, P) = atencao(QKV, Bt, T, H)."""
+        m, E = QKV
+        D = m.shape[1] // 3
+        if not self._q_suportado(T, H, D):
+            Om, P = self.atencao_q(QKV, Bt, T, H)
+            return Om, P, None
+        self.reg.confere_bloco("qkv", QKV)
+        self._formas_atencao("atencao", m, Bt, T, H, D)
+        Om = self._novo_bloco(Bt * T, D, m.device)
+        P = torch.empty(Bt * H, T, T, dtype=torch.uint8, device=m.device)
+        nws, ns = self.lib.jt_atencao_ws_bytes(Bt, T, H, D), self.lib.jt_atencao_salvo_bytes(Bt, T, H, D)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+        salvo = torch.empty(max(ns, 16), dtype=torch.uint8, device=m.device)
+        self._lanca("atencao+quant", "jt_atencao_ws_qs", (m, E, Om[0], Om[1], P, Bt, T, H, D, GA, ws, nws, salvo, ns), dict(qkv=m, qkvE=E),
+                    (Bt * T, D), longos=(11, 13))
+        return Om, P, salvo
+
+    def atencao_back_qs(self, GO, QKV, P, salvo, Bt, T, H):
+        """quant(atencao_back(GO, QKV, P, Bt, T, H)), with q, k, v converted by atencao_qs into salvo."""
+        if salvo is None:
+            return self.atencao_back_q(GO, QKV, P, Bt, T, H)
+        (gm, gE), (m, E) = GO, QKV
+        D = gm.shape[1]
+        self.reg.confere_bloco("go", GO); self.reg.confere_bloco("qkv", QKV)
+        self._formas_atencao("atencao_back", m, Bt, T, H, D)
+        self.reg.exige(tuple(P.shape) == (Bt * H, T, T) and P.dtype == torch.uint8 and P.is_contiguous(),
+                       f"atencao_back: P com forma {tuple(P.shape)}, esperado {(Bt * H, T, T)} uint8")
+        ns = self.lib.jt_atencao_salvo_bytes(Bt, T, H, D)
+        self.reg.exige(salvo.dtype == torch.uint8 and salvo.numel() >= ns, f"atencao_back: salvo com {salvo.numel()} bytes, esperado {ns}")
+        G = self._novo_bloco(Bt * T, 3 * D, m.device)
+        nws = self.lib.jt_atencao_back_ws_bytes(Bt, T, H, D)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=m.device)
+        self._lanca("atencao_back+quant", "jt_atencao_back_ws_qs",
+                    (gm, gE, m, E, P, G[0], G[1], Bt, T, H, D, GA, int(ATENCAO_LIMITE), ws, nws, salvo, ns),
+                    dict(go=gm, goE=gE, qkv=m, qkvE=E, P=P), (Bt * T, 3 * D), longos=(14, 16))
         return G
 
     def _formas_atencao(self, op, m, Bt, T, H, D):

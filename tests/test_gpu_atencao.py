@@ -88,6 +88,34 @@ def test_atencao_q_igual_a_quant(T, H, limite):
         _cmp(a, b, nome)
 
 
+@pytest.mark.parametrize("T,H,limite", [(256, 8, False), (256, 8, True), (512, 4, False), (64, 2, False), (128, 16, False)])
+def test_atencao_qs_igual_a_q(T, H, limite):
+    """atencao_qs / atencao_back_qs (q, k, v converted for the backward by the forward's pass and read back from the
+    saved buffer; the bound variant converts them again) equal atencao_q / atencao_back_q, also on a second backward
+    from the same buffer."""
+    blk, Bt, D = 32, 2, 64 * H
+    gpu = GPU(blk, vigiar=True)
+    seed = R.substream(557, f"qs {T} {H} {limite}")
+    qkv = tuple(gpu.dev(v) for v in R.bloco(R.substream(seed, "qkv"), Bt * T, 3 * D, blk, espalha=4, e0=-7, zera=0.05))
+    go = tuple(gpu.dev(v) for v in R.bloco(R.substream(seed, "go"), Bt * T, D, blk, espalha=4, e0=-20, zera=0.05))
+    go2 = tuple(gpu.dev(v) for v in R.bloco(R.substream(seed, "go2"), Bt * T, D, blk, espalha=4, e0=-18, zera=0.05))
+    o = gpu.ops
+    old = gpu.limite(limite)
+    try:
+        om, P, sv = o.atencao_qs(qkv, Bt, T, H)
+        assert sv is not None
+        om_r, P_r = o.atencao_q(qkv, Bt, T, H)
+        gq = o.atencao_back_qs(go, qkv, P, sv, Bt, T, H)
+        gq2 = o.atencao_back_qs(go2, qkv, P, sv, Bt, T, H)
+        gq_r = o.atencao_back_q(go, qkv, P, Bt, T, H)
+        gq2_r = o.atencao_back_q(go2, qkv, P, Bt, T, H)
+    finally:
+        gpu.limite(old)
+    for nome, a, b in (("om", om[0], om_r[0]), ("omE", om[1], om_r[1]), ("P", P, P_r), ("gq", gq[0], gq_r[0]), ("gqE", gq[1], gq_r[1]),
+                       ("gq2", gq2[0], gq2_r[0]), ("gq2E", gq2[1], gq2_r[1])):
+        _cmp(a, b, nome)
+
+
 @pytest.mark.parametrize("limite", [False, True])
 def test_atencao_hd64_reduz_ao_spec_hd4(limite, via_ws):
     """The head-width-64 kernels on inputs where each head carries one head-width-4 head of the spec's shape

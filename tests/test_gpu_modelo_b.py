@@ -31,6 +31,7 @@ def test_passo_config4_vs_oraculo():
     assert mf.otimizador_fundido and mf.transpostas_em_lote and mf.dw_em_lote and mf.quant_na_atencao and mf.transposta_na_gemm and mf.rms_soma and mf.perda_fundida
     assert not mf._t_na_gemm(Bt * T, FF)        # 512 tokens: a grid below the threshold keeps the batched transpose
     mf.t_na_gemm_min_wg = 0                     # every fusion on, so this step covers the GEMM's transposed write
+    mf.conversoes_salvas = True                 # and the attention backward reading the forward's conversions
     for p in range(2):
         x = R.tokens(R.substream(31, f"b4 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
         tok = torch.from_numpy(x[:, :-1].copy()).long()
