@@ -60,8 +60,10 @@ int jt_gemm_soma16(const void* A, const void* EA, const void* B, const void* EB,
                    void* ZE, void* Y8, void* YE8, int M, int N, int K, int kid);
 
 /* ---- no reference counterpart: n raw-output GEMMs sharing K, in launches of up to 64. `entradas` is a HOST array of
- * n entries {const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad;} (device pointers inside); entry i
- * equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i). For the weight gradients of a step. */
+ * n entries {const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, compacto;} (device pointers inside); entry i
+ * equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i). For the weight gradients of a step.
+ * compacto = 1 (the same in every entry): Ce is an int16 vector of M + N, Ce[i] = RA_i and Ce[M + j] = RB_j - 4,
+ * whose sum is the exponent jt_gemm writes at (i, j) (2 bytes per value fewer written, and read by jt_otimizador). */
 int jt_gemm_lote(const void* entradas, int n, int kid);
 int jt_entrada_g_bytes(void);          /* sizeof of one entry (64) */
 /* ---- no reference counterpart: n weight-gradient GEMMs sharing K with momento + peso in the epilogue, in launches of
@@ -85,11 +87,12 @@ int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nbloc
 int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);
 
 /* ---- no reference counterpart: momento then peso for ntab tensors in one launch. `tabela` is a device array of
- * ntab entries {const int* gacc; const int16_t* ge; int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE; long long inicio, nblocos;}
- * sorted by inicio (the tensor's first block in a global numbering), ntab <= 256, nblocos = the total. Results equal jt_momento
- * followed by jt_peso on each tensor (ops.py:273-290). */
+ * ntab entries {const int* gacc; const int16_t* ge; int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE; long long inicio, nblocos;
+ * int M, N, compacto, pad;} sorted by inicio (the tensor's first block in a global numbering), ntab <= 256, nblocos =
+ * the total; compacto = 1: ge is jt_gemm_lote's compact exponent vector of the [M, N] gradient (N % 16 == 0), else one
+ * exponent per value. Results equal jt_momento followed by jt_peso on each tensor (ops.py:273-290). */
 int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid);
-int jt_tab_otim_bytes(void);           /* sizeof of one table entry (80) */
+int jt_tab_otim_bytes(void);           /* sizeof of one table entry (96) */
 
 /* ---- re-blocking, gathers (jatai_cuda.cu:1155-1166). transpoe: R % 128 == 0, C % 64 == 0. */
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid);

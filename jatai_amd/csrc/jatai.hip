@@ -211,7 +211,9 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
 
 // No reference counterpart: n raw-output GEMMs sharing K in launches of up to 64 (host array of EntradaG, device
 // pointers inside); entry i equals jt_gemm(A, EA, B, EB, NULL, NULL, C32, Ce, M, N, K, 1, kid + i).
-struct EntradaG { const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, pad; };
+// compacto = 1: Ce holds the exponents as the vectors Ce[i] = RA_i (i < M), Ce[M + j] = RB_j - 4 (M + N int16); the
+// raw exponent of (i, j) is their sum. All entries of a launch (64 at a time) share the setting.
+struct EntradaG { const void *A, *EA, *B, *EB; void *C32, *Ce; int M, N, K, compacto; };
 int jt_gemm_lote(const void* entradas, int n, int kid) {
     using namespace gemm;
     if (n < 0 || (n > 0 && !entradas)) return (int)hipErrorInvalidValue;
@@ -220,12 +222,14 @@ int jt_gemm_lote(const void* entradas, int n, int kid) {
         LoteG L;
         L.n = std::min(LOTE_G, n - base);
         L.K = e[base].K;
+        L.compacto = e[base].compacto;
         int r = 4;                                                   // the tallest forced tile every M of the group allows
         for (int i = 0; i < L.n; i++) r = std::min(r, gemm_r(e[base + i].M > 0 ? e[base + i].M : 32));
         long long tot = 0;
         for (int i = 0; i < L.n; i++) {
             const EntradaG& x = e[base + i];
             if (x.M <= 0 || x.N <= 0 || x.K != L.K || x.M % BM || x.N % BN || x.K % g_blk || !k_ok(x.K) || x.K <= 0) return (int)hipErrorInvalidValue;
+            if (x.compacto != L.compacto || (x.compacto != 0 && x.compacto != 1)) return (int)hipErrorInvalidValue;
             if (!alinhados(x.A, x.EA, x.B, x.EB, x.C32, x.Ce)) return (int)hipErrorInvalidValue;
             L.A[i] = (const int8_t*)x.A; L.EA[i] = (const int8_t*)x.EA; L.B[i] = (const int8_t*)x.B; L.EB[i] = (const int8_t*)x.EB;
             L.C32[i] = (int*)x.C32; L.Ce[i] = (int16_t*)x.Ce; L.M[i] = x.M; L.N[i] = x.N; L.ini[i] = (int)tot;

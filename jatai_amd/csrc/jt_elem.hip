@@ -260,11 +260,14 @@ __global__ void __launch_bounds__(256) k_zera32(int* __restrict__ p, long long n
 // same arithmetic as k_momento followed by k_peso, with Mom read once and the second launch gone.
 // The tensor list is a device table of TabOtim entries (fixed addresses: parameters, momenta, residuals and the
 // persistent raw-gradient buffers of the model); entry t covers global blocks [inicio_t, inicio_t + nblocos_t).
+// compacto = 1: ge holds the gradient's exponents as the vectors ge[i] = RA_i (i < M), ge[M + j] = RB_j - 4 of the
+// grouped GEMM's compact output (the exponent of (i, j) is their sum); else one int16 per value.
 struct TabOtim {
     const int* gacc;
     const int16_t* ge;
     int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE;
     long long inicio, nblocos;
+    int M, N, compacto, pad;
 };
 
 // momento then peso for NV consecutive values of one block, the block held by NL consecutive lanes: g raw with
@@ -373,6 +376,14 @@ __global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ 
     const OtimEnt<NVO> x = otim_le<NVO>(ot, o, w, ef);
     int g[NVO], eg[NVO];
     le_i32(d.gacc + o, g);
-    le_i16(d.ge + o, eg);
+    if (d.compacto) {                                               // 16 values of one row (N % 16 == 0)
+        const int row = (int)(o / d.N), col = (int)(o - (long long)row * d.N);
+        const int er = d.ge[row];
+        le_i16(d.ge + d.M + col, eg);
+#pragma unroll
+        for (int j = 0; j < NVO; j++) eg[j] = max(-30000, er + eg[j]);
+    } else {
+        le_i16(d.ge + o, eg);
+    }
     otim_valores<NVO, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid);
 }

@@ -64,7 +64,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                                            int* __restrict__ C32, int16_t* __restrict__ Ce, const int8_t* __restrict__ Xm,
                                            const int8_t* __restrict__ XE, int8_t* __restrict__ Om2, int8_t* __restrict__ OE2, int M, int N,
                                            int K, int kid, const int row0, const int col0, const Otim ot = Otim{}, int k_lr = 0,
-                                           int ef = 0, int est = 0, int ctab = 0) {
+                                           int ef = 0, int est = 0, int ctab = 0, int compacto = 0) {
     using gemm::BN;
     using gemm::PAD;
     using E = gemm::Est<BLK, R>;
@@ -407,6 +407,9 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     if constexpr (MODO == 1) {
         // raw output in 16-byte pieces: thread t writes columns 4 (t % 32) .. + 3 of rows t / 32 + 8 R k, k = 0 .. 3
         // (a wave: two rows of 512 contiguous bytes of C32 and 256 of Ce)
+        // compacto: the exponent of (i, j) is RA_i + RB_j - 4 (RA, RB maxima of int8 exponents, so never below the
+        // -30000 clamp), stored as the vectors Ce[i] = RA_i (i < M) and Ce[M + j] = RB_j - 4, written by the tiles of
+        // the first column and of the first row: 2 (M + N) bytes instead of 2 M N
         typedef short s4_t __attribute__((ext_vector_type(4)));
         if (tid < GT) {
             const int c = (tid & 31) * 4;
@@ -421,9 +424,14 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
                 for (int q = 1; q < KS; q++) t += *reinterpret_cast<const v4i*>(acc_s + q * TILE + r * (BN + PAD) + c);
                 const size_t oo = (size_t)(row0 + r) * N + col0 + c;
                 *reinterpret_cast<v4i*>(C32 + oo) = t;
+                if (compacto) continue;
                 const int ra = ra_s[r];
                 *reinterpret_cast<s4_t*>(Ce + oo) = s4_t{(short)max(-30000, ra + rbc[0]), (short)max(-30000, ra + rbc[1]),
                                                          (short)max(-30000, ra + rbc[2]), (short)max(-30000, ra + rbc[3])};
+            }
+            if (compacto) {
+                if (col0 == 0 && tid < BM) Ce[row0 + tid] = (short)ra_s[tid];
+                if (row0 == 0 && tid < BN) Ce[M + col0 + tid] = (short)(rb_s[tid] - 4);
             }
         }
         return;
@@ -577,8 +585,8 @@ __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_
 // Many raw-output GEMMs with one K in one launch (the weight gradients of a step: K = tokens). The list travels
 // by value in the kernel arguments; GEMM i owns the workgroups [ini_i, ini_{i+1}) of a 1-D grid, row-major over
 // its (M / 32 R) x (N / 128) tiles. Same tiles, same arithmetic as k_gemm<BLK, 1, KS, R>.
-constexpr int LOTE_G = 64;                  // 3852 bytes of kernel arguments: every weight gradient of a step in one launch
-static_assert(sizeof(int8_t*) * 6 * LOTE_G + sizeof(int) * (3 * LOTE_G + 3) <= 4096, "kernel argument limit");
+constexpr int LOTE_G = 64;                  // 3856 bytes of kernel arguments: every weight gradient of a step in one launch
+static_assert(sizeof(int8_t*) * 6 * LOTE_G + sizeof(int) * (3 * LOTE_G + 4) <= 4096, "kernel argument limit");
 struct LoteG {
     const int8_t* A[LOTE_G];
     const int8_t* EA[LOTE_G];
@@ -588,6 +596,7 @@ struct LoteG {
     int16_t* Ce[LOTE_G];
     int M[LOTE_G], N[LOTE_G], ini[LOTE_G + 1];
     int n, K;
+    int compacto;                           // exponents as row and column vectors (the mode-1 epilogue of gemm_corpo)
 };
 
 template <int BLK, int KS, int R = 1>
@@ -599,7 +608,7 @@ __global__ void __launch_bounds__(256 * R * KS) __attribute__((amdgpu_waves_per_
     const int local = t - L.ini[i], ntx = L.N[i] / gemm::BN;
     gemm_corpo<BLK, 1, KS, R, true>(L.A[i], L.EA[i], L.B[i], L.EB[i], nullptr, nullptr, L.C32[i], L.Ce[i], nullptr, nullptr, nullptr, nullptr,
                                     L.M[i], L.N[i], L.K, kid + i, (local / ntx) * 32 * R, (local % ntx) * gemm::BN, Otim{}, 0, 0, 0,
-                                    gemm::CTAB_LOTE);
+                                    gemm::CTAB_LOTE, L.compacto);
 }
 
 // The weight gradients of a step with the optimizer in the epilogue (mode 5): GEMM i's tile goes through

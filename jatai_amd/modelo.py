@@ -98,7 +98,10 @@ class Modelo:
         # ("gradientes dos pesos": the grouped weight-gradient launch), e.g. to split a capture into three graphs
         # so the stage can be timed between replays as the step runs it
         self.marcas = {}
-        self._gbuf, self._tabela = None, None
+        self._gbuf, self._tabela, self._gbuf_compacto = None, None, None
+        # the grouped weight-gradient launch writes the exponents of the fused optimizer's gradient buffers as row
+        # and column vectors (OpsHip)
+        self.grad_compacto = hasattr(ops, "gemm_cru_lote") and hasattr(ops, "otimizador")
 
     def _t_na_gemm(self, M, N):
         """Whether the ReLU^2-backward GEMM of M tokens x N columns writes its transpose too (see transposta_na_gemm)."""
@@ -116,10 +119,16 @@ class Modelo:
         return self.otim_no_gemm and self.otimizador_fundido and self.dw_em_lote and hasattr(self.ops, "gemm_otim_lote")
 
     def _prepara_otimizador(self):
-        if self._gbuf is None:
+        # With the grouped weight-gradient launch the gradient buffers take the compact exponent form (a vector of
+        # M + N: the exponent of (i, j) is RA_i + RB_j - 4), 2 bytes per value fewer written by the GEMM and read by
+        # the optimizer; a per-GEMM launch writes one exponent per value.
+        compacto = bool(self.dw_em_lote and self.grad_compacto)
+        if self._gbuf is None or self._gbuf_compacto != compacto:
             ordem = ["out"] + [f"{w}{l}" for l in reversed(range(self.L)) for w in ("Wd", "Wup", "Wo", "Wqkv")] + ["emb"]
+            fe = lambda t: (t.shape[0] + t.shape[1],) if compacto else t.shape
             self._gbuf = {n: (torch.empty(self.p[n][0].shape, dtype=torch.int32, device=self.dev),
-                              torch.empty(self.p[n][0].shape, dtype=torch.int16, device=self.dev)) for n in ordem}
+                              torch.empty(fe(self.p[n][0]), dtype=torch.int16, device=self.dev)) for n in ordem}
+            self._gbuf_compacto = compacto
             self._tabela = self.ops.tabela_otimizador([(self._gbuf[n], self.mom[n], self.p[n], self.res[n]) for n in ordem])
         return self._gbuf
 
@@ -277,7 +286,8 @@ class Modelo:
                 marca = self.marcas.get("gradientes dos pesos")
                 if marca:
                     marca[0]()
-                for (n, _, _), G in zip(adiados, ops.gemm_cru_lote([(A, B, gb[n] if gb else None) for n, A, B in adiados])):
+                for (n, _, _), G in zip(adiados, ops.gemm_cru_lote([(A, B, gb[n] if gb else None) for n, A, B in adiados],
+                                                                   compacto=bool(gb) and self._gbuf_compacto)):
                     grads[n] = G
                 if marca:
                     marca[1]()

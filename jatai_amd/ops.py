@@ -132,8 +132,10 @@ class OpsHip:
         return C
 
     # no reference counterpart: many raw GEMMs sharing K in one launch (64 per launch)
-    def gemm_cru_lote(self, pares):
-        """[gemm(A, B, cru=True, saida=S) for (A, B, S) in pares]; S may be None. Launch ids are consecutive."""
+    def gemm_cru_lote(self, pares, compacto=False):
+        """[gemm(A, B, cru=True, saida=S) for (A, B, S) in pares]; S may be None. Launch ids are consecutive.
+        compacto: each S[1] is an int16 vector of M + N holding the exponents as RA_i (first M) and RB_j - 4 (last N),
+        whose sum is the exponent of (i, j) -- the form the fused optimizer reads."""
         if not pares:
             return []
         if self._blk != BLK:
@@ -146,16 +148,17 @@ class OpsHip:
             self.reg.confere_bloco("A", A); self.reg.confere_bloco("B", B)
             (a, ea), (b, eb) = A, B
             M, N, K = self._formas_gemm("gemm", a, b)
+            fe = (M + N,) if compacto else (M, N)
             if S is None:
-                S = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(M, N, dtype=torch.int16, device=a.device))
+                S = (torch.empty(M, N, dtype=torch.int32, device=a.device), torch.empty(fe, dtype=torch.int16, device=a.device))
             self.reg.exige(S[0].dtype == torch.int32 and S[1].dtype == torch.int16 and tuple(S[0].shape) == (M, N)
-                           and tuple(S[1].shape) == (M, N) and S[0].is_contiguous() and S[1].is_contiguous(),
-                           f"gemm_cru_lote: saida deve ser (int32, int16) contiguos de forma {(M, N)}")
+                           and tuple(S[1].shape) == fe and S[0].is_contiguous() and S[1].is_contiguous(),
+                           f"gemm_cru_lote: saida deve ser (int32 {(M, N)}, int16 {fe}) contiguos")
             saidas.append(S)
             kid = self.reg.registra("gemm_cru", dict(A=a, EA=ea, B=b, EB=eb), (M, N), tempo=(i == 0))
             kid0 = kid if kid0 is None else kid0
             tab[8 * i:8 * i + 8] = [a.data_ptr(), ea.data_ptr(), b.data_ptr(), eb.data_ptr(), S[0].data_ptr(), S[1].data_ptr(),
-                                    (N << 32) | M, K]
+                                    (N << 32) | M, (int(compacto) << 32) | K]
         r = self.lib.jt_gemm_lote(ctypes.cast(tab, ctypes.c_void_p), ctypes.c_int(len(pares)), ctypes.c_int(kid0))
         self.reg.depois(kid0, r)
         return saidas
@@ -579,19 +582,29 @@ class OpsHip:
 
     # no reference counterpart: momento + peso of every tensor in one launch
     def tabela_otimizador(self, itens):
-        """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] with fixed addresses (updated in place)."""
+        """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] with fixed addresses (updated in place). A
+        gradient whose exponent tensor is a vector of M + N (gemm_cru_lote's compact form) is read as such."""
         itens = [tuple(it) for it in itens]
         linhas, inicio = [], 0
         for Gc, Mom, W, R in itens:
-            self.reg.confere_cru("grad", Gc)
+            compacto = Gc[1].dim() == 1 and Gc[0].dim() == 2
+            if compacto:
+                M, N = Gc[0].shape
+                self.reg.exige(Gc[0].dtype == torch.int32 and Gc[1].dtype == torch.int16 and Gc[1].numel() == M + N and Gc[0].is_cuda
+                               and Gc[0].is_contiguous() and Gc[1].is_contiguous() and N % 16 == 0,
+                               f"otimizador: gradiente compacto (int32 {(M, N)}, int16 {(M + N,)}) esperado")
+            else:
+                self.reg.confere_cru("grad", Gc)
+                M, N = (Gc[0].shape[0], Gc[0].numel() // Gc[0].shape[0]) if Gc[0].dim() >= 1 and Gc[0].shape[0] else (0, 0)
             for n, t in (("momento", Mom), ("W", W), ("residuo", R)):
                 self.reg.confere_bloco(n, t)
             nb = W[0].numel() // BLK
             self.reg.exige(Gc[0].numel() == W[0].numel() == Mom[0].numel() == R[0].numel(), "otimizador: formas diferentes")
-            linhas.append([t.data_ptr() for t in (Gc[0], Gc[1], Mom[0], Mom[1], W[0], W[1], R[0], R[1])] + [inicio, nb])
+            linhas.append([t.data_ptr() for t in (Gc[0], Gc[1], Mom[0], Mom[1], W[0], W[1], R[0], R[1])] + [inicio, nb]
+                          + [(N << 32) | M, int(compacto)])
             inicio += nb
         self.reg.exige(0 < len(linhas) <= 256, "otimizador: de 1 a 256 tensores")
-        self.reg.exige(self.lib.jt_tab_otim_bytes() == 80, "otimizador: tamanho de entrada da tabela inesperado")
+        self.reg.exige(self.lib.jt_tab_otim_bytes() == 96, "otimizador: tamanho de entrada da tabela inesperado")
         tab = torch.tensor(linhas, dtype=torch.int64).to(W[0].device)
         # the table keeps every tensor whose address it holds alive for as long as it exists
         return tab, len(linhas), inicio, tuple(t for it in itens for x in it for t in x)

@@ -95,6 +95,27 @@ def test_gemm_cru_lote_igual_a_gemm(blk, K):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"GEMM {i} {formas[i]}"
 
 
+@pytest.mark.parametrize("blk,K", [(32, 2048), (128, 2048), (32, 8192)])
+def test_gemm_cru_lote_compacto(blk, K):
+    """gemm_cru_lote with compact exponents: the same accumulators, and exponent vectors (RA_i, then RB_j - 4) whose
+    sums are the per-value exponents of the plain launch, in tiles of 32 and 128 rows."""
+    gpu = GPU(blk, vigiar=True)
+    formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(20)] + [(512, 2048), (2048, 512)]
+    pares = []
+    for i, (M, N) in enumerate(formas):
+        A = tuple(gpu.dev(a) for a in R.bloco(R.substream(9, f"A {i}"), M, K, blk, espalha=5, e0=-6))
+        B = tuple(gpu.dev(a) for a in R.bloco(R.substream(9, f"B {i}"), N, K, blk, espalha=5, e0=-9))
+        pares.append((A, B))
+    cheio = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares])
+    comp = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares], compacto=True)
+    torch.cuda.synchronize()
+    for i, ((M, N), a, b) in enumerate(zip(formas, cheio, comp)):
+        assert tuple(b[1].shape) == (M + N,)
+        assert torch.equal(a[0], b[0]), f"GEMM {i} {formas[i]}: accumulators"
+        e = b[1][:M].long()[:, None] + b[1][M:].long()[None, :]
+        assert torch.equal(a[1].long(), e.clamp(min=-30000)), f"GEMM {i} {formas[i]}: exponents"
+
+
 def test_modelo_dw_em_lote():
     import traco as TR
     from jatai_amd import ops as O

@@ -116,9 +116,13 @@ def test_erro_no_grafo():
         OpsOraculo(128).embed(W, salvo["tok"])
 
 
-@pytest.mark.parametrize("dw_lote", [True, False], ids=["otimizador-no-gemm", "tabela"])
+@pytest.mark.parametrize("dw_lote,compacto", [(True, True), (False, True), (False, False)],
+                         ids=["otimizador-no-gemm", "tabela", "tabela-expoente-por-valor"])
 @pytest.mark.parametrize("ef", [True, False])
-def test_otimizador_fundido_igual_por_tensor(ef, dw_lote):
+def test_otimizador_fundido_igual_por_tensor(ef, dw_lote, compacto):
+    """The fused optimizer (one launch over the table of all tensors, reading the gradient exponents in the grouped
+    GEMM's compact form or one per value; or inside the grouped GEMM's epilogue) equals momento then peso per
+    tensor."""
     from jatai_amd.modelo import Modelo
     g = TR.gold()
     f = g["forma"]
@@ -127,6 +131,7 @@ def test_otimizador_fundido_igual_por_tensor(ef, dw_lote):
     fundido, separado = mk(), mk()
     separado.otimizador_fundido = False
     fundido.otim_no_gemm = dw_lote                  # True: momento + peso in the grouped GEMM's epilogue
+    fundido.grad_compacto = compacto
     assert fundido.otimizador_fundido and fundido._otim_no_gemm() == dw_lote
     for m in (fundido, separado):
         m.error_feedback = ef
@@ -138,3 +143,5 @@ def test_otimizador_fundido_igual_por_tensor(ef, dw_lote):
         assert a == b, (p, a, b)
     reg.fim_passo()
     assert _estado(fundido) == _estado(separado)
+    if not dw_lote:
+        assert fundido._gbuf_compacto == compacto
