@@ -182,11 +182,11 @@ def mede_dw_lote(O, ops, c, rep=7):
                 (e0 + torch.randint(-3, 4, (R, C // blk), generator=g)).to(torch.int8).cuda())
     formas, K = formas_dw(c)
     pares, fontes = [], []
-    for _, M, N in formas:
+    for _, M, N in formas:                  # the exponents in the compact form the step's launch writes
         pares.append((bloco(M, K, -20), bloco(N, K, -6),
-                      (torch.empty(M, N, dtype=torch.int32, device="cuda"), torch.empty(M, N, dtype=torch.int16, device="cuda"))))
+                      (torch.empty(M, N, dtype=torch.int32, device="cuda"), torch.empty(M + N, dtype=torch.int16, device="cuda"))))
         fontes.append((tuple(t.clone() for t in pares[-1][0]), tuple(t.clone() for t in pares[-1][1])))
-    f = lambda: ops.gemm_cru_lote(pares)
+    f = lambda: ops.gemm_cru_lote(pares, compacto=True)
     f()
     torch.cuda.synchronize()
     grafo = torch.cuda.CUDAGraph()
@@ -531,11 +531,11 @@ def trafego_despacha(O, ops, c):
             chama()
             torch.cuda.synchronize()
         print(f"dispatch: {nome} {gemm_kernel(O, ops, M, N, K, modo)['symbol']} x2", flush=True)
-    # the step's grouped weight-gradient launch (its dominant kernel), twice
+    # the step's grouped weight-gradient launch (its dominant kernel, exponents in the compact form), twice
     formas, K = formas_dw(c)
     pares = [(bloco(M, K, -20), bloco(N, K, -6), None) for _, M, N in formas]
     for _ in range(2):
-        ops.gemm_cru_lote(pares)
+        ops.gemm_cru_lote(pares, compacto=True)
         torch.cuda.synchronize()
     print(f"dispatch: dW grouped k_gemm_lote<{blk}, 1, 1> x2", flush=True)
 
