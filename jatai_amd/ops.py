@@ -595,7 +595,7 @@ class OpsHip:
                                f"otimizador: gradiente compacto (int32 {(M, N)}, int16 {(M + N,)}) esperado")
             else:
                 self.reg.confere_cru("grad", Gc)
-                M, N = (Gc[0].shape[0], Gc[0].numel() // Gc[0].shape[0]) if Gc[0].dim() >= 1 and Gc[0].shape[0] else (0, 0)
+                M = N = 0                                   # read only for the compact form
             for n, t in (("momento", Mom), ("W", W), ("residuo", R)):
                 self.reg.confere_bloco(n, t)
             nb = W[0].numel() // BLK
