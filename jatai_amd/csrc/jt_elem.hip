@@ -272,7 +272,7 @@ struct TabOtim {
 
 // momento then peso for NV consecutive values of one block, the block held by NL consecutive lanes: g raw with
 // exponents eg; o = offset of the first value in the tensor, w = its block, lider = the block's first lane. Used by
-// k_otimizador (NV = 8) and by the weight-gradient GEMM's epilogue (NV = 16).
+// k_otimizador and by the weight-gradient GEMM's epilogue (NV = 16 in both).
 struct Otim {
     int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE;
 };
