@@ -55,7 +55,8 @@ int jt_gemm(const void* A, const void* EA, const void* B, const void* EB, void* 
             int M, int N, int K, int modo, int kid);
 /* no reference counterpart: Z16 = soma16(X16, A.B^T) (R16, int16 mantissas) and Y8 = para8(Z16) in one launch, the
  * bits of jt_gemm (modo 0), jt_soma16 and jt_para8 in turn (the R16 step's residual add, modelo.py:67-72, 78-84).
- * X16, Z16 int16 [M,N]; XE, ZE, YE8 int8 [M,N/BLK]; Y8 int8 [M,N]. Shapes as jt_gemm_f. */
+ * X16, Z16 int16 [M,N]; XE, ZE, YE8 int8 [M,N/BLK]; Y8 int8 [M,N]. Shapes as jt_gemm_f. Launch ids: kid for the GEMM,
+ * kid + 1 for the soma16 stage, kid + 2 for the para8 stage. */
 int jt_gemm_soma16(const void* A, const void* EA, const void* B, const void* EB, const void* X16, const void* XE, void* Z16,
                    void* ZE, void* Y8, void* YE8, int M, int N, int K, int kid);
 

@@ -306,7 +306,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     // the ALiBi term (i - j) << incl of key j = l + LPR k is ab - k (LPR << incl) (shifts distribute over the
     // subtraction in 32-bit arithmetic); the score's rounding shift su is one per head: for su >= 0 one FMA (Desl,
     // exact for |score| < 2^26), a left shift (checked) otherwise
-    const int ab = (ii - l) << incl, pa = LPR << incl;
+    const int ab = (ii - l) * (1 << incl), pa = LPR << incl;         // ii - l may be negative: no left shift of it
     const bool direita = su >= 0;
     const Desl dsu(su);
     int u[NJ], mx = U_MIN;

@@ -119,9 +119,9 @@ __device__ __forceinline__ void exp_tab_lds(unsigned short* t) {
     for (int c = threadIdx.x; c < EXP_N / 8; c += blockDim.x)
         reinterpret_cast<int4*>(t)[c] = reinterpret_cast<const int4*>(TAB_EXP.v)[c];
 }
-// exp_dif(mx, u) >> 3 from the table for u <= mx: the difference as unsigned is exact (below 2^32) however far
-// apart mx and u are, and every difference from EXP_D0 on reads the final 0 (an index never leaves the table)
-__device__ __forceinline__ int exp_tab(const unsigned short* t, int mx, int u) { return t[min((unsigned)(mx - u), (unsigned)EXP_D0)]; }
+// exp_dif(mx, u) >> 3 from the table for u <= mx: the difference, taken in unsigned arithmetic (no signed
+// overflow), is exact (below 2^32) however far apart mx and u are, and every difference from EXP_D0 on reads the final 0 (an index never leaves the table)
+__device__ __forceinline__ int exp_tab(const unsigned short* t, int mx, int u) { return t[min((unsigned)mx - (unsigned)u, (unsigned)EXP_D0)]; }
 
 // The spec's isqrt (ops.py:84-89: 10 Newton steps from 2^ceil(bitlen(n)/2)) is floor(sqrt(n)) for every
 // 1 <= n < 2^31 (checked over all of them) and 1 for n <= 0. Here: a float square root, within 0.01 of sqrt(n) for

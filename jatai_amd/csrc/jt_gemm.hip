@@ -481,14 +481,14 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             int s[16], q[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) s[j] = (dx(xin[j]) & mx) + (dm((int)m[j]) & mm);
-            const int Ez = quant_u<16, LPB, true, 15, 32767>(s, ec, q, kid, (long long)o);
+            const int Ez = quant_u<16, LPB, true, 15, 32767>(s, ec, q, kid + 1, (long long)o);   // soma16's launch id
             int16_t z[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) z[j] = (int16_t)q[j];
             grava_i16(reinterpret_cast<int16_t*>(Cm) + o, z);
             if (lider) CE[oe] = (int8_t)Ez;
             int8_t y[16];
-            const int Ey = quant8_u8<16, LPB>(q, (int)(int8_t)Ez, y, kid, (long long)o);
+            const int Ey = quant8_u8<16, LPB>(q, (int)(int8_t)Ez, y, kid + 2, (long long)o);     // para8's launch id
             grava_i8(Om2 + o, y);
             if (lider) OE2[oe] = (int8_t)Ey;
         }

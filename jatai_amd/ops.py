@@ -335,8 +335,16 @@ class OpsHip:
         reg.exige(tuple(X16[0].shape) == (M, N), f"gemm_soma16: x16 com forma {tuple(X16[0].shape)}, esperado {(M, N)}")
         Z = (torch.empty(M, N, dtype=torch.int16, device=a.device), torch.empty(M, N // BLK, dtype=torch.int8, device=a.device))
         Y = self._novo_bloco(M, N, a.device)
-        self._lanca("gemm_soma16", "jt_gemm_soma16", (a, ea, b, eb, X16[0], X16[1], Z[0], Z[1], Y[0], Y[1], M, N, K),
-                    dict(A=a, EA=ea, B=b, EB=eb, x16=X16[0], xE=X16[1]), (M, N))
+        if self._blk != BLK:
+            self.reg.exige(self.lib.jt_bloco(BLK) == 0, f"BLK={BLK} not supported (32 or 128)")
+            self._blk = BLK
+        # launch ids: kid the GEMM, kid + 1 its soma16 stage, kid + 2 its para8 stage (a device event names its stage)
+        kid = self.reg.registra("gemm_soma16", dict(A=a, EA=ea, B=b, EB=eb, x16=X16[0], xE=X16[1]), (M, N))
+        self.reg.registra("soma16", dict(x16=X16[0], xE=X16[1]), (M, N), tempo=False)
+        self.reg.registra("para8", dict(), (M, N), tempo=False)
+        r = self.lib.jt_gemm_soma16(*[self._a(t) for t in (a, ea, b, eb, X16[0], X16[1], Z[0], Z[1], Y[0], Y[1])], M, N, K,
+                                    ctypes.c_int(kid))
+        self.reg.depois(kid, r)
         return Z, Y
 
     def relu2(self, Hh):

@@ -11,8 +11,14 @@
 //   gemm (blk 32 / 128), quant, soma, relu2, relu2_back, transpoe, embed, um_quente, rms, rms_back,
 //   atencao / atencao_back (hd = 4), softmax_ce, momento, peso ...... reference golden vectors
 //                                        (ops_blk128.json, ops_blk32.json, config1.json, trace_r.json)
-//   atencao / atencao_back at hd > 4 (declared extension) ...... parity unpinned beyond the hd = 4 reduction
-//   para16 / para8 / soma16 ............ invariants only (exact round trip, float64 error bound): parity unpinned
+//   atencao / atencao_back at hd > 4 (declared extension) ...... reduction to the golden-pinned hd = 4 code with
+//                                        the data in dims 0-3, 32-35 or 60-63 (the head's second block, its first
+//                                        all-zero); q = 0 (ALiBi alone) and one-hot keys (forward closed forms);
+//                                        v = 0 (gq = gk = 0, gv = P^T dO over all 64 dims, closed form and float
+//                                        bound); head-dimension permutation equivariance across both blocks
+//   para16 / para8 / soma16 (no spec) ... closed forms on exact integers (test_r16_formas_fechadas)
+//   soma_est (no spec) .................. lowbias32 pinned by its published inverse; the seed layout restates
+//                                        jatai_cuda.cu:375 and no vector can pin it: parity unpinned
 //
 // All arithmetic is int64 with two's-complement wraparound where the spec's torch int64 tensors wrap.
 #include <cstdint>

@@ -3,6 +3,7 @@ the CPU oracle's generalized restatement (jatai_oracle.cpp, which reduces to the
 the golden fixtures). Bit-exact: P, the raw output (acc, e), and the backward's raw (acc, e) in both variants.
 The generalization has no reference counterpart; test_atencao_hd64_reduz_ao_spec_hd4 pins it to the spec's
 head-width-4 arithmetic on inputs where the two problems coincide (T <= 128)."""
+import numpy as np
 import pytest
 import torch
 
@@ -13,7 +14,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _cmp(a, b, nome):
-    d = primeira_diferenca(host(a), host(b))
+    a, b = (x if isinstance(x, np.ndarray) else host(x) for x in (a, b))
+    d = primeira_diferenca(a, b)
     assert d is None, f"{nome}: (flat index, gpu, oracle, count) = {d}"
 
 
@@ -116,14 +118,70 @@ def test_atencao_qs_igual_a_q(T, H, limite):
         _cmp(a, b, nome)
 
 
+def _frente_tras(be, qn, gn, Bt, T, H, limite):
+    """(oacc, oe, P, gacc, ge) of one forward and backward on a backend, as host arrays."""
+    qkv = tuple(be.dev(v) for v in qn)
+    go = tuple(be.dev(v) for v in gn)
+    old = be.limite(limite)
+    try:
+        (oacc, oe), P = be.ops.atencao(qkv, Bt, T, H)
+        gacc, ge = be.ops.atencao_back(go, qkv, P, Bt, T, H)
+    finally:
+        be.limite(old)
+    return [host(x) for x in (oacc, oe, P, gacc, ge)]
+
+
 @pytest.mark.parametrize("limite", [False, True])
-def test_atencao_hd64_reduz_ao_spec_hd4(limite, via_ws):
-    """The head-width-64 kernels on inputs where each head carries one head-width-4 head of the spec's shape
-    (tests/reducoes.py) give that head's outputs as the oracle's head-width-4 code computes them -- the code the
+def test_atencao_hd64_tras_v_zero(limite, via_ws):
+    """Config 4's attention shape with v = 0 and q, k, dO random in every dimension of both blocks
+    (tests/reducoes.py, family 2): each kernel family gives gq = gk = 0 and gv = sum_i P_ij a_i over all 64
+    dimensions (the closed form), and every output equals the oracle's."""
+    import reducoes as RD
+    Bt, T, H = 2, 256, 8
+    qn, gn = RD.problema_v_zero(7310, Bt, T)
+    g = _frente_tras(GPU(32, vigiar=True), qn, gn, Bt, T, H, limite)
+    c = _frente_tras(CPU(32), qn, gn, Bt, T, H, limite)
+    acc = g[3].astype(np.int64)
+    assert not np.any(acc[:, :2 * RD.D64]), "gq, gk must be 0"
+    gv, _ = RD.gv_v_zero(gn, g[2], Bt, T)
+    assert np.array_equal(acc[:, 2 * RD.D64:], gv), "gv closed form"
+    for nome, a, b in zip(("oacc", "oe", "P", "gacc", "ge"), g, c):
+        _cmp(a, b, nome)
+
+
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_permutacao(limite, via_ws):
+    """Config 4's attention shape with one exponent per (token, head) on both blocks (tests/reducoes.py, family 3):
+    permuting each head's q, k dimensions by pi and v, dO dimensions by sigma permutes each kernel family's o, gv
+    by sigma and gq, gk by pi and leaves P unchanged, bit for bit; the unpermuted outputs equal the oracle's."""
+    import reducoes as RD
+    Bt, T, H, D = 2, 256, 8, 512
+    (qn, gn), (qp, gp), pi, sigma = RD.problema_permutado(7311, Bt, T)
+    gpu = GPU(32, vigiar=True)
+    a = _frente_tras(gpu, qn, gn, Bt, T, H, limite)
+    b = _frente_tras(gpu, qp, gp, Bt, T, H, limite)
+    c = _frente_tras(CPU(32), qn, gn, Bt, T, H, limite)
+    for nome, x, y in zip(("oacc", "oe", "P", "gacc", "ge"), a, c):
+        _cmp(x, y, nome)
+    _cmp(b[2], a[2], "P permuted")
+    _cmp(b[0], RD.permuta_colunas(a[0], sigma, D, 0), "o permuted")
+    _cmp(b[1], RD.permuta_colunas(a[1], sigma, D, 0), "o exponents permuted")
+    for i, nome in ((3, "acc"), (4, "e")):
+        y = RD.permuta_colunas(RD.permuta_colunas(RD.permuta_colunas(a[i], pi, D, 0), pi, D, 1), sigma, D, 2)
+        _cmp(b[i], y, f"backward {nome} permuted")
+    assert np.count_nonzero(a[3][:, :2 * D]) > 0.5 * a[3][:, :2 * D].size
+
+
+@pytest.mark.parametrize("desloc", [0, 32, 60])
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_reduz_ao_spec_hd4(limite, desloc, via_ws):
+    """The head-width-64 kernels on inputs where each head carries one head-width-4 head of the spec's shape in its
+    dimensions desloc .. desloc + 3 (tests/reducoes.py, family 1; from 32 on in the head's second block, the first
+    all-zero) give that head's outputs as the oracle's head-width-4 code computes them -- the code the
     reference's goldens pin (ops.py:186-258): P, o, and the backward's gq, gk, gv."""
     import reducoes as RD
     Bt, T = 2, 128
-    (q4, g4), (q64, g64) = RD.problemas(5151, Bt, T)
+    (q4, g4), (q64, g64) = RD.problemas(5151 + desloc, Bt, T, desloc)
     cpu = CPU(32)
     gpu = GPU(32, vigiar=True)
     Q4, G4 = (tuple(cpu.dev(v) for v in x) for x in (q4, g4))
@@ -137,5 +195,5 @@ def test_atencao_hd64_reduz_ao_spec_hd4(limite, via_ws):
     finally:
         cpu.limite(old_c)
         gpu.limite(old_g)
-    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt)
-    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64])
+    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt, desloc)
+    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64], desloc)

@@ -95,20 +95,33 @@ def test_gemm_cru_lote_igual_a_gemm(blk, K):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"GEMM {i} {formas[i]}"
 
 
-@pytest.mark.parametrize("blk,K", [(32, 2048), (128, 2048), (32, 8192)])
-def test_gemm_cru_lote_compacto(blk, K):
+@pytest.mark.parametrize("blk,K,bm", [(32, 2048, 0), (128, 2048, 0), (32, 8192, 0), (32, 2048, 64), (32, 2048, 128),
+                                      (128, 2048, 128), (32, 8192, 128)])
+def test_gemm_cru_lote_compacto(blk, K, bm):
     """gemm_cru_lote with compact exponents: the same accumulators, and exponent vectors (RA_i, then RB_j - 4) whose
-    sums are the per-value exponents of the plain launch, in tiles of 32 and 128 rows."""
+    sums are the per-value exponents of the plain launch. bm = 0: ragged M (multiples of 32), so the group runs
+    32-row tiles; bm = 64 / 128 (jt_gemm_bm): every M a multiple of 128, so the group runs 64- or 128-row tiles and
+    the compact epilogue writes RA for 64 or 128 rows per tile."""
     gpu = GPU(blk, vigiar=True)
-    formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(20)] + [(512, 2048), (2048, 512)]
+    if bm == 0:
+        formas = [(32 * (1 + i % 5), 128 * (1 + i % 3)) for i in range(20)] + [(512, 2048), (2048, 512)]
+    else:
+        formas = [(128 * (1 + i % 4), 128 * (1 + i % 3)) for i in range(12)] + [(512, 2048), (2048, 512)]
     pares = []
     for i, (M, N) in enumerate(formas):
         A = tuple(gpu.dev(a) for a in R.bloco(R.substream(9, f"A {i}"), M, K, blk, espalha=5, e0=-6))
         B = tuple(gpu.dev(a) for a in R.bloco(R.substream(9, f"B {i}"), N, K, blk, espalha=5, e0=-9))
         pares.append((A, B))
-    cheio = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares])
-    comp = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares], compacto=True)
-    torch.cuda.synchronize()
+    try:
+        gpu.ops.lib.jt_gemm_bm(bm)
+        cheio = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares])
+        comp = gpu.ops.gemm_cru_lote([(A, B, None) for A, B in pares], compacto=True)
+        torch.cuda.synchronize()
+    finally:
+        gpu.ops.lib.jt_gemm_bm(0)
+    ref = [gpu.ops.gemm(A, B, cru=True) for A, B in pares]          # the single-GEMM path at the automatic tile
+    for i, (a, b) in enumerate(zip(cheio, ref)):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), f"GEMM {i} {formas[i]}: grouped vs single"
     for i, ((M, N), a, b) in enumerate(zip(formas, cheio, comp)):
         assert tuple(b[1].shape) == (M + N,)
         assert torch.equal(a[0], b[0]), f"GEMM {i} {formas[i]}: accumulators"

@@ -372,24 +372,95 @@ def test_r16_formas_fechadas(blk):
         assert list(pm[r * C:(r + 1) * C]) == mq and list(pE[r * (C // blk):(r + 1) * (C // blk)]) == Eq, f"para8 row {r}"
 
 
+@pytest.mark.parametrize("desloc", [0, 32, 60])
 @pytest.mark.parametrize("limite", [False, True])
-def test_atencao_hd64_reduz_ao_spec_hd4(limite):
+def test_atencao_hd64_reduz_ao_spec_hd4(limite, desloc):
     """The head-width-64 attention (the declared extension run at configs 4 and 5) on inputs where each head
-    carries one head-width-4 head of the spec's shape (tests/reducoes.py) gives that head's outputs: P, o and,
-    in the backward (both variants), gq, gk, gv. The head-width-4 side is the oracle code the reference's goldens
-    pin (ops.py:186-258). This pins the extension's alignment over a head's blocks, its score shift
-    -(log2 hd)/2, its ALiBi schedule 8 - 8h/H and its backward at T <= 128."""
+    carries one head-width-4 head of the spec's shape in its dimensions desloc .. desloc + 3 (tests/reducoes.py,
+    family 1) gives that head's outputs: P, o and, in the backward (both variants), gq, gk, gv. The head-width-4
+    side is the oracle code the reference's goldens pin (ops.py:186-258). This pins the extension's alignment
+    over a head's blocks (desloc 32 and 60: the data in the head's second block, its first block all-zero), its
+    score shift -(log2 hd)/2, its ALiBi schedule 8 - 8h/H and its backward at T <= 128."""
     import reducoes as RD
     Bt, T = 2, 128
     ops = OpsOraculo(32, limite=limite)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
-    (q4, g4), (q64, g64) = RD.problemas(5150, Bt, T)
+    (q4, g4), (q64, g64) = RD.problemas(5150 + desloc, Bt, T, desloc)
     Q4, G4, Q64, G64 = [tuple(t(v) for v in x) for x in (q4, g4, q64, g64)]
     f4, f64 = ops.atencao(Q4, Bt, T, RD.H4), ops.atencao(Q64, Bt, T, RD.H64)
-    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt)
+    RD.confere_frente([[host(x) for x in f4[0]], host(f4[1])], [[host(x) for x in f64[0]], host(f64[1])], Bt, desloc)
     b4 = ops.atencao_back(G4, Q4, f4[1], Bt, T, RD.H4)
     b64 = ops.atencao_back(G64, Q64, f64[1], Bt, T, RD.H64)
-    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64])
+    RD.confere_tras([host(x) for x in b4], [host(x) for x in b64], desloc)
+
+
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_tras_v_zero(limite):
+    """Head width 64 at config 4's shape (8 heads x 64, T = 256, BLK = 32) with v = 0 and q, k, dO random in all
+    64 dimensions of both blocks (tests/reducoes.py, family 2). Then gP = dO v^T = 0, so s_lin = dS = 0 and
+    (ops.py:221-258, both variants):
+      * gq = gk = 0 exactly, at exponents eds + ek and eds + eq with eds = ego + ev - 9 (both shrink counts 0);
+      * gv_j = sum_i P_ij a_i over every dimension, a = dO aligned to the head's largest block exponent over
+        both blocks and T tokens (exact half-even rounding), at exponent ego - 8;
+      * and, independently of any rounding rule, gv 2^(ego - 8) is within sum_i P_ij 2^(ego - 1) / 256 of the
+        exact sum_i (P_ij / 256) dO_i (each aligned value is within half its ulp 2^ego of dO_i)."""
+    import reducoes as RD
+    Bt, T, H, D, blk, GA = 2, 256, 8, 512, 32, 4
+    (qm, qE), (gm, gE) = RD.problema_v_zero(7310, Bt, T)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    ops = OpsOraculo(blk, limite=limite)
+    _, P = ops.atencao((t(qm), t(qE)), Bt, T, H)
+    acc, e = (host(x).astype(np.int64) for x in ops.atencao_back((t(gm), t(gE)), (t(qm), t(qE)), P, Bt, T, H))
+    P = host(P)
+    assert np.count_nonzero(P) > Bt * H * T                     # P is not trivial
+    assert not np.any(acc[:, :2 * D]), "gq, gk must be 0"
+    gv, expo = RD.gv_v_zero((gm, gE), P, Bt, T)
+    assert np.array_equal(acc[:, 2 * D:], gv), "gv"
+    assert np.count_nonzero(gv[:, 64 * np.arange(H)[:, None] + np.arange(4, 64)[None, :]]) > 0.9 * Bt * T * H * 60
+    Pb = P.astype(np.int64).reshape(Bt, H, T, T)
+    qE64, gE64 = qE.astype(np.int64), gE.astype(np.int64)
+    for b in range(Bt):
+        rows = slice(b * T, (b + 1) * T)
+        for h in range(H):
+            cols = slice(64 * h, 64 * (h + 1))
+            emx = lambda E, part: int(E[rows, part * (D // blk) + 2 * h:part * (D // blk) + 2 * h + 2].max())
+            ego, eq, ek, ev = emx(gE64, 0) - GA, emx(qE64, 0) - GA, emx(qE64, 1) - GA, -127 - GA
+            eds = ego + ev - 9
+            assert ev == emx(qE64, 2) - GA
+            assert np.all(e[rows, cols] == eds + ek) and np.all(e[rows, D:][:, cols] == eds + eq), (b, h, "gq/gk e")
+            assert np.all(e[rows, 2 * D:][:, cols] == expo[b, h]) and expo[b, h] == ego - 8, (b, h, "gv e")
+            # float bound (exact in float64: 256 terms of 2^15 x 2^E over a 12-step exponent range)
+            x = gm[rows, cols].astype(np.float64) * np.exp2(np.repeat(gE64[rows, 2 * h:2 * h + 2], blk, 1))
+            exato = Pb[b, h].astype(np.float64) @ x / 256.0
+            folga = Pb[b, h].sum(1).astype(np.float64)[:, None] * 2.0 ** (ego - 1) / 256.0
+            assert np.all(np.abs(gv[rows, cols] * 2.0 ** (ego - 8) - exato) <= folga), (b, h, "gv bound")
+
+
+@pytest.mark.parametrize("limite", [False, True])
+def test_atencao_hd64_permutacao(limite):
+    """Head width 64 at config 4's shape with one exponent per (token, head) on both blocks of q, k, v and dO
+    (tests/reducoes.py, family 3): permuting every head's q and k dimensions jointly by pi[h] and its v and dO
+    dimensions by sigma[h] (across both blocks) leaves P unchanged and permutes o and gv by sigma and gq, gk by
+    pi, values and exponents, bit for bit, in both backward variants. An oracle that drops, repeats or
+    misindexes any dimension of 4 .. 63, or treats the second block differently, fails it."""
+    import reducoes as RD
+    Bt, T, H, D, blk = 2, 256, 8, 512, 32
+    (qkv, go), (qkv_p, go_p), pi, sigma = RD.problema_permutado(7311, Bt, T)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    ops = OpsOraculo(blk, limite=limite)
+    saidas = []
+    for q, g in ((qkv, go), (qkv_p, go_p)):
+        (oacc, oe), P = ops.atencao(tuple(t(v) for v in q), Bt, T, H)
+        ga, ge = ops.atencao_back(tuple(t(v) for v in g), tuple(t(v) for v in q), P, Bt, T, H)
+        saidas.append([host(x) for x in (oacc, oe, P, ga, ge)])
+    (oa, oe, P, ga, ge), (oa_p, oe_p, P_p, ga_p, ge_p) = saidas
+    assert np.array_equal(P, P_p), "P"
+    assert np.array_equal(oa_p, RD.permuta_colunas(oa, sigma, D, 0)), "o"
+    assert np.array_equal(oe_p, RD.permuta_colunas(oe, sigma, D, 0)), "o exponents"
+    for x, x_p, nome in ((ga, ga_p, "acc"), (ge, ge_p, "e")):
+        y = RD.permuta_colunas(RD.permuta_colunas(RD.permuta_colunas(x, pi, D, 0), pi, D, 1), sigma, D, 2)
+        assert np.array_equal(x_p, y), f"backward {nome}"
+    assert np.count_nonzero(ga[:, :2 * D]) > 0.5 * ga[:, :2 * D].size    # dS is not trivial
 
 
 def test_atencao_hd64_q_zero_so_alibi():

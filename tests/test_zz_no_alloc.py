@@ -73,10 +73,19 @@ def test_sem_alocar_igual_ao_workspace(limite):
 
 
 def test_sem_alocar_recusa_acima_do_maximo():
+    """Every buffer at its real size for the shape (so a broken guard could not touch memory it does not own), the
+    matrix-core family selected (the path that reaches the size check), and the outputs left as filled."""
     lib = _lib()
     assert lib.jt_bloco(32) == 0
+    lib.jt_atencao_mfma(1)
     Bt, T, H, D = 64, 256, 8, 512                    # config 5: about 66 MB of workspace
+    M = Bt * T
     assert lib.jt_atencao_back_ws_bytes(Bt, T, H, D) > lib.jt_scratch_bytes()
-    t = torch.zeros(16, dtype=torch.int8, device="cuda")
-    rc = lib.jt_atencao_back_sem_alocar(_p(t), _p(t), _p(t), _p(t), _p(t), _p(t), _p(t), Bt, T, H, D, 4, 0, 0)
+    q, g = _entradas(R.substream(809, "recusa"), Bt, T, H, D)
+    P = torch.zeros(Bt * H, T, T, dtype=torch.uint8, device="cuda")
+    acc = torch.full((M, 3 * D), 7, dtype=torch.int32, device="cuda")
+    e = torch.full((M, 3 * D), 7, dtype=torch.int16, device="cuda")
+    rc = lib.jt_atencao_back_sem_alocar(_p(g[0]), _p(g[1]), _p(q[0]), _p(q[1]), _p(P), _p(acc), _p(e), Bt, T, H, D, 4, 0, 0)
+    torch.cuda.synchronize()
     assert rc == HIP_ERROR_OUT_OF_MEMORY
+    assert bool((acc == 7).all()) and bool((e == 7).all())
