@@ -245,6 +245,44 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         __syncthreads();
         desloca_tab(nb, sst1);
     };
+    // one chunk whose exponent rows are whole 16-byte vectors, at most 8 per row (K <= 4096): no staging. A row is
+    // taken by LR = 1, 2, 4 or 8 consecutive lanes (the power of two at or above its nb / 16 vectors), each loading
+    // one vector into registers; the row maximum is a reduction over those lanes, and each lane writes its 16 table
+    // entries (and the maximum) straight into LDS. All loads are issued before the first reduction. One barrier
+    // (the caller's, after the first stage's store) publishes the tables instead of three.
+    auto tabelas_diretas = [&]() {
+        const int q = nb / 16, LR = q <= 1 ? 1 : q <= 2 ? 2 : q <= 4 ? 4 : 8;
+        const int itens = (BM + BN) * LR, NT = GT * KS;
+        constexpr int KMAX = ((32 * R + 128) * 8 + 256 * R * KS - 1) / (256 * R * KS);   // rounds for LR = 8: 5 at most
+        int4 t[KMAX];
+#pragma unroll
+        for (int k = 0; k < KMAX; k++) {
+            const int it = tid + k * NT, row = it / LR, j = it % LR;
+            t[k] = make_int4(0x80808080, 0x80808080, 0x80808080, 0x80808080);   // -128: neutral for the maximum
+            if (it < itens && j < q)
+                t[k] = *reinterpret_cast<const int4*>((row < BM ? EA + (size_t)(row0 + row) * nb : EB + (size_t)(col0 + row - BM) * nb) + 16 * j);
+        }
+#pragma unroll
+        for (int k = 0; k < KMAX; k++) {
+            if (k * NT >= itens) break;                              // uniform
+            const int it = tid + k * NT, row = it / LR, j = it % LR;
+            int m = max(max(max_i8x4(t[k].x), max_i8x4(t[k].y)), max(max_i8x4(t[k].z), max_i8x4(t[k].w)));
+            m = LR == 1 ? m : LR == 2 ? g_max<2>(m) : LR == 4 ? g_max<4>(m) : g_max<8>(m);
+            if (it >= itens || j >= q) continue;
+            const int w4[4] = {t[k].x, t[k].y, t[k].z, t[k].w};
+            if (row < BM) {
+                if (j == 0) ra_s[row] = m;
+                const int ra4 = 4 - m;
+#pragma unroll
+                for (int u = 0; u < 16; u++) na_s[(16 * j + u) * BM + row] = max((int)(int8_t)(w4[u >> 2] >> (8 * (u & 3))) + ra4, -100);
+            } else {
+                const int c = row - BM;
+                if (j == 0) rb_s[c] = m;
+#pragma unroll
+                for (int u = 0; u < 16; u++) nb_s[(16 * j + u) * BN + c] = (int8_t)max((int)(int8_t)(w4[u >> 2] >> (8 * (u & 3))) - m, -100);
+            }
+        }
+    };
     // several chunks: 160 row segments of nbc bytes (a multiple of 16) at column b0 of rows of nb bytes, one
     // 16-byte vector at a time (this runs between chunks, with the accumulators live)
     auto tabelas_parte = [&](int b0, int nbc) {
@@ -267,7 +305,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // chunk 0, before the accumulators are live: its first two stages in flight during the exponent staging
     if (g < min(ns, NBC / BPS)) busca(g, reg);
     if (g + KS < min(ns, NBC / BPS)) busca(g + KS, reg2);
-    if (nch == 1) tabelas_unica();
+    if (nch == 1 && nb % 16 == 0 && nb <= 128) tabelas_diretas();
+    else if (nch == 1) tabelas_unica();
     else tabelas_parte(0, NBC);
     if (g < min(ns, NBC / BPS)) guarda(0, reg);
     __syncthreads();

@@ -17,8 +17,11 @@ Fixtures:
   trace_r.json      every op output of two full training steps (Modelo.passo with k_lr=4) at the reference
                     model shape (V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=8), plus the per-step
                     (d_alvo, soma) hashes and float64 losses of N further steps
+  trace_r_bt16.json the same at Bt=16 (2048 tokens per step: the batch of the reference's own speed runs,
+                    treino_cuda.py:119-165, bench_grafo.py:29-37)
 
-Usage: python tests/golden/make_golden.py [--ref /root/reference] [--only ops|dominio|config1|prim|trace] [--passos N]
+Usage: python tests/golden/make_golden.py [--ref /root/reference] [--only ops|dominio|config1|prim|trace|trace16]
+       [--passos N]
 """
 import argparse
 import contextlib
@@ -168,6 +171,8 @@ def main():
             w(f"ops_dominio_blk{blk}.json", run_ops(O, blk, CS.casos_dominio()))
     if a.only in ("all", "trace"):
         w("trace_r.json", run_trace(O, MO, a.passos))
+    if a.only in ("all", "trace16"):
+        w("trace_r_bt16.json", run_trace(O, MO, a.passos, Bt=16))
 
 
 if __name__ == "__main__":

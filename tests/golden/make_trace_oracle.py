@@ -10,13 +10,13 @@ run it.
                     k_lr 4): as many steps as asked. Attention at head width 64 is the declared extension of the
                     spec (it reduces to the spec at head width 4), so this trace is anchored on the oracle alone.
   trace_c5.jsonl    BASELINE config 5 (the config-4 widths with 24 layers, Bt 64 x T 256 = 16384 tokens and the
-                    16-bit residual stream, modelo.py:60-130): 3 steps (about 3-4 minutes each on 8 cores).
+                    16-bit residual stream, modelo.py:60-130): 10 steps (about 3-4 minutes each on 8 cores).
 
 Both use seed-0 init (modelo.py:16-45) and the batches of tests/traco.py: uniform ids from substream 4242,
 (x[:, :-1], x[:, 1:]) as treino_int8_gpu/treino.py:41-44. Line 1 holds the shape and the init hashes; each
 further line one step: the SHA-256 of the integer softmax outputs d_alvo and soma (the loss is defined on
 them) and the float64 loss mean(d/256 + ln(s/4096)) (modelo.py:93) as a hex float. Lines are appended and
-flushed as steps finish, so a partial file is usable.
+flushed as steps finish into `<name>.parcial`, which replaces the fixture once every step is written.
 
 Usage: python tests/golden/make_trace_oracle.py r600|c4|c5 [--passos N] [--threads T]
 """
@@ -40,7 +40,7 @@ FORMAS = {
     "c4": dict(V=256, D=512, H=8, FF=2048, L=12, T=256, Bt=8, BLK=32, k_lr=4, semente=0, tokens_seed=4242),
     "c5": dict(V=256, D=512, H=8, FF=2048, L=24, T=256, Bt=64, BLK=32, k_lr=4, semente=0, tokens_seed=4242, r16=True),
 }
-PASSOS = {"r600": 600, "c4": 600, "c5": 3}
+PASSOS = {"r600": 600, "c4": 600, "c5": 10}
 
 
 def main():
@@ -65,7 +65,7 @@ def main():
     if gold is not None:
         assert gold["forma"] == f and gold["init"] == init, "oracle model differs from the spec's trace"
     caminho = os.path.join(AQUI, f"trace_{a.qual}.jsonl")
-    with open(caminho, "w") as out:
+    with open(caminho + ".parcial", "w") as out:
         out.write(json.dumps({"forma": f, "init": init}, separators=(",", ":")) + "\n")
         for p in range(n):
             t0 = time.time()
@@ -80,6 +80,7 @@ def main():
             out.write(json.dumps(ent, separators=(",", ":")) + "\n")
             out.flush()
             print(f"{a.qual} passo {p}: loss {perda:.6f}  {time.time() - t0:.1f}s", flush=True)
+    os.replace(caminho + ".parcial", caminho)
     O.BLK = 128
 
 
