@@ -144,8 +144,12 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             }
         }
     };
-    // output-stage coordinates (threads 0 .. GT - 1): row orow, columns oc .. oc + 15
-    const int orow = (tid >> 3) & (BM - 1), oc = (tid & 7) * 16;
+    // output-stage coordinates: row orow, columns oc .. oc + EV - 1. The block-output epilogues (modes 0, 2, 3, 4,
+    // 6) run on every thread, EV = 16 / KS values each (all K-split groups share the partial sums and the
+    // quantization); the raw-output and optimizer epilogues (modes 1, 5) on the first group, 16 values each.
+    constexpr int EV = (MODO == 1 || MODO == 5) ? 16 : 16 / KS, LPR_ = 128 / EV;
+    const int orow = (tid / LPR_) & (BM - 1), oc = (tid % LPR_) * EV;
+    const bool saida = EV < 16 || tid < GT;
     // Several chunks: RA and RB first, by one pass over the exponent rows in global memory (rows of nb bytes, nb a
     // multiple of 16 there: 16-byte loads). One chunk: from the staged exponents, below.
     if (nch > 1) {
@@ -412,18 +416,18 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
     // of modes 2 and 4 is read here, not before the K loop, so its 16 registers do not cost a resident wave.
     const size_t o = (size_t)(row0 + orow) * N + col0 + oc;
     const size_t oe = (size_t)(row0 + orow) * (N / BLK) + (col0 + oc) / BLK;
-    int xin[16], exin = 0;
+    int xin[EV], exin = 0;
     if constexpr (MODO == 2 || MODO == 4) {
-        if (tid < GT) { le_i8(Xm + o, xin); exin = XE[oe]; }
+        if (saida) { le_i8(Xm + o, xin); exin = XE[oe]; }
     }
     if constexpr (MODO == 6) {                                     // the R16 residual (int16 mantissas)
-        if (tid < GT) { le_i16(reinterpret_cast<const int16_t*>(Xm) + o, xin); exin = XE[oe]; }
+        if (saida) { le_i16(reinterpret_cast<const int16_t*>(Xm) + o, xin); exin = XE[oe]; }
     }
-    int base[16];
-    if (tid < GT) {
+    int base[EV];
+    if (saida) {
         const int ra = ra_s[orow];
 #pragma unroll
-        for (int j = 0; j < 16; j++) base[j] = ra + rb_s[oc + j] - 4;
+        for (int j = 0; j < EV; j++) base[j] = ra + rb_s[oc + j] - 4;
     }
     int* acc_s = reinterpret_cast<int*>(buf);                      // [KS][BM][BN + PAD]
     constexpr int TILE = BM * (BN + PAD);
@@ -475,16 +479,16 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         return;
     } else {
-        if (tid >= GT) return;
-        int v[16];
+        if (!saida) return;
+        int v[EV];
 #pragma unroll
-        for (int j = 0; j < 16; j += 4) {
+        for (int j = 0; j < EV; j += 4) {
             v4i t = *reinterpret_cast<const v4i*>(acc_s + orow * (BN + PAD) + oc + j);
 #pragma unroll
             for (int q = 1; q < KS; q++) t += *reinterpret_cast<const v4i*>(acc_s + q * TILE + orow * (BN + PAD) + oc + j);
             v[j] = t[0]; v[j + 1] = t[1]; v[j + 2] = t[2]; v[j + 3] = t[3];
         }
-        constexpr int LPB = BLK / 16;
+        constexpr int LPB = BLK / EV;
         const bool lider = (tid & (LPB - 1)) == 0;
         if constexpr (MODO == 5) {                                 // weight gradient straight into momento + peso
             int eg[16];
@@ -493,18 +497,18 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             otim_valores<16, LPB>(v, eg, otx, ot, (long long)o, (long long)(o / BLK), lider, k_lr, ef, kid);
             return;
         }
-        int8_t m[16];
-        const int E = quant8_d<16, LPB>(v, base, m, kid, o);        // |base| <= 260
+        int8_t m[EV];
+        const int E = quant8_d<EV, LPB>(v, base, m, kid, o);        // |base| <= 260
         if constexpr (MODO == 0 || MODO == 3) {
             grava_i8(Cm + o, m);
             if (lider) CE[oe] = (int8_t)E;
         }
         if constexpr (MODO == 3) {                                 // a = relu2(h): max(m, 0)^2, exponent 2E
-            int a[16];
+            int a[EV];
 #pragma unroll
-            for (int j = 0; j < 16; j++) { const int h = max((int)m[j], 0); a[j] = h * h; }
-            int8_t q[16];
-            const int Ea = quant8_comum<16, LPB>(a, 2 * E, q);
+            for (int j = 0; j < EV; j++) { const int h = max((int)m[j], 0); a[j] = h * h; }
+            int8_t q[EV];
+            const int Ea = quant8_comum<EV, LPB>(a, 2 * E, q);
             if (Ea > 126 && lider) reporta(E_EXP, kid, (long long)o, Ea, -7);
             grava_i8(Om2 + o, q);
             if (lider) OE2[oe] = (int8_t)Ea;
@@ -517,51 +521,51 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             const int ey = (int)(int8_t)E, ec = max(exin + 15, ey + 7) - 28;
             const Desl dx(ec - exin), dm(ec - ey);                 // left shifts keep |values| below 2^28
             const int mx = exin == E_ZERO ? 0 : -1, mm = ey == E_ZERO ? 0 : -1;
-            int s[16], q[16];
+            int s[EV], q[EV];
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = (dx(xin[j]) & mx) + (dm((int)m[j]) & mm);
-            const int Ez = quant_u<16, LPB, true, 15, 32767>(s, ec, q, kid + 1, (long long)o);   // soma16's launch id
-            int16_t z[16];
+            for (int j = 0; j < EV; j++) s[j] = (dx(xin[j]) & mx) + (dm((int)m[j]) & mm);
+            const int Ez = quant_u<EV, LPB, true, 15, 32767>(s, ec, q, kid + 1, (long long)o);   // soma16's launch id
+            int16_t z[EV];
 #pragma unroll
-            for (int j = 0; j < 16; j++) z[j] = (int16_t)q[j];
+            for (int j = 0; j < EV; j++) z[j] = (int16_t)q[j];
             grava_i16(reinterpret_cast<int16_t*>(Cm) + o, z);
             if (lider) CE[oe] = (int8_t)Ez;
-            int8_t y[16];
-            const int Ey = quant8_u8<16, LPB>(q, (int)(int8_t)Ez, y, kid + 2, (long long)o);     // para8's launch id
+            int8_t y[EV];
+            const int Ey = quant8_u8<EV, LPB>(q, (int)(int8_t)Ez, y, kid + 2, (long long)o);     // para8's launch id
             grava_i8(Om2 + o, y);
             if (lider) OE2[oe] = (int8_t)Ey;
         }
         if constexpr (MODO == 2) {                                 // z = soma(X, C): ec = max(xE, E) - 21
-            int s[16];
+            int s[EV];
             const int ec = max(exin, E) - 21;
             const Desl dx(ec - exin), dm(ec - E);                  // exact left shifts or roundings, |s| <= 2^28
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = dx(xin[j]) + dm((int)m[j]);
-            int8_t q[16];
+            for (int j = 0; j < EV; j++) s[j] = dx(xin[j]) + dm((int)m[j]);
+            int8_t q[EV];
             int Ez;
             if (est) {                                             // stochastic rounding (jt_res_estocastico)
                 // seeds as the reference's epilogue lays out a 128-column tile: the value at tile column c has seed
                 // 8 (flat index of column c & 60 of its row) + (c & 3) + 4 (c >= 64), in 32-bit arithmetic
-                uint32_t h[16];
+                uint32_t h[EV];
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
+                for (int j = 0; j < EV; j++) {
                     const int c = oc + j;
                     h[j] = (uint32_t)((size_t)(row0 + orow) * N + col0 + (c & 60)) * 8u + (uint32_t)((c & 3) + 4 * ((c >> 6) & 1));
                 }
-                Ez = quant8_est<16, LPB>(s, ec, q, h);
+                Ez = quant8_est<EV, LPB>(s, ec, q, h);
             } else {
-                Ez = quant8_comum<16, LPB>(s, ec, q);
+                Ez = quant8_comum<EV, LPB>(s, ec, q);
             }
             if (Ez > 126 && lider) reporta(E_EXP, kid, (long long)o, Ez, -6);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Ez;
         }
         if constexpr (MODO == 4) {                                 // gh = C * 2 max(H, 0), exponent E + eh
-            int s[16];
+            int s[EV];
 #pragma unroll
-            for (int j = 0; j < 16; j++) s[j] = (int)m[j] * max(xin[j], 0) * 2;
-            int8_t q[16];
-            const int Eg = quant8_comum<16, LPB>(s, E + exin, q);
+            for (int j = 0; j < EV; j++) s[j] = (int)m[j] * max(xin[j], 0) * 2;
+            int8_t q[EV];
+            const int Eg = quant8_comum<EV, LPB>(s, E + exin, q);
             if (Eg > 126 && lider) reporta(E_EXP, kid, (long long)o, Eg, -8);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Eg;

@@ -1,8 +1,8 @@
 """Model-level parity of the HIP path.
 
 * two full training steps (522 ops each: forward, backward, optimizer) at the reference model shape
-  (V=256, D=256, H=64, FF=1024, L=12, T=128, Bt=8, BLK=128): every op output equals the spec's
-  (trace written from OpsRef + Modelo.passo, the reference's `conferir 2` protocol, treino_cuda.py:48-60);
+  (V=256, D=256, H=64, FF=1024, L=12, T=128, BLK=128) at Bt=8 and Bt=16: every op output equals the spec's
+  (traces written from OpsRef + Modelo.passo, the reference's `conferir 2` protocol, treino_cuda.py:48-60);
 * the hipGraph-captured step replays to the same bits as eager steps, for every replay, with eager work and
   synchronization between replays; and the per-step (d_alvo, soma) of the golden loss trace;
 * the fused optimizer (momento + peso of all 50 tensors in one launch, or in the epilogue of the grouped
@@ -30,21 +30,23 @@ def _ops(vigiar=False):
     return O.OpsHip(reg), reg
 
 
-def test_dois_passos_vs_spec():
+@pytest.mark.parametrize("nome", TR.TRACOS)
+def test_dois_passos_vs_spec(nome):
     ops, reg = _ops()
     reg.novo_passo(0)
-    _, init, passos = TR.roda(ops, reg, "cuda", 2, host)
+    _, init, passos = TR.roda(ops, reg, "cuda", 2, host, nome)
     reg.fim_passo()
-    TR.confere(init, passos)
+    TR.confere(init, passos, nome)
 
 
 def _estado(m):
     return [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
 
 
-def test_grafo_igual_ao_eager_e_ao_spec():
+@pytest.mark.parametrize("nome", TR.TRACOS)
+def test_grafo_igual_ao_eager_e_ao_spec(nome):
     from jatai_amd.modelo import Modelo, PassoGravado
-    g = TR.gold()
+    g = TR.gold(nome)
     f = g["forma"]
     n = len(g["passos"])                                 # every step of the golden loss trace
     ops, reg = _ops()

@@ -1,5 +1,7 @@
 """Runs the training step at the reference model shape and records every op output, for comparison with the
-trace written from the reference spec (tests/golden/trace_r.json: Modelo.passo with OpsRef, modelo.py:51-140)."""
+traces written from the reference spec (Modelo.passo with OpsRef, modelo.py:51-140): tests/golden/trace_r.json
+(Bt = 8, the reference's `conferir` batch) and tests/golden/trace_r_bt16.json (Bt = 16, the batch of its speed
+runs)."""
 import contextlib
 import json
 import os
@@ -9,11 +11,12 @@ import torch
 import cases as CS
 import recipe as R
 
-GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "trace_r.json")
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TRACOS = ("trace_r.json", "trace_r_bt16.json")
 
 
-def gold():
-    return json.load(open(GOLD))
+def gold(nome="trace_r.json"):
+    return json.load(open(os.path.join(GOLDEN, nome)))
 
 
 class RegStub:
@@ -33,10 +36,10 @@ def lote(p, Bt, T, V, dev):
     return tok, alvo
 
 
-def roda(ops, reg, dev, passos, host):
+def roda(ops, reg, dev, passos, host, nome="trace_r.json"):
     """Builds the model exactly as the golden writer did and runs `passos` steps; returns (init hashes, steps)."""
     from jatai_amd.modelo import Modelo
-    g = gold()
+    g = gold(nome)
     f = g["forma"]
     rec = CS.Gravador(ops, host)
     m = Modelo(f["V"], f["D"], f["H"], f["FF"], f["L"], f["semente"], dev, rec, reg)
@@ -58,9 +61,9 @@ def roda(ops, reg, dev, passos, host):
     return m, init, out
 
 
-def confere(init, passos):
+def confere(init, passos, nome="trace_r.json"):
     """Asserts init hashes and every op output of each step against the golden trace."""
-    g = gold()
+    g = gold(nome)
     assert init == g["init"], "initial weights differ from the reference init (modelo.py:16-45)"
     for p, ent in enumerate(passos):
         gp = g["passos"][p]
