@@ -740,7 +740,9 @@ int jt_atencao_back(const void* gom, const void* goE, const void* qm, const void
 // No reference counterpart: jt_atencao_back with a caller workspace of jt_atencao_back_ws_bytes(Bt, T, H, D)
 // bytes (16-byte aligned). Same outputs as jt_atencao_back. At head width 64 on matrix cores (T % 64 == 0,
 // T <= 512) it converts dO, q, k, v once per (sequence, head) into the workspace and splits each 16-row tile's
-// partner tiles over four waves (4 launches, 5 for the exact variant); otherwise it runs jt_atencao_back.
+// partner tiles over four waves (4 launches; the exact variant's per-tile max |gP| in the conversion launch at
+// T <= 256, a launch of its own past that or when the forward saved the q, k, v conversions); otherwise it runs
+// jt_atencao_back.
 long long jt_atencao_back_ws_bytes(int Bt, int T, int H, int D) {
     if (Bt <= 0 || H <= 0 || T <= 0 || D % H) return 0;
     return (long long)atw::bytes_back((long long)Bt * H, T);
@@ -765,8 +767,9 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
 #define FASES(NTW, LM, B)                                                                                                 \
     {                                                                                                                     \
         if (!LM && smx) k_atb_prep_s<<<gp, 256, 0, g_stream>>>(go8, goE8, w, smx, T, H, D, g_blk, GA);                     \
+        else if (!LM && T <= 256) k_atb_prep<0, true><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA); \
         else k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                         \
-        if (!LM) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                                          \
+        if (!LM && (smx || T > 256)) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                      \
         k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \
         k_atbqkv<NTW, LM, B><<<2 * gt, 256, 0, g_stream>>>(w, P8, (int*)G1, (int16_t*)G2, T, H, D, dsb, kid);              \
     }

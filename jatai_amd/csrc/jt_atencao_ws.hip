@@ -443,14 +443,21 @@ __device__ __forceinline__ int wg_max4(int v, int (&red)[4]) {
     return r;
 }
 
-template <int LIMITE>
+// GP (exact variant, T <= 256): also max |gP| over the causal pairs of each of the part's four query tiles, what
+// k_atb1 computes, into the same slots: each wave takes one query tile, with v of keys 0 .. 64 part + 63 as m8 << L
+// fragments in LDS (the q, k tiles once written out; the earlier keys' v converted here again) and the part's dO
+// fragments in the dO tile. Parts are then taken in decreasing order (the last part has the most key tiles).
+template <int LIMITE, bool GP = false>
 __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
                                                   const int8_t* __restrict__ qE, atw::WsB w, int T, int H, int D, int blk, int GA) {
     constexpr int HD = 64;
     __shared__ int red[4][4];
     __shared__ int red1[4];
-    __shared__ __align__(16) TileT tg, tq, tk;
-    const int nparts = T / 64, bh = blockIdx.x / nparts, part = blockIdx.x % nparts, b = bh / H, h = bh % H;
+    __shared__ __align__(16) TileT tg, tqk[2];
+    TileT &tq = tqk[0], &tk = tqk[1];
+    const int nparts = T / 64, BH = (int)gridDim.x / nparts;
+    const int bh = GP ? (int)blockIdx.x % BH : (int)blockIdx.x / nparts;
+    const int part = GP ? nparts - 1 - (int)blockIdx.x / BH : (int)blockIdx.x % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, tid = threadIdx.x, nbl = ld / blk, nbg = D / blk;
     // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t. Every value it converts is loaded first, so the
     // loads overlap the head maxima's reduction below.
@@ -485,13 +492,15 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     }
     if (part == 0 && tid == 0) { w.mx[bh * 4] = emg - GA; w.mx[bh * 4 + 1] = emq - GA; w.mx[bh * 4 + 2] = emk - GA; w.mx[bh * 4 + 3] = emv - GA; }
     int amax = 0, v1 = 0;
+    int8_t gm8r[16], vm8r[16];                                       // this thread's dO and v fragments (GP reuses them)
+    int gLr = 0, vLr = 0;
     {   // dO: m8 << L fragments and aligned f16
         int v[16];
         abre_i8(rg, v);
         const int s = emg - egt;
         const Desl ds(s);
-        int8_t m8[16];
-        int L = 0;
+        int8_t (&m8)[16] = gm8r;
+        int& L = gLr;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
@@ -507,8 +516,8 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         abre_i8(rv, v);
         const int s = emv - evt;
         const Desl ds(s);
-        int8_t m8[16];
-        int L = 0;
+        int8_t (&m8)[16] = vm8r;
+        int& L = vLr;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
@@ -534,6 +543,84 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         v1 = quad_soma(v1);
         const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
         if (tid == 0) { w.p1a[bh * atw::SLOTS + part] = a; w.p1b[bh * atw::SLOTS + part] = c; }
+    }
+    if constexpr (GP) {
+        // LDS, rows 72 bytes apart (8-byte fragment reads of 16 consecutive rows fall in distinct banks): v m8 of keys
+        // 0 .. 64 part + 63 in the q, k tiles (256 x 72 bytes), this part's dO m8 [64][72] then the L bytes in tg
+        constexpr int RS = 72;
+        int8_t* vm_s = reinterpret_cast<int8_t*>(&tqk[0][0][0]);
+        int8_t* dm_s = reinterpret_cast<int8_t*>(&tg[0][0]);
+        int8_t* dl_s = dm_s + 64 * RS;                                // [64][2]
+        int8_t* vl_s = dl_s + 128;                                    // [256][2]
+        const int tl = tid >> 2;
+        // the earlier keys' raw v, loaded before the barrier that frees the tiles
+        int4 rx[3];
+        int ex[3];
+#pragma unroll
+        for (int r = 0; r < 3; r++)
+            if (r < part) {
+                const int tk2 = 64 * r + tl;
+                rx[r] = ld16(qm + (size_t)(b0 + tk2) * ld + 2 * D + colg);
+                ex[r] = qE[(size_t)(b0 + tk2) * nbl + (2 * D + colg) / blk];
+            }
+        auto guarda16 = [](int8_t* d, const int8_t (&m)[16]) {         // two 8-byte stores (rows are 8-byte aligned)
+            long a = 0, c = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) { a |= (long)(uint8_t)m[k] << (8 * k); c |= (long)(uint8_t)m[8 + k] << (8 * k); }
+            reinterpret_cast<long*>(d)[0] = a;
+            reinterpret_cast<long*>(d)[1] = c;
+        };
+        __syncthreads();                                              // grava_t64 has read the tiles
+        guarda16(dm_s + tl * RS + 16 * c4, gm8r);
+        guarda16(vm_s + (64 * part + tl) * RS + 16 * c4, vm8r);
+        if ((c4 & 1) == 0) { dl_s[tl * 2 + half] = (int8_t)gLr; vl_s[(64 * part + tl) * 2 + half] = (int8_t)vLr; }
+#pragma unroll
+        for (int r = 0; r < 3; r++)
+            if (r < part) {
+                int v[16];
+                abre_i8(rx[r], v);
+                const int s = emv - ex[r];
+                int8_t m8[16];
+                int L = 0;
+#pragma unroll
+                for (int k = 0; k < 16; k++) { int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a; }
+                guarda16(vm_s + (64 * r + tl) * RS + 16 * c4, m8);
+                if ((c4 & 1) == 0) vl_s[(64 * r + tl) * 2 + half] = (int8_t)L;
+            }
+        __syncthreads();
+        // wave wv: query tile qt = 4 part + wv (local rows 16 wv ..), key tiles 0 .. qt, as k_atb1's gp_tile
+        const int wv = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4, qt = 4 * part + wv;
+        const int8_t* da = dm_s + (16 * wv + lr) * RS + 8 * lg;
+        const long ga0 = *reinterpret_cast<const long*>(da), ga1 = *reinterpret_cast<const long*>(da + 32);
+        int lx[4][2];
+#pragma unroll
+        for (int v = 0; v < 4; v++) { lx[v][0] = dl_s[(16 * wv + 4 * lg + v) * 2]; lx[v][1] = dl_s[(16 * wv + 4 * lg + v) * 2 + 1]; }
+        const int i0 = 16 * qt + 4 * lg;
+        int mg = 0;
+        for (int t0 = 0; t0 <= qt; t0 += 4) {                         // four independent tiles in flight
+            long vb0[4], vb1[4];
+            int l0[4], l1[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int j = 16 * min(t0 + u, qt) + lr;              // past qt: a repeat of tile qt, not counted
+                const int8_t* vb = vm_s + j * RS + 8 * lg;
+                vb0[u] = *reinterpret_cast<const long*>(vb);
+                vb1[u] = *reinterpret_cast<const long*>(vb + 32);
+                l0[u] = vl_s[j * 2];
+                l1[u] = vl_s[j * 2 + 1];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (t0 + u > qt) break;                               // uniform
+                const int j = 16 * (t0 + u) + lr;
+                int o[4];
+                tile_xyt(ga0, ga1, vb0[u], vb1[u], lx, l0[u], l1[u], o);
+#pragma unroll
+                for (int v = 0; v < 4; v++) if (j <= i0 + v) mg = max(mg, abs(o[v]));
+            }
+        }
+        mg = g_max<64>(mg);
+        if (lane == 0) w.p1a[bh * atw::SLOTS + qt] = mg;
     }
 }
 
