@@ -42,8 +42,10 @@ int jt_bloco_atual(void);
 
 /* ---- GEMM C = A . B^T, A [M,K], B [N,K] blocked along K (jatai_cuda.cu:1093-1127)
  * modo 0: block C (Cm, CE) | 1: raw C (C32, Ce), split-K over K-blocks | 2: Cm = soma(X, A.B^T)
- * 3: Cm = h = A.B^T and Om2 = relu2(h) | 4: Cm = relu2_back(A.B^T, X), and when Om2/OE2 are given (no reference
- * counterpart; BLK = 32 only) also Om2 = transpoe(Cm) [N, M]
+ * 3: Cm = h = A.B^T and Om2 = relu2(h), and when C32/Ce are given (no reference counterpart; BLK = 32 only) also
+ * transpoe(Om2) [N, M] into them, as int8 mantissas (C32) and int8 exponents [N, M/BLK] (Ce)
+ * | 4: Cm = relu2_back(A.B^T, X), and when Om2/OE2 are given (no reference counterpart; BLK = 32 only) also
+ * Om2 = transpoe(Cm) [N, M]
  * Requires M % 32 == 0, N % 128 == 0, K % BLK == 0, K <= 4096 (the reference: M % 64, N % 128, K % 128). */
 int jt_gemm_f(const void* A, const void* EA, const void* B, const void* EB, void* Cm, void* CE, void* C32, void* Ce,
               const void* Xm, const void* XE, void* Om2, void* OE2, int M, int N, int K, int modo, int kid);

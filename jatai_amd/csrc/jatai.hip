@@ -160,9 +160,10 @@ static int gemm_f(const void* A, const void* EA, const void* B, const void* EB, 
     if (M <= 0 || N <= 0 || K <= 0 || M % BM || N % BN || K % g_blk || !k_ok(K)) return (int)hipErrorInvalidValue;
     if (!alinhados(A, EA, B, EB, Cm, CE, C32, Ce, Xm, XE, Om2, OE2)) return (int)hipErrorInvalidValue;
     const int nb = K / g_blk, r = gemm_r(M, N, modo);
-    // mode 4 with Om2: the transposed copy needs a single K-split (BLK = 32 only)
+    // mode 4 with Om2 (T(gh)) and mode 3 with C32, Ce (T(a)): the transposed copy needs a single K-split (BLK = 32 only)
     if (modo == 4 && (Om2 || OE2) && (g_blk != 32 || !Om2 || !OE2)) return (int)hipErrorInvalidValue;
-    const int ks = (modo == 4 && Om2) ? 1 : gemm_divisoes_r(M, N, K, modo, r);
+    if (modo == 3 && (C32 || Ce) && (g_blk != 32 || !C32 || !Ce)) return (int)hipErrorInvalidValue;
+    const int ks = ((modo == 4 && Om2) || (modo == 3 && C32)) ? 1 : gemm_divisoes_r(M, N, K, modo, r);
     const dim3 grade(N / BN, M / (32 * r));
     const size_t lds = gemm_lds(nb, ks, g_blk, r);
 #define ARGS (const int8_t*)A, (const int8_t*)EA, (const int8_t*)B, (const int8_t*)EB, (int8_t*)Cm, (int8_t*)CE, (int*)C32, (int16_t*)Ce, \

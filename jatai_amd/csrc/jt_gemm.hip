@@ -490,6 +490,39 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
         }
         constexpr int LPB = BLK / EV;
         const bool lider = (tid & (LPB - 1)) == 0;
+        // KS = 1, BLK = 32 (every thread here, EV = 16, so the barriers are uniform): the block-format output q (its
+        // block's exponent Eq) also written transposed, Yt [N, M] blocked along M. The tile's BM rows are R blocks of
+        // each of its 128 columns: the same requantization as k_transpoe (quant(m^T, expand(E)^T), ops.py:121-123),
+        // from the quantized tile staged in LDS.
+        // LDS layout: mantissa rows of BN bytes whose 16-byte chunk j sits at chunk j ^ ((row / 16) % 8), and exponent
+        // rows 5 bytes apart: the column reads below (8 threads of a column each take rows 16 pt .. 16 pt + 15, pt =
+        // 0 .. 7) then fall in 8 distinct chunks and banks instead of one bank 8 times over.
+        auto escreve_t = [&](const int8_t (&q)[EV], int Eq, int8_t* __restrict__ Yt, int8_t* __restrict__ YEt) {
+            if constexpr (KS == 1 && BLK == 32) {
+                constexpr int ES = 5;
+                int8_t* qs = reinterpret_cast<int8_t*>(buf);           // [BM][BN] mantissas, chunk-swizzled
+                int8_t* es = qs + BM * BN;                              // [BM][ES] exponents
+                __syncthreads();                                        // acc_s fully read before the reuse
+                grava_i8(qs + orow * BN + 16 * ((oc >> 4) ^ ((orow >> 4) & 7)), q);
+                if (lider) es[orow * ES + oc / 32] = (int8_t)Eq;
+                __syncthreads();
+                // column c, rows 16 pt .. 16 pt + 15 (2 R threads per column; lanes 2j, 2j + 1 hold one block)
+                const int c = tid / (2 * R), pt = tid % (2 * R);
+                const int8_t* qc = qs + 16 * ((c >> 4) ^ (pt & 7)) + (c & 15);
+                int tv[16], te[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    const int r = 16 * pt + k;
+                    tv[k] = qc[r * BN];
+                    te[k] = es[r * ES + (c >> 5)];
+                }
+                int8_t t8[16];
+                const long long ot = (long long)(col0 + c) * M + row0 + 16 * pt;
+                const int Et = quant8_d<16, 2>(tv, te, t8, kid, ot);   // int8 exponents
+                grava_i8(Yt + ot, t8);
+                if ((pt & 1) == 0) YEt[(size_t)(col0 + c) * (M / 32) + row0 / 32 + (pt >> 1)] = (int8_t)Et;
+            }
+        };
         if constexpr (MODO == 5) {                                 // weight gradient straight into momento + peso
             int eg[16];
 #pragma unroll
@@ -512,6 +545,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             if (Ea > 126 && lider) reporta(E_EXP, kid, (long long)o, Ea, -7);
             grava_i8(Om2 + o, q);
             if (lider) OE2[oe] = (int8_t)Ea;
+            if (C32 != nullptr) escreve_t(q, Ea, reinterpret_cast<int8_t*>(C32), reinterpret_cast<int8_t*>(Ce));   // T(a)
         }
         if constexpr (MODO == 6) {
             // z16 = soma16(X16, C) (jatai_cuda.cu:514-531: ec = max(xE + 15, E + 7) - 28, zero blocks add 0, a
@@ -569,33 +603,7 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             if (Eg > 126 && lider) reporta(E_EXP, kid, (long long)o, Eg, -8);
             grava_i8(Cm + o, q);
             if (lider) CE[oe] = (int8_t)Eg;
-            if constexpr (KS == 1 && BLK == 32) {
-                // Om2 given: also the transpose T(gh) [N, M] blocked along M. The tile's BM rows are R blocks of each
-                // of its 128 columns: the same requantization as k_transpoe (quant(m^T, expand(E)^T), ops.py:121-123),
-                // from the quantized tile staged in LDS. KS = 1: every thread is here, so the barriers are uniform.
-                if (Om2 != nullptr) {
-                    int8_t* qs = reinterpret_cast<int8_t*>(buf);           // [BM][BN + 16] mantissas
-                    int8_t* es = qs + BM * (BN + 16);                       // [BM][BN / 32] exponents
-                    __syncthreads();                                        // acc_s fully read before the reuse
-                    grava_i8(qs + orow * (BN + 16) + oc, q);
-                    if (lider) es[orow * (BN / 32) + oc / 32] = (int8_t)Eg;
-                    __syncthreads();
-                    // column c, rows 16 pt .. 16 pt + 15 (2 R threads per column; lanes 2j, 2j + 1 hold one block)
-                    const int c = tid / (2 * R), pt = tid % (2 * R);
-                    int tv[16], te[16];
-#pragma unroll
-                    for (int k = 0; k < 16; k++) {
-                        const int r = 16 * pt + k;
-                        tv[k] = qs[r * (BN + 16) + c];
-                        te[k] = es[r * (BN / 32) + (c >> 5)];
-                    }
-                    int8_t t8[16];
-                    const long long ot = (long long)(col0 + c) * M + row0 + 16 * pt;
-                    const int Et = quant8_d<16, 2>(tv, te, t8, kid, ot);   // int8 exponents
-                    grava_i8(Om2 + ot, t8);
-                    if ((pt & 1) == 0) OE2[(size_t)(col0 + c) * (M / 32) + row0 / 32 + (pt >> 1)] = (int8_t)Et;
-                }
-            }
+            if (Om2 != nullptr) escreve_t(q, Eg, Om2, OE2);            // T(gh)
         }
     }
 }

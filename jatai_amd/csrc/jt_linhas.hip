@@ -201,7 +201,9 @@ __global__ void __launch_bounds__(256) k_softmax_ce(const int* __restrict__ acc,
 // Tile TR rows x 64 cols (TR = 64 at BLK=32, 128 at BLK=128: a multiple of the output block), 2 TR threads.
 // Lane (cg, rc) owns 4 columns (one 32-bit LDS word) x 8 rows: it reads 8 words, unpacks 32 values and runs 4
 // block quantizations side by side; the LPB = BLK/8 lanes of a column block are consecutive lanes. Rows of the
-// LDS tile are 17 words long so the word reads spread over the banks.
+// LDS tile are 18 words long and word w of row r sits at word w ^ (r / 8): the reads (a half-wave takes word cg
+// of rows 8 rc + k, rc = 0 .. 15) then hit 32 distinct banks at TR = 128 (4 rows to a bank with 17-word rows and
+// no swizzle); the row-pair writes stay 2-way.
 // One tile's global loads (row tid / 2, half tid % 2: 32 bytes and the exponent byte of those 32 columns), kept in
 // registers so a workgroup can issue the loads of several tiles before it stages the first.
 struct CargaT {
@@ -214,15 +216,17 @@ __device__ __forceinline__ CargaT transpoe_carga(const int8_t* __restrict__ X, c
     const int4* src = reinterpret_cast<const int4*>(X + (size_t)(r0 + row) * C + c0 + half * 32);
     return CargaT{src[0], src[1], (int)EX[(size_t)(r0 + row) * (C / BLK) + (c0 + half * 32) / BLK]};
 }
+constexpr int TLD = 18;                     // LDS row length of a transpose tile, in words
 template <int BLK, int TR>
-__device__ __forceinline__ void transpoe_tile(const CargaT& cg_, int (&tile)[TR][17], int8_t (&er)[TR][2], int8_t* __restrict__ Y,
+__device__ __forceinline__ void transpoe_tile(const CargaT& cg_, int (&tile)[TR][TLD], int8_t (&er)[TR][2], int8_t* __restrict__ Y,
                                               int8_t* __restrict__ EY, int R, int bx, int by, int kid) {
     constexpr int LPB = BLK / 8, RC = TR / 8;
     const int r0 = by * TR, c0 = bx * 64, tid = threadIdx.x;
     {
-        const int row = tid >> 1, half = tid & 1;
-        int* d = &tile[row][half * 8];
-        d[0] = cg_.v0.x; d[1] = cg_.v0.y; d[2] = cg_.v0.z; d[3] = cg_.v0.w; d[4] = cg_.v1.x; d[5] = cg_.v1.y; d[6] = cg_.v1.z; d[7] = cg_.v1.w;
+        const int row = tid >> 1, half = tid & 1, sw = (row >> 3) & 15;
+        const int w8[8] = {cg_.v0.x, cg_.v0.y, cg_.v0.z, cg_.v0.w, cg_.v1.x, cg_.v1.y, cg_.v1.z, cg_.v1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) tile[row][(8 * half + j) ^ sw] = w8[j];
         er[row][half] = (int8_t)cg_.e;
     }
     __syncthreads();
@@ -230,7 +234,7 @@ __device__ __forceinline__ void transpoe_tile(const CargaT& cg_, int (&tile)[TR]
     int m[4][8], e[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        const int row = rc * 8 + k, word = tile[row][cg];
+        const int row = rc * 8 + k, word = tile[row][cg ^ (rc & 15)];     // (row / 8) % 16 = rc % 16
         e[k] = er[row][cg >> 3];
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) m[cc][k] = (word << (24 - 8 * cc)) >> 24;
@@ -249,7 +253,7 @@ __device__ __forceinline__ void transpoe_tile(const CargaT& cg_, int (&tile)[TR]
 template <int BLK, int TR>
 __global__ void __launch_bounds__(2 * TR) k_transpoe(const int8_t* __restrict__ X, const int8_t* __restrict__ EX, int8_t* __restrict__ Y,
                                                      int8_t* __restrict__ EY, int R, int C, int kid) {
-    __shared__ int tile[TR][17];
+    __shared__ int tile[TR][TLD];
     __shared__ int8_t er[TR][2];
     transpoe_tile<BLK, TR>(transpoe_carga<BLK, TR>(X, EX, C, blockIdx.x, blockIdx.y), tile, er, Y, EY, R, blockIdx.x, blockIdx.y, kid);
 }
@@ -270,7 +274,7 @@ struct LoteT {
 
 template <int BLK, int TR, int TPW>
 __global__ void __launch_bounds__(2 * TR) k_transpoe_lote(const LoteT L, int kid) {
-    __shared__ int tile[TPW][TR][17];
+    __shared__ int tile[TPW][TR][TLD];
     __shared__ int8_t er[TPW][TR][2];
     int ti[TPW], bx[TPW], by[TPW];
     CargaT c[TPW];

@@ -87,6 +87,10 @@ class Modelo:
         # workgroups: 34.62 fused, 34.76 batched)
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
         self.t_na_gemm_min_wg = None    # the workgroup threshold (None: 4 per CU of the device; 0: always)
+        # the same for the FFN-up GEMM's ReLU^2 output a, whose transpose the weight gradient of the FFN-down layer
+        # reads (training steps only; same workgroup threshold)
+        self.transposta_na_relu2 = hasattr(ops, "gemm_relu2_t")
+        self.t_na_relu2_min_wg = None
         # the residual update of the backward, soma(gx, rms_back(...)), in one launch
         self.rms_soma = hasattr(ops, "rms_back_soma")
         # the R16 step's residual adds, soma16(x16, gemm(...)) and soma16(gx16, rms_back(...)), each with the INT8
@@ -103,16 +107,23 @@ class Modelo:
         # and column vectors (OpsHip)
         self.grad_compacto = hasattr(ops, "gemm_cru_lote") and hasattr(ops, "otimizador")
 
+    def _t_produtor(self, M, N, modo, min_wg):
+        """Whether the ReLU^2 (modo 3) or ReLU^2-backward (modo 4) GEMM of M tokens x N columns, on a grid with a
+        workgroup threshold of min_wg (None: 4 per CU of the device; 0: always), writes its transpose too."""
+        lib = getattr(self.ops, "lib", None)
+        if min_wg == 0 or lib is None:
+            return True
+        if min_wg is None:
+            min_wg = 4 * torch.cuda.get_device_properties(self.dev).multi_processor_count
+        return (M // lib.jt_gemm_tile(M, N, modo)) * (N // 128) >= min_wg
+
     def _t_na_gemm(self, M, N):
         """Whether the ReLU^2-backward GEMM of M tokens x N columns writes its transpose too (see transposta_na_gemm)."""
-        if not self.transposta_na_gemm:
-            return False
-        lib = getattr(self.ops, "lib", None)
-        if self.t_na_gemm_min_wg == 0 or lib is None:
-            return True
-        if self.t_na_gemm_min_wg is None:
-            self.t_na_gemm_min_wg = 4 * torch.cuda.get_device_properties(self.dev).multi_processor_count
-        return (M // lib.jt_gemm_tile(M, N, 4)) * (N // 128) >= self.t_na_gemm_min_wg
+        return self.transposta_na_gemm and self._t_produtor(M, N, 4, self.t_na_gemm_min_wg)
+
+    def _t_na_relu2(self, M, N):
+        """Whether the FFN-up GEMM of M tokens x N columns writes the transpose of its ReLU^2 output too."""
+        return self.transposta_na_relu2 and self._t_produtor(M, N, 3, self.t_na_relu2_min_wg)
 
     def _otim_no_gemm(self):
         """Weight gradients straight into momento + peso in the grouped GEMM's epilogue (no gradient buffers)."""
@@ -146,6 +157,7 @@ class Modelo:
         def oito(x16):              # para8(x16), or the copy already written
             return x8 if x8 is not None else ops.para8(x16)
         tok, alvo = tok.reshape(-1).to(torch.int32).contiguous(), alvo.reshape(-1).to(torch.int32).contiguous()
+        prontas = {}                # id(mantissas) -> transpose already written by its producer (or a batched launch)
         with reg.trecho("forward"):
             with reg.trecho("embedding"):
                 x = ops.embed(p["emb"], tok)
@@ -176,7 +188,11 @@ class Modelo:
                         self._st(f"c{l}.qkv", qkv); self._st(f"c{l}.atencao_saida", om); self._st(f"c{l}.residuo1", x)
                     with reg.trecho("mlp"):
                         n2, c2 = ops.rms(oito(x16) if r16 else x)
-                        h, a = ops.gemm_relu2(n2, p[f"Wup{l}"])
+                        if k_lr is not None and self._t_na_relu2(n2[0].shape[0], p[f"Wup{l}"][0].shape[0]):
+                            h, a, ta = ops.gemm_relu2_t(n2, p[f"Wup{l}"])
+                            prontas[id(a[0])] = ta
+                        else:
+                            h, a = ops.gemm_relu2(n2, p[f"Wup{l}"])
                         if s16:
                             x16, x8 = ops.gemm_soma16(a, p[f"Wd{l}"], x16)
                             x = x8 if self.estatisticas else None
@@ -194,11 +210,10 @@ class Modelo:
         perda = (d_alvo, soma) if self.perda_inteira else perda_de(d_alvo, soma, ops if self.perda_fundida else None)
         if k_lr is None:
             return perda
-        prontas = {}
         if self.transpostas_em_lote:
             with reg.trecho("transpostas"):
                 pesos = [p[f"{w}{l}"] for l in range(self.L) for w in ("Wd", "Wup", "Wo", "Wqkv")] + [p["out"]]
-                ativ = [t for c in caches for t in (c[8], c[5], c[4], c[0])] + [nf]     # a, n2, om, n1 per layer
+                ativ = [t for c in caches for t in (c[8], c[5], c[4], c[0]) if id(t[0]) not in prontas] + [nf]   # a, n2, om, n1
                 for X, Y in zip(pesos + ativ, ops.transpoe_lote(pesos) + ops.transpoe_lote(ativ)):
                     prontas[id(X[0])] = Y
 

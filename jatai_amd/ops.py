@@ -227,6 +227,20 @@ class OpsHip:
                     dict(A=a, EA=ea, B=b, EB=eb, X=Hh[0], XE=Hh[1]), (M, N))
         return C, Ct
 
+    # no reference counterpart: (gemm_relu2(A, B), transpoe of its ReLU^2 output) from one launch at BLK = 32
+    def gemm_relu2_t(self, A, B):
+        if BLK != 32:
+            h, a = self.gemm_relu2(A, B)
+            return h, a, self.transpoe(a)
+        reg = self.reg
+        reg.confere_bloco("A", A); reg.confere_bloco("B", B)
+        (a, ea), (b, eb) = A, B
+        M, N, K = self._formas_gemm("gemm_relu2", a, b)
+        Hh, Aa, At = self._novo_bloco(M, N, a.device), self._novo_bloco(M, N, a.device), self._novo_bloco(N, M, a.device)
+        self._lanca("gemm_relu2+transpoe", "jt_gemm_f", (a, ea, b, eb, Hh[0], Hh[1], At[0], At[1], None, None, Aa[0], Aa[1], M, N, K, 3),
+                    dict(A=a, EA=ea, B=b, EB=eb), (M, N))
+        return Hh, Aa, At
+
     def gemm_relu2_back(self, A, B, Hh):
         return self._gemm_fundida("gemm_relu2_back", 4, A, B, X=Hh)
 

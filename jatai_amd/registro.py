@@ -109,7 +109,51 @@ class Diario:
         return rec
 
 
+class Cronometro:
+    """GPU time per op over a step (`perfil`): a pair of events around each timed launch, read once per step."""
+
+    def __init__(self):
+        self.pares = []
+
+    def abre(self, op):
+        ini, fim = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ini.record()
+        self.pares.append([op, ini, fim, False])
+
+    def fecha_ultimo(self):
+        if self.pares and not self.pares[-1][3]:
+            self.pares[-1][2].record()
+            self.pares[-1][3] = True
+
+    def soma_em(self, tempos):
+        """Adds this step's closed pairs to tempos (op -> [launches, ms]) and forgets them."""
+        torch.cuda.synchronize()
+        for op, ini, fim, fechado in self.pares:
+            if fechado:
+                ent = tempos.setdefault(op, [0, 0.0])
+                ent[0] += 1
+                ent[1] += ini.elapsed_time(fim)
+        self.pares = []
+
+
+def _problemas_tensor(t, dtype, papel):
+    """What keeps one tensor from being a kernel operand: dtype, device, layout."""
+    if not torch.is_tensor(t):
+        return [f"{papel} is {type(t).__name__}, not a tensor"]
+    p = []
+    if t.dtype != dtype:
+        p.append(f"{papel} {t.dtype}, expected {dtype}")
+    if not t.is_cuda:
+        p.append(f"{papel} not on the GPU")
+    if not t.is_contiguous():
+        p.append(f"{papel} not contiguous")
+    return p
+
+
 class Registro:
+    # how each level of message is echoed: (stream or None, prefix); "erro" raises instead
+    ECO = {"info": ("out", ""), "aviso": ("err", "[warning] "), "estatistica": (None, "")}
+
     def __init__(self, pasta, nome, lib=None, vigiar=False, perfil=False, eco=True):
         os.makedirs(pasta, exist_ok=True)
         self.pasta, self.nome, self.lib = pasta, nome, lib
@@ -118,33 +162,42 @@ class Registro:
         self.escopo = []                 # current scope path, innermost last
         self.lancamentos = []            # Lancamento per launch id of the current step (or of a captured graph)
         self.passo = None
-        self._cronos = []                # (op, start event, end event) of the current step, with perfil
-        self.tempos = {}                 # op -> accumulated GPU ms over the steps since the last report
+        self.cronometro = Cronometro()
+        self.tempos = {}                 # op -> [launches, GPU ms] accumulated since the last report
+        self.passos_medidos = 0
         self.ultimo_evento = None
 
-    # ------------------------------------------------------------------ log and failure
+    # ------------------------------------------------------------------ messages
     def onde(self):
         return " / ".join(self.escopo) or "-"
 
     def escreve(self, tipo, **kw):
+        """One record of the run's log, stamped with the step and scope."""
         return self.diario.grava(tipo, self.passo, self.onde(), **kw)
 
+    def _relata(self, nivel, msg, **kw):
+        """Logs msg at a level; echoes info (when `eco`) and warnings; an error raises ErroJatai whose text leads with
+        the step and the scope path, then the message."""
+        self.escreve(nivel, msg=msg, **kw)
+        if nivel == "erro":
+            raise ErroJatai(f"step {self.passo}, {self.onde()}:\n{msg}")
+        destino, prefixo = self.ECO[nivel]
+        if destino == "err" or (destino == "out" and self.eco):
+            print(f"{prefixo}{msg}" if destino == "out" else f"{prefixo}step {self.passo}, {self.onde()}: {msg}",
+                  file=sys.stderr if destino == "err" else sys.stdout, flush=True)
+
     def info(self, msg, **kw):
-        self.escreve("info", msg=msg, **kw)
-        if self.eco:
-            print(msg, flush=True)
+        self._relata("info", msg, **kw)
 
     def aviso(self, msg, **kw):
-        self.escreve("aviso", msg=msg, **kw)
-        print(f"[warning] step {self.passo} | {self.onde()} | {msg}", file=sys.stderr, flush=True)
+        self._relata("aviso", msg, **kw)
 
     def falha(self, msg, **kw):
-        self.escreve("erro", msg=msg, **kw)
-        raise ErroJatai(f"\n[ERRO] passo {self.passo} | {self.onde()}\n{msg}")
+        self._relata("erro", msg, **kw)
 
     def exige(self, cond, msg):
         if not cond:
-            self.falha(msg)
+            self._relata("erro", msg)
 
     @contextlib.contextmanager
     def trecho(self, nome):
@@ -158,7 +211,7 @@ class Registro:
     def novo_passo(self, passo):
         self.passo = passo
         self.lancamentos = []
-        self._cronos = []
+        self.cronometro.pares = []
         if self.lib is not None:
             self.lib.jt_erro_limpa()
 
@@ -168,14 +221,12 @@ class Registro:
         kid = len(self.lancamentos)
         self.lancamentos.append(Lancamento(kid, op, self.onde(), entradas, tuple(forma_saida) if forma_saida else None))
         if self.perfil and tempo:
-            par = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            par[0].record()
-            self._cronos.append((op, *par))
+            self.cronometro.abre(op)
         return kid
 
     def depois(self, kid, codigo):
-        if self.perfil and self._cronos:
-            self._cronos[-1][2].record()
+        if self.perfil:
+            self.cronometro.fecha_ultimo()
         if codigo != 0:
             l = self.lancamentos[kid]
             self.falha(f"the HIP runtime refused the launch of '{l.op}' (hipError {codigo}); inputs {_formas(l.entradas)}")
@@ -214,88 +265,92 @@ class Registro:
         self.falha(ev.mensagem(), codigo=ev.codigo, op=ev.lancamento.op, idx=ev.idx, valor=ev.valor, aux=ev.aux, arquivo=ev.arquivo)
 
     def fim_passo(self):
+        """End of a step: the device record is read (an event raises), and with `perfil` the step's op times are
+        added to the running totals."""
         if self.lib is not None:
             self.confere_device()
         if self.perfil:
-            torch.cuda.synchronize()
-            for op, a, b in self._cronos:
-                self.tempos[op] = self.tempos.get(op, 0.0) + a.elapsed_time(b)
+            self.cronometro.soma_em(self.tempos)
+            self.passos_medidos += 1
 
-    def relatorio_tempos(self, passos):
+    def relatorio_tempos(self, passos=None):
+        """Logs (and echoes) the GPU time per op since the last report -- launches and milliseconds per step,
+        microseconds per launch, share and running share of the step -- and restarts the totals."""
         if not self.tempos:
-            return
-        tot = sum(self.tempos.values())
-        ordem = sorted(self.tempos.items(), key=lambda kv: -kv[1])
-        linhas = [f"  {op:24s} {ms / passos:8.3f} ms/step  {100 * ms / tot:5.1f}%" for op, ms in ordem]
-        self.info("GPU time per op:\n" + "\n".join(linhas) + f"\n  {'total':24s} {tot / passos:8.3f} ms/step",
-                  tempos={k: v / passos for k, v in self.tempos.items()})
-        self.tempos = {}
+            return None
+        passos = passos or max(self.passos_medidos, 1)
+        total = sum(ms for _, ms in self.tempos.values())
+        tabela, acumulado = [], 0.0
+        for op, (n, ms) in sorted(self.tempos.items(), key=lambda kv: -kv[1][1]):
+            acumulado += ms
+            tabela.append(dict(op=op, lancamentos_por_passo=n / passos, ms_por_passo=ms / passos, us_por_lancamento=1e3 * ms / n,
+                               fracao=ms / total, fracao_acumulada=acumulado / total))
+        texto = [f"GPU time over {passos} step(s): {total / passos:.3f} ms per step"]
+        texto += [f"  {t['op']:28s} {t['lancamentos_por_passo']:6.1f} x {t['us_por_lancamento']:9.2f} us = {t['ms_por_passo']:8.3f} ms"
+                  f"  {100 * t['fracao']:5.1f}%  (cum. {100 * t['fracao_acumulada']:5.1f}%)" for t in tabela]
+        self.info("\n".join(texto), tempos=tabela)
+        self.tempos, self.passos_medidos = {}, 0
+        return tabela
 
     # ------------------------------------------------------------------ format guards
     def _formato(self, nome, m, E, tipo):
         """Block formats: mantissa `tipo` [R, C] with C a multiple of BLK, int8 exponents [R, C / BLK], both
         contiguous on the GPU (BLK read from jatai_amd.ops at call time)."""
-        erros = []
-        if m.dtype != tipo:
-            erros.append(f"mantissa {m.dtype}, expected {tipo}")
-        if E.dtype != torch.int8:
-            erros.append(f"exponent {E.dtype}, expected int8")
-        if not (m.is_cuda and E.is_cuda):
-            erros.append("not on the GPU")
-        if not (m.is_contiguous() and E.is_contiguous()):
-            erros.append("not contiguous")
-        if m.dim() != 2:
-            erros.append(f"mantissa of {m.dim()} dimensions, expected 2")
-        elif m.shape[1] % O.BLK:
-            erros.append(f"{m.shape[1]} columns, not a multiple of BLK={O.BLK}")
-        elif tuple(E.shape) != (m.shape[0], m.shape[1] // O.BLK):
-            erros.append(f"exponent shape {tuple(E.shape)}, expected {(m.shape[0], m.shape[1] // O.BLK)}")
+        erros = _problemas_tensor(m, tipo, "mantissa") + _problemas_tensor(E, torch.int8, "exponent")
+        if torch.is_tensor(m) and torch.is_tensor(E):
+            if m.dim() != 2:
+                erros.append(f"mantissa of {m.dim()} dimensions, expected 2")
+            elif m.shape[1] % O.BLK:
+                erros.append(f"{m.shape[1]} columns, not a multiple of BLK={O.BLK}")
+            elif tuple(E.shape) != (m.shape[0], m.shape[1] // O.BLK):
+                erros.append(f"exponent shape {tuple(E.shape)}, expected {(m.shape[0], m.shape[1] // O.BLK)}")
         if erros:
             self.falha(f"argument '{nome}': " + "; ".join(erros))
 
     def confere_bloco(self, nome, t):
-        m, E = t
-        if not (torch.is_tensor(m) and torch.is_tensor(E)):
-            self.falha(f"argument '{nome}': expected a (mantissa, exponent) pair of tensors, got {type(m)}, {type(E)}")
-        self._formato(nome, m, E, torch.int8)
+        self._formato(nome, t[0], t[1], torch.int8)
 
     def confere_r16(self, nome, t):
         self._formato(nome, t[0], t[1], torch.int16)
 
     def confere_cru(self, nome, t):
+        """Raw format: int32 accumulators and int16 exponents of one shape, contiguous on the GPU."""
         acc, e = t
-        erros = []
-        if acc.dtype != torch.int32:
-            erros.append(f"accumulator {acc.dtype}, expected int32")
-        if e.dtype != torch.int16:
-            erros.append(f"exponent {e.dtype}, expected int16")
-        if acc.shape != e.shape:
-            erros.append(f"shapes differ: {tuple(acc.shape)} and {tuple(e.shape)}")
-        if not (acc.is_cuda and acc.is_contiguous() and e.is_contiguous()):
-            erros.append("not on the GPU or not contiguous")
+        erros = _problemas_tensor(acc, torch.int32, "accumulator") + _problemas_tensor(e, torch.int16, "exponent")
+        if torch.is_tensor(acc) and torch.is_tensor(e) and acc.shape != e.shape:
+            erros.append(f"accumulator {tuple(acc.shape)} and exponent {tuple(e.shape)} shapes differ")
         if erros:
             self.falha(f"raw argument '{nome}': " + "; ".join(erros))
 
     # ------------------------------------------------------------------ statistics
     def estatistica(self, nome, t, zeros_normais=False):
-        """Summary of a block tensor, logged (torch reductions outside the hot path); warns on the patterns that
-        precede trouble: a tensor rounded to zero, a majority of zero mantissas, exponents near -126."""
+        """How well a block tensor uses its format, logged as one record (torch reductions, off the hot path):
+        share of zero blocks; over the other blocks, the exponent range and median, the mantissa bits the block
+        maximum uses (7 when the quantization is normalized), the share of zero and of saturated (+-127)
+        mantissas. Warns when every block is zero, when most mantissas of live blocks are zero (unless zeros are
+        expected, as after ReLU), when a block maximum uses fewer than 6 bits, and when an exponent comes within
+        16 of either end of the INT8 exponent range (-126 .. 126)."""
         m, E = t
+        blocos = m.reshape(m.shape[0], -1, O.BLK)
         vivos = E != O.E_ZERO
-        nz = bool(vivos.any())
-        rec = {
-            "nome": nome,
-            "zeros": round(float((m == 0).float().mean()), 4),
-            "blocos_zerados": round(float((~vivos).float().mean()), 4),
-            "exp_min": int(E[vivos].min()) if nz else None,
-            "exp_max": int(E[vivos].max()) if nz else None,
-            "maior_mantissa_media": round(float(m.abs().reshape(m.shape[0], -1, O.BLK).amax(-1).float().mean()), 1),
-        }
+        n_vivos = int(vivos.sum())
+        rec = {"nome": nome, "blocos": int(E.numel()), "blocos_zero": round(1 - n_vivos / max(E.numel(), 1), 4)}
+        if n_vivos:
+            ev = E[vivos].to(torch.int32)
+            mv = blocos[vivos].to(torch.int32)
+            maior = mv.abs().amax(-1)
+            bits = torch.where(maior > 0, torch.floor(torch.log2(maior.clamp(min=1).float())) + 1, torch.zeros_like(maior, dtype=torch.float32))
+            rec.update(exp_min=int(ev.min()), exp_mediana=int(ev.median()), exp_max=int(ev.max()),
+                       bits_usados=round(float(bits.mean()), 3), zeros_em_vivos=round(float((mv == 0).float().mean()), 4),
+                       saturados=round(float((mv.abs() == 127).float().mean()), 5))
         self.escreve("estatistica", **rec)
-        if not nz:
-            self.aviso(f"'{nome}' is all zero")
-        elif not zeros_normais and rec["zeros"] > 0.5:
-            self.aviso(f"'{nome}' has {rec['zeros']:.0%} zero mantissas: small values lost to rounding?")
-        if rec["exp_min"] is not None and rec["exp_min"] < -110:
-            self.aviso(f"'{nome}' has exponent {rec['exp_min']}, close to the INT8 limit -126")
+        if not n_vivos:
+            self.aviso(f"'{nome}': every block is zero")
+            return rec
+        if not zeros_normais and rec["zeros_em_vivos"] > 0.5:
+            self.aviso(f"'{nome}': {rec['zeros_em_vivos']:.0%} of the mantissas of its live blocks are zero")
+        if rec["bits_usados"] < 6:
+            self.aviso(f"'{nome}': block maxima use {rec['bits_usados']:.2f} of 7 mantissa bits on average")
+        if rec["exp_min"] < -110 or rec["exp_max"] > 110:
+            self.aviso(f"'{nome}': exponents {rec['exp_min']} .. {rec['exp_max']}, within 16 of the INT8 exponent range")
         return rec

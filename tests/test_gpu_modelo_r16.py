@@ -31,7 +31,7 @@ def test_passo_r16_vs_oraculo():
         cpu = CS.Gravador(OpsOraculo(32), host)
         mg = Modelo(V, D, H, FF, L, 0, "cuda", gpu, reg, r16=True)
         mc = Modelo(V, D, H, FF, L, 0, "cpu", cpu, TR.RegStub(), r16=True)
-        mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.rms_soma = mg.perda_fundida = False
+        mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.transposta_na_relu2 = mg.rms_soma = mg.perda_fundida = False
         mg.soma16_fundida = False
         mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg, r16=True)
         assert mf.soma16_fundida

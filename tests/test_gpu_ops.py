@@ -346,6 +346,32 @@ def test_gemm_relu2_back_t(M, N, K):
         _compara(Gt, cpu.ops.transpoe(tuple(torch.from_numpy(host(t)) for t in ref)), "transpoe (oracle)")
 
 
+@pytest.mark.parametrize("M,N,K,bm", [(2048, 2048, 512, 0), (256, 384, 96, 0), (64, 128, 32, 0), (512, 1024, 1536, 64),
+                                      (512, 512, 4096, 32)])
+def test_gemm_relu2_t(M, N, K, bm):
+    """Mode 3 with the transposed copy of its ReLU^2 output (BLK = 32): h and a equal gemm_relu2's and the copy
+    equals transpoe(a), at the automatic tile (128 rows at config 4's shape) and at forced 64- and 32-row tiles."""
+    blk = 32
+    gpu = GPU(blk, vigiar=True)
+    s = lambda t: R.substream(96, f"{M} {N} {K} {t}")
+    A = tuple(gpu.dev(v) for v in R.bloco(s("A"), M, K, blk, espalha=4, e0=-6, zera=0.05))
+    B = tuple(gpu.dev(v) for v in R.bloco(s("B"), N, K, blk, espalha=4, e0=-9))
+    o = gpu.ops
+    try:
+        o.lib.jt_gemm_bm(bm)
+        h, a, at = o.gemm_relu2_t(A, B)
+    finally:
+        o.lib.jt_gemm_bm(0)
+    hr, ar = o.gemm_relu2(A, B)
+    _compara(h, hr, "gemm_relu2: h")
+    _compara(a, ar, "gemm_relu2: a")
+    if M % 128 == 0:
+        _compara(at, o.transpoe(ar), "transpoe")
+    else:                                                            # transpoe needs R % 128: check against the oracle
+        cpu = CPU(blk)
+        _compara(at, cpu.ops.transpoe(tuple(torch.from_numpy(host(t)) for t in ar)), "transpoe (oracle)")
+
+
 @pytest.mark.parametrize("blk,D", [(32, 512), (128, 256), (32, 1024)])
 def test_rms_back_soma(blk, D):
     """soma(x, rms_back(g, y, cache)) in one launch equals the two ops."""

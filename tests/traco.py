@@ -48,6 +48,7 @@ def roda(ops, reg, dev, passos, host, nome="trace_r.json"):
     m.dw_em_lote = False
     m.quant_na_atencao = False
     m.transposta_na_gemm = False
+    m.transposta_na_relu2 = False
     m.rms_soma = False
     m.soma16_fundida = False
     m.perda_fundida = False
