@@ -154,9 +154,9 @@ int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const v
                        int H, int D, int GA, int limite, void* ws, long long ws_bytes, int kid);
 /* no reference counterpart; for callers that cannot allocate (code under graph capture, tight serving loops, harnesses
  * that forbid hipMalloc): jt_atencao_back_ws with its workspace in the library's own fixed device array of
- * jt_scratch_bytes() = 16 MiB per GPU (held until the process ends), no workspace argument, and no allocation of
+ * jt_scratch_bytes() = 32 MiB per GPU (held until the process ends), no workspace argument, and no allocation of
  * any kind. A shape whose jt_atencao_back_ws_bytes exceeds the array returns hipErrorOutOfMemory and launches
- * nothing (config 4's backward needs about 8.5 MB; config 5's, 66 MB, is refused). Every call on a GPU shares
+ * nothing (config 4's backward needs about 25 MB; config 5's, about 200 MB, is refused). Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (two streams or host threads) race. */
 int jt_atencao_back_sem_alocar(const void* gom, const void* goE, const void* qm, const void* qE, const void* P, void* Gacc, void* Ge,
                                int Bt, int T, int H, int D, int GA, int limite, int kid);

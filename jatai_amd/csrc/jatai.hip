@@ -793,7 +793,7 @@ int jt_atencao_back_ws(const void* gom, const void* goE, const void* qm, const v
 // nothing. Nothing in the workspace has to start at zero (every slot a kernel reads was written earlier in the
 // same call), so the array needs no clearing. Calls that overlap on one GPU (two streams, two host threads) share
 // the array and race.
-constexpr size_t SCRATCH_BYTES = (size_t)16 << 20;
+constexpr size_t SCRATCH_BYTES = (size_t)32 << 20;       // config 4's backward needs 25 MB
 static __device__ __align__(256) char scratch[SCRATCH_BYTES];
 }  // extern "C"
 // the device address of `scratch` on each device, looked up once per device with that device current (each GPU

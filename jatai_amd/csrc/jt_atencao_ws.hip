@@ -388,11 +388,15 @@ struct WsB {
     int* p1a;                        // [BH][SLOTS]: max |gP| per query tile, or max |dO| per 64 tokens (LIMITE)
     int* p1b;                        // [BH][SLOTS]: max ||v||_1 per 64 tokens (LIMITE)
     int *p2a, *p2b, *p2c;            // [BH][SLOTS]: max |P (gP' - s)|, or max P, max |gP'|, max |s| (LIMITE)
+    int* ds;                         // [BH][T/16 query tiles][T/16 key tiles][16][16]: P (gP' - s) before dS's shrink
 };
+// element (i, j) of head bh's dS before its shrink (|value| < 2^25: P <= 255, |gP' - s| < 2^17), in tile (i/16, j/16)
+// at row i % 16, column j % 16; written by k_atb2 for the causal tiles, read by k_atbqkv
+__device__ __forceinline__ size_t ds_pos(int bh, int nqt, int qt, int kt) { return (((size_t)bh * nqt + qt) * nqt + kt) * 256; }
 inline size_t bytes_back(long long BH, int T) {
     const size_t n = (size_t)BH * T;
     return 2 * (alinha256(n * 64) + alinha256(n * 2)) + 3 * alinha256(n * 64 * 2) + alinha256(n * 4) + alinha256((size_t)BH * 16) +
-           5 * alinha256((size_t)BH * SLOTS * 4);
+           5 * alinha256((size_t)BH * SLOTS * 4) + alinha256((size_t)BH * T * T * 4);
 }
 inline WsB parte_b(void* base, long long BH, int T) {
     const size_t n = (size_t)BH * T;
@@ -411,14 +415,16 @@ inline WsB parte_b(void* base, long long BH, int T) {
     w.p1b = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
     w.p2a = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
     w.p2b = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
-    w.p2c = (int*)p;
+    w.p2c = (int*)p; p += alinha256((size_t)BH * SLOTS * 4);
+    w.ds = (int*)p;
     return w;
 }
-// maximum over n slots of head bh (all lanes read the same addresses)
+// maximum over the first n slots of head bh (every slot value is >= 0): lane i reads slot i (one load for the wave,
+// not a chain of n dependent ones), then a wave-wide maximum; call from uniform control flow
 __device__ __forceinline__ int max_slots(const int* s, int bh, int n) {
-    int m = 0;
-    for (int i = 0; i < n; i++) m = max(m, s[bh * SLOTS + i]);
-    return m;
+    const int lane = threadIdx.x & 63;
+    const int v = lane < n ? s[(size_t)bh * SLOTS + lane] : 0;
+    return g_max<64>(v);
 }
 template <int LIMITE>
 __device__ __forceinline__ int sh_gp_ws(const WsB& w, int bh, int T) {
@@ -759,18 +765,25 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
         sl[v] = rnd_d(tot, 8);
         if (lr == 0 && wv == 0) w.sl[hb + i0 + v] = sl[v];
     }
+    // dS before its shrink, P (gP' - s) (0 past the diagonal, where P = 0), for k_atbqkv: rows 4 lg + v of tile
+    // (qt, t), column lr
+    int md = 0;
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {
+        if (n >= nv) continue;
+        int* dt = w.ds + atw::ds_pos(bh, nqt, qt, wv + 4 * n) + 16 * 4 * lg + lr;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int d = mul24((int)((pr[n] >> (8 * v)) & 255), x[n][v] - sl[v]);
+            dt[16 * v] = d;
+            md = max(md, abs(d));
+        }
+    }
     if (LIMITE) {
         const int a = wg_max4(pm, red), c = wg_max4(gm, red);
         const int d = wg_max4(max(max(abs(sl[0]), abs(sl[1])), max(abs(sl[2]), abs(sl[3]))), red);
         if (tid == 0) { w.p2a[bh * atw::SLOTS + qt] = a; w.p2b[bh * atw::SLOTS + qt] = c; w.p2c[bh * atw::SLOTS + qt] = d; }
     } else {
-        int md = 0;
-#pragma unroll
-        for (int n = 0; n < NTW; n++) {
-            if (n >= nv) continue;
-#pragma unroll
-            for (int v = 0; v < 4; v++) md = max(md, abs(mul24((int)((pr[n] >> (8 * v)) & 255), x[n][v] - sl[v])));
-        }
         md = wg_max4(md, red);
         if (tid == 0) w.p2a[bh * atw::SLOTS + qt] = md;
     }
@@ -817,27 +830,25 @@ __device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __r
     auto dw = reinterpret_cast<short (*)[16][LP]>(lds);
     auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     ATB_TILE_Q_(blk, nblk)
+    (void)P;
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
-    const Desl dsh(sh), dsh2(sh2);                                   // gP's and dS's shrinks, one shift each per head
+    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
     const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
     const int eds = ego + ev + sh - 9 + sh2;
-    const FragQ f = frag_q(w, hb, qt, lr, lg);
-    int sl[4];
+    // dS before its shrink, as k_atb2 stored it (0 past the diagonal): rows 4 lg + v of tile (qt, t), column lr
+    int dr[NTW][4];
 #pragma unroll
-    for (int v = 0; v < 4; v++) sl[v] = w.sl[hb + i0 + v];
-    const uint8_t* Pb = P + (size_t)bh * T * T;
+    for (int n = 0; n < NTW; n++) {                                  // loads of every n issued together: tiles past
+        const int t = min(wv + 4 * n, qt);                           // this wave's last re-read tile qt, unused
+        const int* dt = w.ds + atw::ds_pos(bh, nqt, qt, t) + 16 * 4 * lg + lr;
+#pragma unroll
+        for (int v = 0; v < 4; v++) dr[n][v] = dt[16 * v];
+    }
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
-        const int t = wv + 4 * n, j = 16 * t + lr;
-        int o[4];
-        gp_tile(w, hb, f, t, lr, lg, o);
-        const unsigned pr = *reinterpret_cast<const unsigned*>(Pb + (size_t)j * T + i0);
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int p = (pr >> (8 * v)) & 255;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(j <= i0 + v ? dsh2(mul24(p, dsh(o[v]) - sl[v])) : 0);
-        }
+        for (int v = 0; v < 4; v++) dw[wv][4 * lg + v][16 * n + lr] = (short)dsh2(dr[n][v]);
     }
     if (nv & 1)
 #pragma unroll
@@ -908,32 +919,33 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
     const size_t hb = (size_t)bh * T;
     const int nv = (nqt - kt - wv + 3) / 4;                          // this wave's query tiles kt + wv + 4 n, n < nv
     const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
-    const Desl dsh(sh), dsh2(sh2);                                   // gP's and dS's shrinks, one shift each per head
+    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
     const int ego = w.mx[bh * 4], eq = w.mx[bh * 4 + 1], ev = w.mx[bh * 4 + 3];
     const int eds = ego + ev + sh - 9 + sh2;
-    // v fragments of the tile's 16 keys as the A operand (rows = keys)
-    const size_t ja = hb + 16 * kt + lr;
     const int jr = 16 * kt + 4 * lg;                                 // this lane's 4 keys jr .. jr + 3
-    const long va0 = *reinterpret_cast<const long*>(w.vm8 + ja * 64 + 8 * lg), va1 = *reinterpret_cast<const long*>(w.vm8 + ja * 64 + 32 + 8 * lg);
-    int lx[4][2];
-#pragma unroll
-    for (int v = 0; v < 4; v++) { lx[v][0] = w.vL[(hb + jr + v) * 2]; lx[v][1] = w.vL[(hb + jr + v) * 2 + 1]; }
     const uint8_t* Pb = P + (size_t)bh * T * T;
+    // dS before its shrink, as k_atb2 stored it (0 past the diagonal): row lr (query 16 t + lr) of tile (t, kt),
+    // columns 4 lg .. 4 lg + 3 (this lane's keys), one 16-byte load; P of the same pairs
+    int4 dr[NTW];
+    int pv[NTW][4];
+#pragma unroll
+    for (int n = 0; n < NTW; n++) {                                  // loads of every n issued together: tiles past
+        const int t = min(kt + wv + 4 * n, nqt - 1), i = 16 * t + lr;   // this wave's last re-read tile nqt - 1, unused
+        dr[n] = *reinterpret_cast<const int4*>(w.ds + atw::ds_pos(bh, nqt, t, kt) + 16 * lr + 4 * lg);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int p = Pb[(size_t)(jr + v) * T + i];
+            pv[n][v] = i >= jr + v ? p : 0;
+        }
+    }
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
-        const int t = kt + wv + 4 * n, i = 16 * t + lr;               // this lane's query (column)
-        const size_t ig = hb + i;
-        int o[4];
-        tile_xyt(va0, va1, *reinterpret_cast<const long*>(w.gm8 + ig * 64 + 8 * lg), *reinterpret_cast<const long*>(w.gm8 + ig * 64 + 32 + 8 * lg),
-                 lx, w.gL[ig * 2], w.gL[ig * 2 + 1], o);
-        const int sl = w.sl[ig];
+        const int d4[4] = {dr[n].x, dr[n].y, dr[n].z, dr[n].w};
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int j = jr + v;
-            const int p = i >= j ? (int)Pb[(size_t)j * T + i] : 0;
-            dw[wv][4 * lg + v][16 * n + lr] = (short)(i >= j ? dsh2(mul24(p, dsh(o[v]) - sl)) : 0);
-            pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)p;
+            dw[wv][4 * lg + v][16 * n + lr] = (short)dsh2(d4[v]);
+            pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)pv[n][v];
         }
     }
     if (nv & 1)

@@ -5,10 +5,12 @@ the integer softmax outputs (d_alvo, soma) of the CPU oracle's trace, hence the 
   trace_r600.jsonl  600 steps at the reference model shape (BLK 128, 64 heads x 4); its first 32 steps are the
                     reference spec's own (trace_r.json), the rest the oracle's extension of them;
   trace_c4.jsonl    BASELINE config 4 (D 512, 8 heads x 64, FF 2048, 12 layers, Bt 8, T 256, BLK 32): the
-                    steps the oracle wrote (parity unpinned by the reference beyond the head-width-4 reduction);
+                    steps the oracle wrote, from ops pinned by the reference's goldens and an attention extension
+                    pinned by the head-width-4 reductions, the v = 0 closed form and the head-dimension
+                    permutation tests (tests/test_oracle.py);
   trace_c5.jsonl    BASELINE config 5 at its workload: 24 layers, Bt 64 x T 256 = 16384 tokens, the 16-bit
                     residual stream (modelo.py:60-130) -- the step bench.py times, with its grouped
-                    weight-gradient GEMMs at K = 16384.
+                    weight-gradient GEMMs at K = 16384: 10 steps.
 
 Both fixtures come from tests/golden/make_trace_oracle.py."""
 import json

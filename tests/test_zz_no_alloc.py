@@ -78,7 +78,7 @@ def test_sem_alocar_recusa_acima_do_maximo():
     lib = _lib()
     assert lib.jt_bloco(32) == 0
     lib.jt_atencao_mfma(1)
-    Bt, T, H, D = 64, 256, 8, 512                    # config 5: about 66 MB of workspace
+    Bt, T, H, D = 64, 256, 8, 512                    # config 5: about 200 MB of workspace
     M = Bt * T
     assert lib.jt_atencao_back_ws_bytes(Bt, T, H, D) > lib.jt_scratch_bytes()
     q, g = _entradas(R.substream(809, "recusa"), Bt, T, H, D)
