@@ -579,7 +579,7 @@ def cpu_baseline(c, segundos):
         if dt >= segundos:
             break
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=n * bt * c["T"] / dt, unit="tokens/s", cores=threads, kind="port",
+    return dict(value=n * bt * c["T"] / dt, unit="tokens/s", cores=threads, kind="port", host=cpu_maquina(),
                 sample=f"{n} training steps of the same {c['L']}-layer model at Bt={bt} x T={c['T']} on the int64 CPU oracle "
                        f"(oracle/jatai_oracle.cpp, OpenMP {threads} threads), {dt:.1f} s")
 
@@ -592,6 +592,28 @@ def cpu_modelo():
     except OSError:
         pass
     return "unknown CPU"
+
+
+def cpu_maquina():
+    """The host the CPU baselines ran on: lscpu's model name, sockets, cores per socket, threads per core and
+    logical CPUs, and the CPUs this process may use (`nproc`: its affinity mask)."""
+    import subprocess
+    d = dict(model=cpu_modelo(), nproc=len(os.sched_getaffinity(0)))
+    try:
+        texto = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return d
+    campos = {"Model name": ("model", str), "Socket(s)": ("sockets", int), "Core(s) per socket": ("cores_per_socket", int),
+              "Thread(s) per core": ("threads_per_core", int), "CPU(s)": ("cpus", int)}
+    for linha in texto.splitlines():
+        chave, _, valor = linha.partition(":")
+        if chave.strip() in campos and valor.strip():
+            nome, tipo = campos[chave.strip()]
+            try:
+                d[nome] = tipo(valor.strip())
+            except ValueError:
+                pass
+    return d
 
 
 def mede_fp32(c, segundos, dev="cpu", passos_min=2):
@@ -666,7 +688,7 @@ def mede_fp32(c, segundos, dev="cpu", passos_min=2):
     ultima = float(ultima)
     if dev == "cpu":
         threads = torch.get_num_threads()
-        return dict(value=n * bt * T / dt, unit="tokens/s", cores=threads, kind="port",
+        return dict(value=n * bt * T / dt, unit="tokens/s", cores=threads, kind="port", host=cpu_maquina(),
                     sample=f"{n} float32 training steps (forward, backward, SGD) of the same {L}-layer model at "
                            f"Bt={bt} x T={T} after one warm-up, PyTorch {torch.__version__} on {threads} threads of "
                            f"{cpu_modelo()}, {dt:.1f} s; last loss {ultima:.4f}")

@@ -106,6 +106,11 @@ int jt_transpoe_lote(const void* entradas, int n, int kid);
 int jt_entrada_t_bytes(void);          /* sizeof of one entry (40) */
 int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE, int M, int D, int V, int kid);
 int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid);
+/* Training windows of a byte corpus in device memory (no reference entry point: the reference draws them on the
+ * host, treino_int8_gpu/treino.py:41-44, and copies int64 tokens in). corpus: uint8 [n]; ini: int64 [Bt] window
+ * starts; tok, alvo: int32 [Bt, T] get corpus[ini[b] + t] and corpus[ini[b] + t + 1]. A start outside
+ * [0, n - T - 1] raises E_ARG (index b*T, value the start) and zeroes that row. */
+int jt_janelas(const void* corpus, long long n, const void* ini, void* tok, void* alvo, int Bt, int T, int kid);
 
 /* ---- rows (jatai_cuda.cu:1167-1176, 1195-1200): rms / rms_back take any D <= 1024 that is a multiple of BLK
  * (ops.py:453), softmax_ce any V <= 1024 that is a multiple of 128 (ops.py:496) */

@@ -446,6 +446,13 @@ int jt_embed(const void* Wm, const void* WE, const void* tok, void* Xm, void* XE
 #undef L
     return fim();
 }
+int jt_janelas(const void* corpus, long long n, const void* ini, void* tok, void* alvo, int Bt, int T, int kid) {
+    if (Bt <= 0 || T <= 0 || n < (long long)T + 1 || !corpus || !ini || !tok || !alvo) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)ini & 7) || ((uintptr_t)tok & 3) || ((uintptr_t)alvo & 3)) return (int)hipErrorInvalidValue;
+    const unsigned g = (unsigned)(((long long)Bt * T + 255) / 256);
+    k_janelas<<<g, 256, 0, g_stream>>>((const uint8_t*)corpus, n, (const long long*)ini, (int*)tok, (int*)alvo, Bt, T, kid);
+    return fim();
+}
 int jt_um_quente(const void* tok, void* U, void* UE, int M, int V, int kid) {
     if (M <= 0 || V % g_blk || V % 16) return (int)hipErrorInvalidValue;
     if (!alinhados(tok, U, UE)) return (int)hipErrorInvalidValue;

@@ -226,6 +226,22 @@ __global__ void __launch_bounds__(256) k_embed(const int8_t* __restrict__ Wm, co
         if (b * BLK >= c * 16) XE[(size_t)t * nb + b] = ok ? WE[(size_t)v * nb + b] : (int8_t)E_ZERO;
 }
 
+// Training windows of a byte corpus resident in device memory (treino_int8_gpu/treino.py:41-44): sequence b is the
+// T + 1 bytes from ini[b]; tok gets its first T and alvo its last T, as int32 token ids (the kernels' token type),
+// so the step's inputs are written in place with no host copy and no int64 -> int32 conversion. A start outside
+// [0, n - T - 1] is reported (E_ARG, index = b * T, value = the start, aux = n - T - 1) and its rows written as 0.
+__global__ void __launch_bounds__(256) k_janelas(const uint8_t* __restrict__ corpus, long long n, const long long* __restrict__ ini,
+                                                 int* __restrict__ tok, int* __restrict__ alvo, int Bt, int T, int kid) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)Bt * T) return;
+    const int b = (int)(i / T), t = (int)(i - (long long)b * T);
+    const long long s = ini[b], ult = n - T - 1;
+    const bool ok = s >= 0 && s <= ult;
+    if (!ok && t == 0) reporta(E_ARG, kid, (long long)b * T, s, ult);
+    tok[i] = ok ? (int)corpus[s + t] : 0;
+    alvo[i] = ok ? (int)corpus[s + t + 1] : 0;
+}
+
 // one-hot rows: U[t, tok[t]] = 1, exponent 0 (not -127) for every block (ops.py:147-151)
 template <int BLK>
 __global__ void __launch_bounds__(256) k_um_quente(const int* __restrict__ tok, int8_t* __restrict__ U, int8_t* __restrict__ UE, int M,

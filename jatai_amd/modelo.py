@@ -326,12 +326,16 @@ class PassoGravado:
     computed inside the graph too: a call returns the graph's loss tensor, which the next replay overwrites.
     """
 
-    def __init__(self, modelo, Bt, T, k_lr):
+    def __init__(self, modelo, Bt, T, k_lr, corpus=None):
         self.m, self.reg, self.k_lr = modelo, modelo.reg, k_lr
         lib = modelo.ops.lib
         # int32, the kernels' token type: the replay's copy_ converts, and the graph holds no conversion
         self.tok = torch.zeros(Bt, T, dtype=torch.int32, device=modelo.dev)
         self.alvo = torch.zeros(Bt, T, dtype=torch.int32, device=modelo.dev)
+        # with a device-resident corpus (jatai_amd.dados.Corpus) the graph starts with the window gather, and a
+        # step's only input is its Bt window starts
+        self.corpus, self.Bt, self.T = corpus, Bt, T
+        self.ini = torch.zeros(Bt, dtype=torch.int64, device=modelo.dev) if corpus is not None else None
         self.grafo = torch.cuda.CUDAGraph()
         est, vig, pi = modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira
         modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = False, False, True
@@ -342,6 +346,9 @@ class PassoGravado:
         try:
             with torch.cuda.graph(self.grafo):
                 lib.jt_stream(torch.cuda.current_stream().cuda_stream)
+                if corpus is not None:
+                    with self.reg.trecho("dados"):
+                        corpus.janelas(self.ini, T, self.tok, self.alvo)
                 self.d_alvo, self.soma = modelo.passo(self.tok, self.alvo, k_lr=k_lr)
                 self.perda = perda_de(self.d_alvo, self.soma, modelo.ops if modelo.perda_fundida else None)     # in the graph, as modelo.py:170 captures passo's loss
         finally:
@@ -351,8 +358,18 @@ class PassoGravado:
         self.reg.info(f"passo gravado num hipGraph: {len(self.lancamentos)} lancamentos", lancamentos=len(self.lancamentos))
 
     def __call__(self, tok, alvo):
+        if self.corpus is not None:
+            raise RuntimeError("this graph reads its tokens from its corpus: call de_corpus(gerador)")
         self.tok.copy_(tok)
         self.alvo.copy_(alvo)
+        self.reg.lancamentos = self.lancamentos
+        self.grafo.replay()
+        return self.perda
+
+    def de_corpus(self, gerador):
+        """One step on the batch that jatai_amd.dados.lote(dados, gerador, Bt, T) would draw: the Bt starts go to
+        the device (64 bytes at Bt = 8) and the graph's first node writes the windows into its token buffers."""
+        self.ini.copy_(self.corpus.inicios(gerador, self.Bt, self.T))
         self.reg.lancamentos = self.lancamentos
         self.grafo.replay()
         return self.perda

@@ -34,7 +34,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
            "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
            "jt_rms_back_soma", "jt_perda", "jt_gemm_tile", "jt_gemm_soma16", "jt_rms_back_soma16", "jt_atencao_ws_qs",
-           "jt_atencao_back_ws_qs")
+           "jt_atencao_back_ws_qs", "jt_janelas")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -375,6 +375,21 @@ class OpsHip:
         X = self._novo_bloco(M, D, m.device)
         self._lanca("embed", "jt_embed", (m, E, tok, X[0], X[1], M, D, V), dict(W=m, tok=tok), (M, D))
         return X
+
+    def janelas(self, corpus, ini, T, tok=None, alvo=None):
+        """Training windows from a device-resident byte corpus (treino_int8_gpu/treino.py:41-44 draws them on the
+        host): tok[b, t] = corpus[ini[b] + t], alvo[b, t] = corpus[ini[b] + t + 1], int32. corpus: uint8 [n] on the
+        device; ini: int64 [Bt] on the device. tok and alvo ([Bt, T] int32) are written in place when given."""
+        Bt, n = ini.numel(), corpus.numel()
+        if tok is None:
+            tok = torch.empty(Bt, T, dtype=torch.int32, device=corpus.device)
+        if alvo is None:
+            alvo = torch.empty(Bt, T, dtype=torch.int32, device=corpus.device)
+        self.reg.exige(corpus.dtype == torch.uint8 and ini.dtype == torch.int64, "janelas: corpus uint8 and ini int64")
+        self.reg.exige(tuple(tok.shape) == (Bt, T) and tuple(alvo.shape) == (Bt, T) and tok.dtype == torch.int32
+                       and alvo.dtype == torch.int32, f"janelas: tok and alvo must be int32 [{Bt}, {T}]")
+        self._lanca("janelas", "jt_janelas", (corpus, n, ini, tok, alvo, Bt, T), dict(ini=ini), (Bt, T), longos=(1,))
+        return tok, alvo
 
     def um_quente(self, tok, V):
         M = tok.numel()

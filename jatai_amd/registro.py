@@ -43,7 +43,7 @@ EVENTOS = {
     3: "mantissa beyond +-127 after the exponent bump",
     4: "division by zero (softmax sum <= 0)",
     5: "left shift would lose bits (result >= 2^30)",
-    6: "invalid argument (token or target outside the vocabulary)",
+    6: "invalid argument (token or target outside the vocabulary, or a corpus window past its end)",
 }
 
 

@@ -83,3 +83,31 @@ def sha(a):
     """SHA-256 of an array's C-contiguous little-endian bytes (dtype fixed by the caller)."""
     a = np.ascontiguousarray(a)
     return hashlib.sha256(a.tobytes()).hexdigest()
+
+
+# words of the synthetic byte corpus: 1- to 4-byte UTF-8 characters, JSON escapes (quote, backslash, newline, tab)
+_PALAVRAS = ("o", "a", "de", "que", "não", "ação", "coração", "está", "você", "pão", "the", "of", "and", "naïve",
+             "café", "über", "€5", "日本語", "한국어", "😀", "🚀ok", 'aspas "x"', "barra \\ y", "linha\nnova", "tab\tz",
+             "ñ", "ß", "Ωμέγα", "—", "…", "123", "")
+
+
+def corpus_sintetico(pasta, semente=1, linhas=(("Portuguese", 3012), ("English", 57))):
+    """Writes Portuguese.jsonl and English.jsonl (one {"text": ...} per line, as the reference's corpus) into `pasta`
+    and returns the texts per language. Line i of a file starts with "[<first letter><i>]"; its length and words
+    come from a SplitMix64 stream; every 97th line is empty text. Lines past 3000 exercise carregar's limit."""
+    import json
+    import os
+    textos = {}
+    for lingua, n in linhas:
+        s = substream(semente, "corpus:" + lingua)
+        tam = uniform_int(substream(s, "tam"), (n,), 0, 40)
+        pal = uniform_int(substream(s, "pal"), (n, 40), 0, len(_PALAVRAS) - 1)
+        ts = []
+        for i in range(n):
+            corpo = " ".join(_PALAVRAS[p] for p in pal[i, :tam[i]])
+            ts.append("" if i % 97 == 5 else f"[{lingua[0]}{i}] {corpo}")
+        with open(os.path.join(pasta, f"{lingua}.jsonl"), "w", encoding="utf-8") as f:
+            for t in ts:
+                f.write(json.dumps({"text": t, "id": len(t)}, ensure_ascii=(len(t) % 2 == 0)) + "\n")
+        textos[lingua] = ts
+    return textos
