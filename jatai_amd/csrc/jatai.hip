@@ -775,7 +775,7 @@ static int atencao_back_ws(const void* gom, const void* goE, const void* qm, con
 #define FASES(NTW, LM, B)                                                                                                 \
     {                                                                                                                     \
         if (!LM && smx) k_atb_prep_s<<<gp, 256, 0, g_stream>>>(go8, goE8, w, smx, T, H, D, g_blk, GA);                     \
-        else if (!LM && T <= 256) k_atb_prep<0, true><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA); \
+        else if (!LM && T <= 256) k_atb_prep<0, true><<<2 * gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA); \
         else k_atb_prep<LM><<<gp, 256, 0, g_stream>>>(go8, goE8, q8, qE8, w, T, H, D, g_blk, GA);                         \
         if (!LM && (smx || T > 256)) k_atb1<NTW><<<gt, 256, 0, g_stream>>>(w, T, H);                                      \
         k_atb2<NTW, LM><<<gt, 256, 0, g_stream>>>(w, P8, T, H, D, kid);                                                    \

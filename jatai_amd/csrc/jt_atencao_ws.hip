@@ -449,21 +449,166 @@ __device__ __forceinline__ int wg_max4(int v, int (&red)[4]) {
     return r;
 }
 
-// GP (exact variant, T <= 256): also max |gP| over the causal pairs of each of the part's four query tiles, what
-// k_atb1 computes, into the same slots: each wave takes one query tile, with v of keys 0 .. 64 part + 63 as m8 << L
-// fragments in LDS (the q, k tiles once written out; the earlier keys' v converted here again) and the part's dO
-// fragments in the dO tile. Parts are then taken in decreasing order (the last part has the most key tiles).
+// GP (exact variant, T <= 256): the launch also computes max |gP| over the causal pairs of every query tile, what
+// k_atb1 computes, into the same slots, in workgroups of their own that run beside the conversion workgroups:
+// blocks [0, BH T/64) take the per-tile maxima, the next BH T/64 the conversions. Workgroup g of head bh takes
+// query tiles {a, n - 1 - a} for a = g and a = n/2 - 1 - g (n = T/16 query tiles): 2 (n + 1) causal tile pairs,
+// the same for every g, dealt round-robin to its four waves. It converts the dO rows of its four query tiles and v
+// of keys 0 .. 16 (n - 1 - g) + 15 itself (m8 << L fragments in LDS, rows 72 bytes apart), so it waits for no
+// other workgroup.
+template <int LIMITE>
+__device__ __forceinline__ void atb_gp(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
+                                       const int8_t* __restrict__ qE, atw::WsB& w, int T, int H, int D, int blk, int GA, int BH,
+                                       int8_t* lds, int (&red)[4][4]) {
+    constexpr int HD = 64, RS = 72;
+    static_assert(3 * sizeof(TileT) >= 256 * RS + 64 * RS + 128 + 512, "atb_gp's LDS fits k_atb_prep's tiles");
+    const int bh = (int)blockIdx.x % BH, g = (int)blockIdx.x / BH, b = bh / H, h = bh % H;
+    const int ld = 3 * D, b0 = b * T, tid = threadIdx.x, nbl = ld / blk, nbg = D / blk, nqt = T / 16;
+    const int c4 = tid & 3, half = c4 >> 1, tl = tid >> 2, colg = h * HD + 16 * c4;
+    const int a1 = g, a2 = nqt / 2 - 1 - g;
+    const int qs0 = a1, qs1 = nqt - 1 - a1, qs2 = a2, qs3 = nqt - 1 - a2;
+    const int nk = 16 * qs1 + 16;                                     // keys 0 .. nk - 1 (qs1 is the last tile)
+    int8_t* vm_s = lds;                                               // [T][RS]
+    int8_t* dm_s = vm_s + 256 * RS;                                   // [64][RS]: rows 16 i + r of query tile qs_i
+    int8_t* dl_s = dm_s + 64 * RS;                                    // [64][2]
+    int8_t* vl_s = dl_s + 128;                                        // [T][2]
+    // every operand load first: v of 64-key chunk r (key 64 r + tl), dO of row tl of the four query tiles
+    int4 rx[4];
+    int ex[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        if (64 * r < nk) {
+            const int key = 64 * r + tl;
+            rx[r] = ld16(qm + (size_t)(b0 + key) * ld + 2 * D + colg);
+            ex[r] = qE[(size_t)(b0 + key) * nbl + (2 * D + colg) / blk];
+        }
+    const int qti = tl >> 4, qt_l = qti == 0 ? qs0 : qti == 1 ? qs1 : qti == 2 ? qs2 : qs3;
+    const int tq = 16 * qt_l + (tl & 15);
+    const int4 rg = ld16(gom + (size_t)(b0 + tq) * D + colg);
+    const int egt = goE[(size_t)(b0 + tq) * nbg + colg / blk];
+    int emv, emg;
+    {
+        int mv = SEM_TOPO, mg = SEM_TOPO;
+        for (int tk = tid; tk < T; tk += 256) {
+            mv = max(mv, emx_fatia(qE + (size_t)(b0 + tk) * nbl, 2 * D + h * HD, blk));
+            mg = max(mg, emx_fatia(goE + (size_t)(b0 + tk) * nbg, h * HD, blk));
+        }
+        mv = g_max<64>(mv);
+        mg = g_max<64>(mg);
+        if ((tid & 63) == 0) { red[0][tid >> 6] = mv; red[1][tid >> 6] = mg; }
+        __syncthreads();
+        emv = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+        emg = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+    }
+    auto guarda16 = [](int8_t* d, const int8_t (&m)[16]) {             // two 8-byte stores (rows are 8-byte aligned)
+        long x = 0, y = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) { x |= (long)(uint8_t)m[k] << (8 * k); y |= (long)(uint8_t)m[8 + k] << (8 * k); }
+        reinterpret_cast<long*>(d)[0] = x;
+        reinterpret_cast<long*>(d)[1] = y;
+    };
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        if (64 * r < nk) {
+            int v[16];
+            abre_i8(rx[r], v);
+            const int sft = emv - ex[r];
+            int8_t m8[16];
+            int L = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) { int x; m8_L(v[k], sft, GA, x, L); m8[k] = (int8_t)x; }
+            guarda16(vm_s + (64 * r + tl) * RS + 16 * c4, m8);
+            if ((c4 & 1) == 0) vl_s[(64 * r + tl) * 2 + half] = (int8_t)L;
+        }
+    {
+        int v[16];
+        abre_i8(rg, v);
+        const int sft = emg - egt;
+        int8_t m8[16];
+        int L = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) { int x; m8_L(v[k], sft, GA, x, L); m8[k] = (int8_t)x; }
+        guarda16(dm_s + tl * RS + 16 * c4, m8);
+        if ((c4 & 1) == 0) dl_s[tl * 2 + half] = (int8_t)L;
+    }
+    __syncthreads();
+    // pair k of the list (query tile i, key tile kt) for kt = 0 .. qs_i, i = 0 .. 3, goes to wave k % 4
+    const int wv = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int n0 = qs0 + 1, n01 = n0 + qs1 + 1, n012 = n01 + qs2 + 1, np = n012 + qs3 + 1;
+    int mg0 = 0, mg1 = 0, mg2 = 0, mg3 = 0;
+    for (int k0 = wv; k0 < np; k0 += 16) {                             // four pairs in flight
+        long da0[4], da1[4], vb0[4], vb1[4];
+        int lxs[4][2], l0[4], l1[4], iq[4], ktile[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int k = min(k0 + 4 * u, np - 1);                    // past the list: a repeat, not counted
+            const int i = k < n0 ? 0 : k < n01 ? 1 : k < n012 ? 2 : 3;
+            const int kt = k - (i == 0 ? 0 : i == 1 ? n0 : i == 2 ? n01 : n012);
+            iq[u] = i; ktile[u] = kt;
+            const int8_t* da = dm_s + (16 * i + lr) * RS + 8 * lg;
+            da0[u] = *reinterpret_cast<const long*>(da);
+            da1[u] = *reinterpret_cast<const long*>(da + 32);
+            const long lxw = *reinterpret_cast<const long*>(dl_s + (16 * i + 4 * lg) * 2);   // L of rows 4 lg .. 4 lg + 3
+            lxs[u][0] = (int)lxw; lxs[u][1] = (int)(lxw >> 32);
+            const int j = 16 * kt + lr;
+            const int8_t* vb = vm_s + j * RS + 8 * lg;
+            vb0[u] = *reinterpret_cast<const long*>(vb);
+            vb1[u] = *reinterpret_cast<const long*>(vb + 32);
+            const int lv = *reinterpret_cast<const unsigned short*>(vl_s + j * 2);
+            l0[u] = (int)(int8_t)lv; l1[u] = (int)(int8_t)(lv >> 8);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (k0 + 4 * u >= np) break;                               // uniform
+            const int i = iq[u], qt = i == 0 ? qs0 : i == 1 ? qs1 : i == 2 ? qs2 : qs3;
+            int lx[4][2];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int wd = lxs[u][v >> 1] >> (16 * (v & 1));
+                lx[v][0] = (int)(int8_t)wd; lx[v][1] = (int)(int8_t)(wd >> 8);
+            }
+            int o[4];
+            tile_xyt(da0[u], da1[u], vb0[u], vb1[u], lx, l0[u], l1[u], o);
+            const int j = 16 * ktile[u] + lr, i0 = 16 * qt + 4 * lg;
+            int m = 0;
+#pragma unroll
+            for (int v = 0; v < 4; v++) if (j <= i0 + v) m = max(m, abs(o[v]));
+            mg0 = i == 0 ? max(mg0, m) : mg0;
+            mg1 = i == 1 ? max(mg1, m) : mg1;
+            mg2 = i == 2 ? max(mg2, m) : mg2;
+            mg3 = i == 3 ? max(mg3, m) : mg3;
+        }
+    }
+    mg0 = g_max<64>(mg0); mg1 = g_max<64>(mg1); mg2 = g_max<64>(mg2); mg3 = g_max<64>(mg3);
+    __syncthreads();                                                   // red was read above by every thread
+    if (lane == 0) { red[wv][0] = mg0; red[wv][1] = mg1; red[wv][2] = mg2; red[wv][3] = mg3; }
+    __syncthreads();
+    if (tid < 4) {
+        const int qt = tid == 0 ? qs0 : tid == 1 ? qs1 : tid == 2 ? qs2 : qs3;
+        w.p1a[bh * atw::SLOTS + qt] = max(max(red[0][tid], red[1][tid]), max(red[2][tid], red[3][tid]));
+    }
+}
+
 template <int LIMITE, bool GP = false>
 __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom, const int8_t* __restrict__ goE, const int8_t* __restrict__ qm,
                                                   const int8_t* __restrict__ qE, atw::WsB w, int T, int H, int D, int blk, int GA) {
     constexpr int HD = 64;
     __shared__ int red[4][4];
     __shared__ int red1[4];
-    __shared__ __align__(16) TileT tg, tqk[2];
-    TileT &tq = tqk[0], &tk = tqk[1];
-    const int nparts = T / 64, BH = (int)gridDim.x / nparts;
-    const int bh = GP ? (int)blockIdx.x % BH : (int)blockIdx.x / nparts;
-    const int part = GP ? nparts - 1 - (int)blockIdx.x / BH : (int)blockIdx.x % nparts, b = bh / H, h = bh % H;
+    __shared__ __align__(16) TileT tiles[3];                         // dO, q, k; or atb_gp's fragments (23.7 KB)
+    TileT &tg = tiles[0], &tq = tiles[1], &tk = tiles[2];
+    const int nparts = T / 64;
+    int wg = (int)blockIdx.x;
+    if constexpr (GP) {
+        static_assert(LIMITE == 0, "per-tile max |gP| belongs to the exact variant");
+        const int BH = (int)gridDim.x / (2 * nparts);
+        if (wg < BH * nparts) {                                        // uniform per workgroup
+            atb_gp<LIMITE>(gom, goE, qm, qE, w, T, H, D, blk, GA, BH, reinterpret_cast<int8_t*>(&tiles[0][0][0]), red);
+            return;
+        }
+        wg -= BH * nparts;
+    }
+    const int bh = wg / nparts, part = wg % nparts, b = bh / H, h = bh % H;
     const int ld = 3 * D, b0 = b * T, tid = threadIdx.x, nbl = ld / blk, nbg = D / blk;
     // thread (t, c4): dimensions 16 c4 .. 16 c4 + 15 of token t. Every value it converts is loaded first, so the
     // loads overlap the head maxima's reduction below.
@@ -498,15 +643,13 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
     }
     if (part == 0 && tid == 0) { w.mx[bh * 4] = emg - GA; w.mx[bh * 4 + 1] = emq - GA; w.mx[bh * 4 + 2] = emk - GA; w.mx[bh * 4 + 3] = emv - GA; }
     int amax = 0, v1 = 0;
-    int8_t gm8r[16], vm8r[16];                                       // this thread's dO and v fragments (GP reuses them)
-    int gLr = 0, vLr = 0;
     {   // dO: m8 << L fragments and aligned f16
         int v[16];
         abre_i8(rg, v);
         const int s = emg - egt;
         const Desl ds(s);
-        int8_t (&m8)[16] = gm8r;
-        int& L = gLr;
+        int8_t m8[16];
+        int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
@@ -522,8 +665,8 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         abre_i8(rv, v);
         const int s = emv - evt;
         const Desl ds(s);
-        int8_t (&m8)[16] = vm8r;
-        int& L = vLr;
+        int8_t m8[16];
+        int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
@@ -549,84 +692,6 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         v1 = quad_soma(v1);
         const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
         if (tid == 0) { w.p1a[bh * atw::SLOTS + part] = a; w.p1b[bh * atw::SLOTS + part] = c; }
-    }
-    if constexpr (GP) {
-        // LDS, rows 72 bytes apart (8-byte fragment reads of 16 consecutive rows fall in distinct banks): v m8 of keys
-        // 0 .. 64 part + 63 in the q, k tiles (256 x 72 bytes), this part's dO m8 [64][72] then the L bytes in tg
-        constexpr int RS = 72;
-        int8_t* vm_s = reinterpret_cast<int8_t*>(&tqk[0][0][0]);
-        int8_t* dm_s = reinterpret_cast<int8_t*>(&tg[0][0]);
-        int8_t* dl_s = dm_s + 64 * RS;                                // [64][2]
-        int8_t* vl_s = dl_s + 128;                                    // [256][2]
-        const int tl = tid >> 2;
-        // the earlier keys' raw v, loaded before the barrier that frees the tiles
-        int4 rx[3];
-        int ex[3];
-#pragma unroll
-        for (int r = 0; r < 3; r++)
-            if (r < part) {
-                const int tk2 = 64 * r + tl;
-                rx[r] = ld16(qm + (size_t)(b0 + tk2) * ld + 2 * D + colg);
-                ex[r] = qE[(size_t)(b0 + tk2) * nbl + (2 * D + colg) / blk];
-            }
-        auto guarda16 = [](int8_t* d, const int8_t (&m)[16]) {         // two 8-byte stores (rows are 8-byte aligned)
-            long a = 0, c = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) { a |= (long)(uint8_t)m[k] << (8 * k); c |= (long)(uint8_t)m[8 + k] << (8 * k); }
-            reinterpret_cast<long*>(d)[0] = a;
-            reinterpret_cast<long*>(d)[1] = c;
-        };
-        __syncthreads();                                              // grava_t64 has read the tiles
-        guarda16(dm_s + tl * RS + 16 * c4, gm8r);
-        guarda16(vm_s + (64 * part + tl) * RS + 16 * c4, vm8r);
-        if ((c4 & 1) == 0) { dl_s[tl * 2 + half] = (int8_t)gLr; vl_s[(64 * part + tl) * 2 + half] = (int8_t)vLr; }
-#pragma unroll
-        for (int r = 0; r < 3; r++)
-            if (r < part) {
-                int v[16];
-                abre_i8(rx[r], v);
-                const int s = emv - ex[r];
-                int8_t m8[16];
-                int L = 0;
-#pragma unroll
-                for (int k = 0; k < 16; k++) { int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a; }
-                guarda16(vm_s + (64 * r + tl) * RS + 16 * c4, m8);
-                if ((c4 & 1) == 0) vl_s[(64 * r + tl) * 2 + half] = (int8_t)L;
-            }
-        __syncthreads();
-        // wave wv: query tile qt = 4 part + wv (local rows 16 wv ..), key tiles 0 .. qt, as k_atb1's gp_tile
-        const int wv = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4, qt = 4 * part + wv;
-        const int8_t* da = dm_s + (16 * wv + lr) * RS + 8 * lg;
-        const long ga0 = *reinterpret_cast<const long*>(da), ga1 = *reinterpret_cast<const long*>(da + 32);
-        int lx[4][2];
-#pragma unroll
-        for (int v = 0; v < 4; v++) { lx[v][0] = dl_s[(16 * wv + 4 * lg + v) * 2]; lx[v][1] = dl_s[(16 * wv + 4 * lg + v) * 2 + 1]; }
-        const int i0 = 16 * qt + 4 * lg;
-        int mg = 0;
-        for (int t0 = 0; t0 <= qt; t0 += 4) {                         // four independent tiles in flight
-            long vb0[4], vb1[4];
-            int l0[4], l1[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int j = 16 * min(t0 + u, qt) + lr;              // past qt: a repeat of tile qt, not counted
-                const int8_t* vb = vm_s + j * RS + 8 * lg;
-                vb0[u] = *reinterpret_cast<const long*>(vb);
-                vb1[u] = *reinterpret_cast<const long*>(vb + 32);
-                l0[u] = vl_s[j * 2];
-                l1[u] = vl_s[j * 2 + 1];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                if (t0 + u > qt) break;                               // uniform
-                const int j = 16 * (t0 + u) + lr;
-                int o[4];
-                tile_xyt(ga0, ga1, vb0[u], vb1[u], lx, l0[u], l1[u], o);
-#pragma unroll
-                for (int v = 0; v < 4; v++) if (j <= i0 + v) mg = max(mg, abs(o[v]));
-            }
-        }
-        mg = g_max<64>(mg);
-        if (lane == 0) w.p1a[bh * atw::SLOTS + qt] = mg;
     }
 }
 
