@@ -335,7 +335,8 @@ def tabela_kernels(c, gem, dw, ops2, ot, ms_passo):
                     per_step=dw["launches"], TOPS=t / 1e12, frac_i8_peak=t / PEAK_I8, frac_format_bound=t / lim))
     for nome, chave, n in (("attention forward", "atencao_q", L), ("attention backward", "atencao_back_q", L)):
         if chave in ops2:
-            lin.append(dict(name=nome, kernel="k_atf_prep + k_atf" if "back" not in chave else "k_atb_prep + k_atb1 + k_atb2 + k_atbqkv",
+            lin.append(dict(name=nome, kernel="k_atf_prep + k_atf" if "back" not in chave else
+                            "k_atb_prep + k_atb2 + k_atbqkv" if c["T"] <= 256 else "k_atb_prep + k_atb1 + k_atb2 + k_atbqkv",
                             us=ops2[chave]["us"], per_step=n))
     for nome, chave, n in (("rms", "rms", 2 * L + 1), ("rms_back + soma", "rms_back+soma", 2 * L)):
         e = ops2[chave]
