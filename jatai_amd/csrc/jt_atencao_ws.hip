@@ -186,11 +186,12 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
 // Outputs of 16 rows x the head's 64 columns in block format (BLK = 32: two blocks per row): thread t holds row
 // t / 16, columns 4 (t % 16) .. + 3; the 8 lanes of a block are consecutive. Same result as quant of the raw
 // output (ops.py:125-126) with the block's common exponent e.
+template <bool NT = true>
 __device__ __forceinline__ void grava_bloco4(const int (&v)[4], int e, int8_t* __restrict__ Mm, int8_t* __restrict__ ME, size_t x, size_t xe,
                                              int kid) {
     int8_t q[4];
     const int E = quant8_u8<4, 8>(v, e, q, kid, (long long)x);
-    grava_i8(Mm + x, q);
+    grava_i8<4, NT>(Mm + x, q);
     if ((threadIdx.x & 7) == 0) ME[xe] = (int8_t)E;
 }
 
@@ -348,7 +349,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
             ov[k] = (int)(so[0][r][c + k] + so[1][r][c + k] + so[2][r][c + k] + so[3][r][c + k]);
             if (ov[k] >= LIM || ov[k] <= -LIM) reporta(E_ACUM, kid, x + k, ov[k], -3);
         }
-        grava_bloco4(ov, ev - 8, (int8_t*)Oacc_, (int8_t*)Oe_, x, (size_t)(b0 + 16 * qt + r) * (D / 32) + (h * HD + c) / 32, kid);
+        grava_bloco4<false>(ov, ev - 8, (int8_t*)Oacc_, (int8_t*)Oe_, x, (size_t)(b0 + 16 * qt + r) * (D / 32) + (h * HD + c) / 32, kid);
         return;
     }
     int* Oacc = (int*)Oacc_;

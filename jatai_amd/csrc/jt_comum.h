@@ -414,16 +414,30 @@ __device__ __forceinline__ void le_i8(const int8_t* p, int (&v)[N]) {
             for (int i = 0; i < 4; i++) v[4 * j + i] = (int)(int8_t)(ws[j] >> (8 * i));
     }
 }
-template <int N>
+// N int8 values packed into one store. NT (the default): a non-temporal store (global_store ... nt), which
+// leaves fewer lines of the step's large outputs for the kernel's end-of-launch L2 write-back to other XCDs'
+// readers (config-4 step 2.918 -> 2.909 ms); the attention forward's output keeps plain stores (its reader, the
+// next GEMM, measured faster so).
+template <int N, bool NT = true>
 __device__ __forceinline__ void grava_i8(int8_t* p, const int8_t (&m)[N]) {
+    typedef int nt2 __attribute__((ext_vector_type(2)));
+    typedef int nt4 __attribute__((ext_vector_type(4)));
     int ws[(N + 3) / 4];
 #pragma unroll
     for (int j = 0; j < N / 4; j++)
         ws[j] = (int)(uint8_t)m[4 * j] | ((int)(uint8_t)m[4 * j + 1] << 8) | ((int)(uint8_t)m[4 * j + 2] << 16) |
                 ((int)(uint8_t)m[4 * j + 3] << 24);
-    if constexpr (N == 4) *reinterpret_cast<int*>(p) = ws[0];
-    else if constexpr (N == 8) *reinterpret_cast<int2*>(p) = make_int2(ws[0], ws[1]);
-    else *reinterpret_cast<int4*>(p) = make_int4(ws[0], ws[1], ws[2], ws[3]);
+    if constexpr (!NT) {
+        if constexpr (N == 4) *reinterpret_cast<int*>(p) = ws[0];
+        else if constexpr (N == 8) *reinterpret_cast<int2*>(p) = make_int2(ws[0], ws[1]);
+        else *reinterpret_cast<int4*>(p) = make_int4(ws[0], ws[1], ws[2], ws[3]);
+    } else if constexpr (N == 4) {
+        __builtin_nontemporal_store(ws[0], reinterpret_cast<int*>(p));
+    } else if constexpr (N == 8) {
+        __builtin_nontemporal_store(nt2{ws[0], ws[1]}, reinterpret_cast<nt2*>(p));
+    } else {
+        __builtin_nontemporal_store(nt4{ws[0], ws[1], ws[2], ws[3]}, reinterpret_cast<nt4*>(p));
+    }
 }
 // 16 int8 values: one 16-byte load, and its unpacking to ints (split so that loads can be issued early)
 __device__ __forceinline__ int4 ld16(const int8_t* p) { return *reinterpret_cast<const int4*>(p); }
