@@ -90,12 +90,17 @@ int jt_para8(const void* xm, const void* xE, void* ym, void* yE, long long nbloc
 int jt_soma16(const void* xm, const void* xE, const void* ym, const void* yE, void* zm, void* zE, long long nblocos, int kid);
 
 /* ---- no reference counterpart: momento then peso for ntab tensors in one launch. `tabela` is a device array of
- * ntab entries {const int* gacc; const int16_t* ge; int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE; long long inicio, nblocos;
- * int M, N, compacto, pad;} sorted by inicio (the tensor's first block in a global numbering), ntab <= 256, nblocos =
- * the total; compacto = 1: ge is jt_gemm_lote's compact exponent vector of the [M, N] gradient (N % 16 == 0), else one
- * exponent per value. Results equal jt_momento followed by jt_peso on each tensor (ops.py:273-290). */
+ * ntab entries {const int* gacc; const int16_t* ge; int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE, *Tm, *TE; long long inicio,
+ * nblocos; int M, N, compacto, pad;} sorted by inicio (the tensor's first block in a global numbering), ntab <= 256,
+ * nblocos = the total; [M, N] the tensor's shape; compacto = 1: ge is jt_gemm_lote's compact exponent vector of the
+ * gradient (N % 16 == 0), else one exponent per value. Results equal jt_momento followed by jt_peso on each tensor
+ * (ops.py:273-290). jt_otimizador ignores Tm, TE. */
 int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid);
-int jt_tab_otim_bytes(void);           /* sizeof of one table entry (96) */
+int jt_tab_otim_bytes(void);           /* sizeof of one table entry (112) */
+/* The same with one workgroup per 32 x 128 tile (BLK 32; every entry with M % 32 == 0 and N % 128 == 0), also
+ * writing transpoe(W) of the new weight into Tm [N, M], TE [N, M / 32] where an entry sets them (null: not written):
+ * the weights' transposes of the next step's backward (ops.py:121-123) without a transpose launch. */
+int jt_otimizador_t(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid);
 
 /* ---- re-blocking, gathers (jatai_cuda.cu:1155-1166). transpoe: R % 128 == 0, C % 64 == 0. */
 int jt_transpoe(const void* X, const void* EX, void* Y, void* EY, int R, int C, int kid);

@@ -362,6 +362,14 @@ int jt_otimizador(const void* tabela, int ntab, long long nblocos, int k_lr, int
     return fim();
 }
 int jt_tab_otim_bytes() { return (int)sizeof(TabOtim); }
+// No reference counterpart: jt_otimizador with one workgroup per 32 x 128 tile, which also writes the transposes of
+// the new weights (entries with Tm, TE set). BLK 32; every entry M % 32 == 0, N % 128 == 0 (so nblocos % 128 == 0).
+int jt_otimizador_t(const void* tabela, int ntab, long long nblocos, int k_lr, int ef, int kid) {
+    if (nblocos <= 0 || ntab <= 0 || ntab > 256) return nblocos == 0 ? 0 : (int)hipErrorInvalidValue;
+    if (g_blk != 32 || nblocos % 128 || !alinhados(tabela)) return (int)hipErrorInvalidValue;
+    k_otimizador_t<<<(unsigned)(nblocos / 128), 256, 0, g_stream>>>((const TabOtim*)tabela, ntab, k_lr, ef, kid);
+    return fim();
+}
 int jt_para16(const void* xm, const void* xE, void* zm, void* zE, long long nblocos, int kid) {
     if (nblocos <= 0) return 0;
     if (!alinhados(xm, xE, zm, zE)) return (int)hipErrorInvalidValue;

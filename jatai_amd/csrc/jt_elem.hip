@@ -277,11 +277,13 @@ __global__ void __launch_bounds__(256) k_zera32(int* __restrict__ p, long long n
 // The tensor list is a device table of TabOtim entries (fixed addresses: parameters, momenta, residuals and the
 // persistent raw-gradient buffers of the model); entry t covers global blocks [inicio_t, inicio_t + nblocos_t).
 // compacto = 1: ge holds the gradient's exponents as the vectors ge[i] = RA_i (i < M), ge[M + j] = RB_j - 4 of the
-// grouped GEMM's compact output (the exponent of (i, j) is their sum); else one int16 per value.
+// grouped GEMM's compact output (the exponent of (i, j) is their sum); else one int16 per value. M, N: the tensor's
+// shape. Tm, TE (k_otimizador_t only, may be null): the transpose of the new weight, transpoe(W) [N, M] blocked
+// along M (ops.py:121-123).
 struct TabOtim {
     const int* gacc;
     const int16_t* ge;
-    int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE;
+    int8_t *Mm, *ME, *Wm, *WE, *Rm, *RE, *Tm, *TE;
     long long inicio, nblocos;
     int M, N, compacto, pad;
 };
@@ -328,9 +330,10 @@ __device__ __forceinline__ OtimEnt<NV> otim_le(const Otim& d, long long o, long 
 // Every shift below keeps |x| < 2^28 (the momentum terms by ec >= bitlen - 28 per value, the weight terms by
 // ec >= largest exponent + 7 - 27), so none of the spec's left-shift checks can fire and the shifts run without
 // branches (desl_f per value, Desl per block); a gradient value out of range is still reported.
+// qw, Ew: the new weight's mantissas and block exponent, for a caller that also writes its transpose
 template <int NV, int NL>
 __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)[NV], const OtimEnt<NV>& x, const Otim& d, long long o, long long w,
-                                             bool lider, int k_lr, int ef, int kid) {
+                                             bool lider, int k_lr, int ef, int kid, int (&qw)[NV], int& Ew) {
     int v[NV], ee[NV];
     const int em = x.me - 3;
     unsigned gmax = 0;
@@ -355,10 +358,10 @@ __device__ __forceinline__ void otim_valores(const int (&g)[NV], const int (&eg)
     const int ew = x.we, emk = Em - k_lr, er = x.re;
     const int ec = max(max(ew + 7, emk + 7), er + 7) - 27;
     const Desl dw(ec - ew), dm(ec - emk), dr(ec - er);
-    int alvo[NV], qw[NV];
+    int alvo[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) alvo[i] = dw(x.w(i)) - dm(q[i]) + dr(x.r(i));
-    const int Ew = quant8_u<NV, NL>(alvo, ec, qw, kid, o);
+    Ew = quant8_u<NV, NL>(alvo, ec, qw, kid, o);
     grava_q8(d.Wm + o, qw);
     if (lider) d.WE[w] = (int8_t)Ew;
     if (!ef) return;
@@ -401,5 +404,68 @@ __global__ void __launch_bounds__(256) k_otimizador(const TabOtim* __restrict__ 
     } else {
         le_i16(d.ge + o, eg);
     }
-    otim_valores<NVO, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid);
+    int qw[NVO], Ew;
+    otim_valores<NVO, LPB>(g, eg, x, ot, o, w, (threadIdx.x & (LPB - 1)) == 0, k_lr, ef, kid, qw, Ew);
+}
+
+// The same update with each workgroup on one 32 x 128 tile of a tensor (BLK = 32; every tensor with M % 32 == 0 and
+// N % 128 == 0; its blocks counted from inicio as in k_otimizador, so tile t of the launch is global blocks
+// 128 t .. 128 t + 127), which also writes the transpose of the new weight when the entry's Tm is set: the tile's
+// 128 columns are 128 blocks of 32 rows of transpoe(W), re-quantized from the new mantissas and block exponents
+// staged in LDS (quant of the transposed values with their exponents, ops.py:121-123). The weights' transposes the
+// next step's backward reads are then written here instead of by a separate launch.
+// LDS: mantissa rows of 128 bytes whose 16-byte chunk j sits at chunk j ^ (row / 16), and exponent rows 5 bytes
+// apart, so the column reads (two threads per column, rows 16 p .. 16 p + 15) fall in distinct banks.
+__global__ void __launch_bounds__(256) k_otimizador_t(const TabOtim* __restrict__ tab, int ntab, int k_lr, int ef, int kid) {
+    constexpr int NVO = 16, LPB = 2, BN = 128, ES = 5;
+    __shared__ long long ini[256];
+    __shared__ __align__(16) int8_t qs[32 * BN];
+    __shared__ int8_t es[32 * ES];
+    for (int i = threadIdx.x; i < ntab; i += blockDim.x) ini[i] = tab[i].inicio;
+    __syncthreads();
+    const long long b0 = (long long)blockIdx.x * 128;               // the tile's first global block (uniform)
+    int t = 0;
+    for (int s = 128; s; s >>= 1)
+        if (t + s < ntab && ini[t + s] <= b0) t += s;
+    const TabOtim d = tab[t];
+    const int tid = threadIdx.x, ntc = d.N / BN;
+    const long long tl = (b0 - d.inicio) / 128;                     // tile index in the tensor, row-major over tiles
+    const int row0 = (int)(tl / ntc) * 32, col0 = (int)(tl % ntc) * BN;
+    const int orow = tid >> 3, oc = 16 * (tid & 7);
+    const long long o = (long long)(row0 + orow) * d.N + col0 + oc, w = o / 32;
+    const Otim ot{d.Mm, d.ME, d.Wm, d.WE, d.Rm, d.RE};
+    const OtimEnt<NVO> x = otim_le<NVO>(ot, o, w, ef);
+    int g[NVO], eg[NVO];
+    le_i32(d.gacc + o, g);
+    if (d.compacto) {
+        const int er = d.ge[row0 + orow];
+        le_i16(d.ge + d.M + col0 + oc, eg);
+#pragma unroll
+        for (int j = 0; j < NVO; j++) eg[j] = max(-30000, er + eg[j]);
+    } else {
+        le_i16(d.ge + o, eg);
+    }
+    int qw[NVO], Ew;
+    otim_valores<NVO, LPB>(g, eg, x, ot, o, w, (tid & (LPB - 1)) == 0, k_lr, ef, kid, qw, Ew);
+    if (d.Tm == nullptr) return;                                     // uniform: one tensor per workgroup
+    int8_t q8[NVO];
+#pragma unroll
+    for (int i = 0; i < NVO; i++) q8[i] = (int8_t)qw[i];
+    grava_i8<NVO, false>(qs + orow * BN + 16 * ((oc >> 4) ^ ((orow >> 4) & 7)), q8);
+    if ((tid & (LPB - 1)) == 0) es[orow * ES + oc / 32] = (int8_t)Ew;
+    __syncthreads();
+    const int c = tid >> 1, pt = tid & 1;                            // column c, rows 16 pt .. 16 pt + 15
+    const int8_t* qc = qs + 16 * ((c >> 4) ^ pt) + (c & 15);
+    int tv[16], te[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int r = 16 * pt + k;
+        tv[k] = qc[r * BN];
+        te[k] = es[r * ES + (c >> 5)];
+    }
+    int8_t t8[16];
+    const long long ot2 = (long long)(col0 + c) * d.M + row0 + 16 * pt;
+    const int Et = quant8_d<16, 2>(tv, te, t8, kid, ot2);
+    grava_i8(d.Tm + ot2, t8);
+    if (pt == 0) d.TE[(size_t)(col0 + c) * (d.M / 32) + row0 / 32] = (int8_t)Et;
 }

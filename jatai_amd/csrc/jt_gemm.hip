@@ -527,7 +527,8 @@ __device__ __forceinline__ void gemm_corpo(const int8_t* __restrict__ A, const i
             int eg[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) eg[j] = max(-30000, base[j]);   // the raw output's int16 exponent
-            otim_valores<16, LPB>(v, eg, otx, ot, (long long)o, (long long)(o / BLK), lider, k_lr, ef, kid);
+            int qw[16], Ew;
+            otim_valores<16, LPB>(v, eg, otx, ot, (long long)o, (long long)(o / BLK), lider, k_lr, ef, kid, qw, Ew);
             return;
         }
         int8_t m[EV];

@@ -103,6 +103,13 @@ class Modelo:
         # so the stage can be timed between replays as the step runs it
         self.marcas = {}
         self._gbuf, self._tabela, self._gbuf_compacto = None, None, None
+        # the fused optimizer also writes transpoe(W) of every new weight but the embedding's (one workgroup per
+        # 32 x 128 tile, jt_otimizador_t), which the next step's backward then reads instead of transposing the
+        # weights again (BLK 32; the transposes are valid from the first fused update on, so the first step
+        # transposes as before). A caller that changes weights outside the optimizer calls invalida_transpostas().
+        self.transposta_no_otimizador = hasattr(ops, "tabela_otimizador") and O.BLK == 32 and all(
+            t[0].shape[0] % 32 == 0 and t[0].shape[1] % 128 == 0 for t in self.p.values())
+        self._pt, self._pt_validas, self._tabela_t = None, False, None
         # the grouped weight-gradient launch writes the exponents of the fused optimizer's gradient buffers as row
         # and column vectors (OpsHip)
         self.grad_compacto = hasattr(ops, "gemm_cru_lote") and hasattr(ops, "otimizador")
@@ -134,14 +141,26 @@ class Modelo:
         # M + N: the exponent of (i, j) is RA_i + RB_j - 4), 2 bytes per value fewer written by the GEMM and read by
         # the optimizer; a per-GEMM launch writes one exponent per value.
         compacto = bool(self.dw_em_lote and self.grad_compacto)
-        if self._gbuf is None or self._gbuf_compacto != compacto:
+        tw = self.transposta_no_otimizador
+        if self._gbuf is None or self._gbuf_compacto != compacto or self._tabela_t != tw:
             ordem = ["out"] + [f"{w}{l}" for l in reversed(range(self.L)) for w in ("Wd", "Wup", "Wo", "Wqkv")] + ["emb"]
             fe = lambda t: (t.shape[0] + t.shape[1],) if compacto else t.shape
             self._gbuf = {n: (torch.empty(self.p[n][0].shape, dtype=torch.int32, device=self.dev),
                               torch.empty(fe(self.p[n][0]), dtype=torch.int16, device=self.dev)) for n in ordem}
             self._gbuf_compacto = compacto
-            self._tabela = self.ops.tabela_otimizador([(self._gbuf[n], self.mom[n], self.p[n], self.res[n]) for n in ordem])
+            if tw and self._pt is None:         # transpoe(W) of each weight the backward reads: [N, M] blocked along M
+                self._pt = {n: (torch.empty(self.p[n][0].shape[::-1], dtype=torch.int8, device=self.dev),
+                                torch.empty(self.p[n][0].shape[1], self.p[n][0].shape[0] // O.BLK, dtype=torch.int8, device=self.dev))
+                            for n in ordem if n != "emb"}
+            self._tabela = self.ops.tabela_otimizador([(self._gbuf[n], self.mom[n], self.p[n], self.res[n],
+                                                        self._pt.get(n) if tw else None) for n in ordem])
+            self._tabela_t = tw
+            self._pt_validas = False
         return self._gbuf
+
+    def invalida_transpostas(self):
+        """The weights changed outside the optimizer: the next step transposes them again."""
+        self._pt_validas = False
 
     def _st(self, nome, t, zeros_normais=False):
         if self.estatisticas:
@@ -213,6 +232,10 @@ class Modelo:
         if self.transpostas_em_lote:
             with reg.trecho("transpostas"):
                 pesos = [p[f"{w}{l}"] for l in range(self.L) for w in ("Wd", "Wup", "Wo", "Wqkv")] + [p["out"]]
+                if self._pt_validas and self.otimizador_fundido and not self._otim_no_gemm():
+                    for n, Y in self._pt.items():          # written by the last fused update
+                        prontas[id(p[n][0])] = Y
+                    pesos = []
                 ativ = [t for c in caches for t in (c[8], c[5], c[4], c[0]) if id(t[0]) not in prontas] + [nf]   # a, n2, om, n1
                 for X, Y in zip(pesos + ativ, ops.transpoe_lote(pesos) + ops.transpoe_lote(ativ)):
                     prontas[id(X[0])] = Y
@@ -309,6 +332,7 @@ class Modelo:
         with reg.trecho("otimizador"):
             if self.otimizador_fundido:
                 ops.otimizador(self._tabela, k_lr, self.error_feedback)
+                self._pt_validas = bool(self._tabela_t)
                 return perda
             for n, gr in grads.items():
                 with reg.trecho(n):

@@ -34,7 +34,7 @@ FUNCOES = ("jt_gemm", "jt_gemm_f", "jt_quant", "jt_soma", "jt_relu2", "jt_relu2_
            "jt_atencao_ws", "jt_atencao_back_ws", "jt_gemm_lote", "jt_entrada_g_bytes",
            "jt_gemm_otim_lote", "jt_entrada_go_bytes", "jt_atencao_ws_q", "jt_atencao_back_ws_q",
            "jt_rms_back_soma", "jt_perda", "jt_gemm_tile", "jt_gemm_soma16", "jt_rms_back_soma16", "jt_atencao_ws_qs",
-           "jt_atencao_back_ws_qs", "jt_janelas")
+           "jt_atencao_back_ws_qs", "jt_janelas", "jt_otimizador_t")
 VOIDS = ("jt_stream", "jt_gemm_split", "jt_gemm_bm", "jt_atencao_linhas", "jt_atencao_mfma")
 
 
@@ -619,36 +619,48 @@ class OpsHip:
 
     # no reference counterpart: momento + peso of every tensor in one launch
     def tabela_otimizador(self, itens):
-        """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] with fixed addresses (updated in place). A
-        gradient whose exponent tensor is a vector of M + N (gemm_cru_lote's compact form) is read as such."""
-        itens = [tuple(it) for it in itens]
-        linhas, inicio = [], 0
-        for Gc, Mom, W, R in itens:
+        """Device table for `otimizador`. itens: [(grad raw, Mom, W, R)] or [(grad raw, Mom, W, R, Wt)] with fixed
+        addresses (updated in place); Wt = (mantissas [N, M], exponents [N, M / BLK]) receives transpoe(W) of the new
+        weight (BLK 32, M % 32 == 0, N % 128 == 0 for every tensor of the table; None: not written). A gradient whose
+        exponent tensor is a vector of M + N (gemm_cru_lote's compact form) is read as such."""
+        itens = [tuple(it) + (None,) * (5 - len(it)) for it in itens]
+        linhas, inicio, transpostas = [], 0, False
+        for Gc, Mom, W, R, Wt in itens:
+            M, N = W[0].shape
             compacto = Gc[1].dim() == 1 and Gc[0].dim() == 2
             if compacto:
-                M, N = Gc[0].shape
                 self.reg.exige(Gc[0].dtype == torch.int32 and Gc[1].dtype == torch.int16 and Gc[1].numel() == M + N and Gc[0].is_cuda
                                and Gc[0].is_contiguous() and Gc[1].is_contiguous() and N % 16 == 0,
                                f"otimizador: gradiente compacto (int32 {(M, N)}, int16 {(M + N,)}) esperado")
             else:
                 self.reg.confere_cru("grad", Gc)
-                M = N = 0                                   # read only for the compact form
             for n, t in (("momento", Mom), ("W", W), ("residuo", R)):
                 self.reg.confere_bloco(n, t)
+            if Wt is not None:
+                transpostas = True
+                self.reg.confere_bloco("W transposta", Wt)
+                self.reg.exige(tuple(Wt[0].shape) == (N, M), f"otimizador: transposta {tuple(Wt[0].shape)}, esperado {(N, M)}")
             nb = W[0].numel() // BLK
             self.reg.exige(Gc[0].numel() == W[0].numel() == Mom[0].numel() == R[0].numel(), "otimizador: formas diferentes")
-            linhas.append([t.data_ptr() for t in (Gc[0], Gc[1], Mom[0], Mom[1], W[0], W[1], R[0], R[1])] + [inicio, nb]
-                          + [(N << 32) | M, int(compacto)])
+            ptrs = [t.data_ptr() for t in (Gc[0], Gc[1], Mom[0], Mom[1], W[0], W[1], R[0], R[1])]
+            ptrs += [Wt[0].data_ptr(), Wt[1].data_ptr()] if Wt is not None else [0, 0]
+            linhas.append(ptrs + [inicio, nb, (N << 32) | M, int(compacto)])
             inicio += nb
         self.reg.exige(0 < len(linhas) <= 256, "otimizador: de 1 a 256 tensores")
-        self.reg.exige(self.lib.jt_tab_otim_bytes() == 96, "otimizador: tamanho de entrada da tabela inesperado")
-        tab = torch.tensor(linhas, dtype=torch.int64).to(W[0].device)
+        self.reg.exige(self.lib.jt_tab_otim_bytes() == 112, "otimizador: tamanho de entrada da tabela inesperado")
+        if transpostas:
+            self.reg.exige(BLK == 32 and all(W[0].shape[0] % 32 == 0 and W[0].shape[1] % 128 == 0 for _, _, W, _, _ in itens),
+                           "otimizador com transpostas: BLK 32 e tensores com M % 32 == 0, N % 128 == 0")
+        tab = torch.tensor(linhas, dtype=torch.int64).to(itens[0][2][0].device)
         # the table keeps every tensor whose address it holds alive for as long as it exists
-        return tab, len(linhas), inicio, tuple(t for it in itens for x in it for t in x)
+        vivos = tuple(t for it in itens for x in it if x is not None for t in x)
+        return tab, len(linhas), inicio, vivos, transpostas
 
     def otimizador(self, tabela, k, ef):
+        """momento + peso of every tensor of the table (and the transposes of the new weights where it holds them)."""
         tab, ntab, nblocos = tabela[:3]
-        self._lanca("otimizador", "jt_otimizador", (tab, ntab, nblocos, k, int(ef)), dict(), (nblocos * BLK,), longos=(2,))
+        fn = "jt_otimizador_t" if len(tabela) > 4 and tabela[4] else "jt_otimizador"
+        self._lanca("otimizador", fn, (tab, ntab, nblocos, k, int(ef)), dict(), (nblocos * BLK,), longos=(2,))
 
     def peso(self, W, Mom, R, k, ef):
         for n, t in (("W", W), ("momento", Mom), ("residuo", R)):

@@ -50,6 +50,10 @@ def test_passo_config4_vs_oraculo():
         assert abs(pf - pg) <= 1e-14 * abs(pg)     # the fused model's loss sums in another order
     est = lambda m: [R.sha(host(t)) for n in m.p for t in (*m.p[n], *m.mom[n], *m.res[n])]
     assert est(mf) == est(mg), "fused step differs from the op-by-op step"
+    # from its second step on, the fused model's backward read the weights' transposes its optimizer wrote
+    assert mf.transposta_no_otimizador and mf._pt_validas
+    assert not any(l.op == "transpoe" and any(x is mf.p[n][0] for x in l.entradas.values() if torch.is_tensor(x))
+                   for n in mf._pt for l in reg.lancamentos), "step 2 transposed a weight again"
     # a third step: the fused model as a captured hipGraph, the op-by-op model eagerly
     from jatai_amd.modelo import PassoGravado
     pgraf = PassoGravado(mf, Bt, T, 4)

@@ -456,6 +456,51 @@ def test_tabela_otimizador_mantem_tensores():
     assert [R.sha(host(t)) for t in (*w2, *mom2, *res2)] == esperado
 
 
+@pytest.mark.parametrize("compacto", [False, True])
+@pytest.mark.parametrize("ef", [True, False])
+def test_otimizador_t_igual_e_transpostas(ef, compacto):
+    """jt_otimizador_t (one workgroup per 32 x 128 tile, writing transpoe of each new weight) leaves the same weights,
+    momenta and residuals as jt_otimizador, and each transpose it writes equals transpoe of the new weight bit for bit
+    (ops.py:121-123); a tensor without a transpose target is updated alike. Weight shapes of config 4 (Wqkv, Wd, out);
+    the gradient exponents per value or in the grouped GEMM's compact form (row and column vectors)."""
+    blk = 32
+    gpu = GPU(blk)
+    formas = [(1536, 512), (512, 2048), (256, 512), (512, 512)]
+    itens_a, itens_b, ts = [], [], []
+    for i, (M, N) in enumerate(formas):
+        s = lambda t: R.substream(93, f"{i} {t}")
+        w = R.bloco(s("w"), M, N, blk, espalha=4, e0=-9)
+        mom = R.bloco(s("mom"), M, N, blk, e0=-15, zera=0.05)
+        res = R.bloco(s("res"), M, N, blk, e0=-20, zera=0.3)
+        acc, e = R.cru(s("gw"), M, N, bits=24, e0=-40)
+        if compacto:                        # exponent of (i, j) = ra_i + rb_j
+            ra = (-20 + R.uniform_int(s("ra"), (M,), -3, 3)).astype(np.int16)
+            rb = (-24 + R.uniform_int(s("rb"), (N,), -3, 3)).astype(np.int16)
+            gw = (acc, np.concatenate([ra, rb]))
+        else:
+            gw = (acc, e)
+        a = tuple(tuple(gpu.dev(v) for v in t) for t in (gw, mom, w, res))
+        b = tuple(tuple(x.clone() for x in t) for t in a)
+        tw = None if i == 3 else (torch.full((N, M), 99, dtype=torch.int8, device="cuda"),
+                                  torch.full((N, M // blk), 99, dtype=torch.int8, device="cuda"))
+        itens_a.append(a)
+        itens_b.append(b + (tw,))
+        ts.append(tw)
+    ta, tb = gpu.ops.tabela_otimizador(itens_a), gpu.ops.tabela_otimizador(itens_b)
+    assert not ta[4] and tb[4]
+    gpu.ops.otimizador(ta, 4, ef)
+    gpu.ops.otimizador(tb, 4, ef)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(itens_a, itens_b)):
+        for nome, x, y in zip(("momento", "W", "residuo"), a[1:], b[1:4]):
+            assert all(torch.equal(u, v) for u, v in zip(x, y)), f"tensor {i} {formas[i]}: {nome} differs"
+        if ts[i] is not None:
+            esperado = gpu.ops.transpoe(a[2])
+            assert torch.equal(ts[i][0], esperado[0]) and torch.equal(ts[i][1], esperado[1]), f"tensor {i}: transpose differs"
+        else:
+            assert ts[i] is None
+
+
 def _gemm_modos(ops, A, B, X):
     return [ops.gemm(A, B), ops.gemm(A, B, cru=True), ops.gemm_soma(A, B, X), ops.gemm_relu2(A, B), ops.gemm_relu2_back(A, B, X)]
 
