@@ -80,17 +80,17 @@ class Modelo:
         # that read those conversions lose 2.2 us, which they now fetch from HBM instead of from the cache the
         # backward's pass just wrote them to (config-4 step 3.132 -> 3.157 ms; config 5 34.23 either way)
         self.conversoes_salvas = False
-        # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand), on
-        # launches of at least 4 workgroups per CU: the epilogue's transposed write is a serial tail of each
-        # workgroup, hidden by the other resident workgroups of a large grid and exposed at one per CU, where the
-        # batched transpose is faster (config 4, 256 workgroups: step 3.183 ms fused, 3.162 batched; config 5, 8192
-        # workgroups: 34.62 fused, 34.76 batched)
+        # the ReLU^2-backward GEMM also writes the transpose of its output (the next weight gradient's operand). Its
+        # epilogue's transposed write is a serial tail of each workgroup, hidden by the other resident workgroups of
+        # a large grid (config 5, 8192 workgroups: step 34.76 -> 34.62 ms) and about what the batched transpose it
+        # replaces costs at one workgroup per CU (config 4: 2.9158 ms without it, 2.9151 with it). A workgroup
+        # threshold (t_na_gemm_min_wg: None = 4 per CU of the device, 0 = always) can keep small grids batched.
         self.transposta_na_gemm = hasattr(ops, "gemm_relu2_back_t")
-        self.t_na_gemm_min_wg = None    # the workgroup threshold (None: 4 per CU of the device; 0: always)
+        self.t_na_gemm_min_wg = 0
         # the same for the FFN-up GEMM's ReLU^2 output a, whose transpose the weight gradient of the FFN-down layer
-        # reads (training steps only; same workgroup threshold)
+        # reads (training steps only; config 4 with both: 2.9149 ms, and the batched transposes of the step halved)
         self.transposta_na_relu2 = hasattr(ops, "gemm_relu2_t")
-        self.t_na_relu2_min_wg = None
+        self.t_na_relu2_min_wg = 0
         # the residual update of the backward, soma(gx, rms_back(...)), in one launch
         self.rms_soma = hasattr(ops, "rms_back_soma")
         # the R16 step's residual adds, soma16(x16, gemm(...)) and soma16(gx16, rms_back(...)), each with the INT8
@@ -116,8 +116,11 @@ class Modelo:
 
     def _t_produtor(self, M, N, modo, min_wg):
         """Whether the ReLU^2 (modo 3) or ReLU^2-backward (modo 4) GEMM of M tokens x N columns, on a grid with a
-        workgroup threshold of min_wg (None: 4 per CU of the device; 0: always), writes its transpose too."""
+        workgroup threshold of min_wg (None: 4 per CU of the device; 0: always), writes its transpose too. Only at
+        BLK 32, where the GEMM's epilogue writes it (at BLK 128 a separate transpose per use would replace the batch)."""
         lib = getattr(self.ops, "lib", None)
+        if O.BLK != 32:
+            return False
         if min_wg == 0 or lib is None:
             return True
         if min_wg is None:

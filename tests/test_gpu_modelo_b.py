@@ -29,9 +29,7 @@ def test_passo_config4_vs_oraculo():
     mg.otimizador_fundido = mg.transpostas_em_lote = mg.dw_em_lote = mg.quant_na_atencao = mg.transposta_na_gemm = mg.transposta_na_relu2 = mg.rms_soma = mg.perda_fundida = False   # op by op
     mf = Modelo(V, D, H, FF, L, 0, "cuda", O.OpsHip(reg), reg)  # batched transposes + fused optimizer
     assert mf.otimizador_fundido and mf.transpostas_em_lote and mf.dw_em_lote and mf.quant_na_atencao and mf.transposta_na_gemm and mf.transposta_na_relu2 and mf.rms_soma and mf.perda_fundida
-    assert not mf._t_na_gemm(Bt * T, FF)        # 512 tokens: a grid below the threshold keeps the batched transpose
-    mf.t_na_gemm_min_wg = 0                     # every fusion on, so this step covers the GEMMs' transposed writes
-    mf.t_na_relu2_min_wg = 0
+    assert mf._t_na_gemm(Bt * T, FF) and mf._t_na_relu2(Bt * T, FF)   # the GEMMs' transposed writes, on by default
     mf.conversoes_salvas = True                 # and the attention backward reading the forward's conversions
     for p in range(2):
         x = R.tokens(R.substream(31, f"b4 {p}"), Bt * (T + 1), V).reshape(Bt, T + 1)
