@@ -3,8 +3,8 @@
 //
 // Forward in two launches:
 //   (1) k_atf_prep, one workgroup per (sequence, head, 64 tokens): the head-wide exponent maxima of q, k, v (one
-//       pass, one reduction), k as m8 << L fragments (int8 [T][64] + L [T][2]) and v aligned as f16, transposed
-//       ([64][T]), into the workspace -- converted once instead of once per query block;
+//       pass, one reduction), k as m8 << L fragments (int8 [T][64] + L [T][2]) and v aligned as f16 in the order
+//       k_atf's PV MFMAs read it, into the workspace -- converted once instead of once per query block;
 //   (2) k_atf, one workgroup of 4 waves per (sequence, head, 16 query rows): wave w takes the key tiles
 //       t = w, w + 4, ... up to the diagonal. The row maxima and row sums combine across the waves through LDS
 //       (integer max and sum: exact in any order); each wave multiplies its P tiles by V on f16 MFMA, and the
@@ -18,17 +18,25 @@
 constexpr size_t cmax_(size_t a, size_t b) { return a > b ? a : b; }
 
 namespace atw {
-// workspace parts, each 256-byte aligned: km8 int8 [BH][T][64]; kl int8 [BH][T][2]; vt f16 [BH][64][T];
-// mx int [BH][4] (emq, emk, emv)
+// workspace parts, each 256-byte aligned: km8 int8 [BH][T][64]; kl int8 [BH][T][2]; vf f16 [BH][NPV(T)][4][64][8];
+// mx int [BH][4] (emq, emk, emv).
+// km8 rows hold the 8-byte chunks of dimensions 8 k .. 8 k + 7 at chunk 2 (k % 4) + k / 4, so a lane's two MFMA
+// fragments of a key (dimensions 8 g .. and 32 + 8 g ..) are one 16-byte load and a wave's 16 keys one kilobyte.
+// vf holds v as the PV MFMAs' B fragments: slot p pairs the key tiles ta = 8 (p / 4) + p % 4 and ta + 4; its
+// block for dimension group dt is 64 lanes x 8 values, lane 16 lg + lr holding dimension 16 dt + lr of the keys
+// 16 (lg < 2 ? ta : ta + 4) + 8 (lg % 2) .. + 7, so each of a wave's fragment loads reads one contiguous
+// kilobyte. A half past the last key tile is never written: k_atf reads zeros there instead.
 struct Ws {
     int8_t *km8, *kl;
-    _Float16* vt;
+    _Float16* vf;
     int* mx;
 };
+__host__ __device__ inline int npv(int T) { return 4 * ((T / 16 + 7) / 8); }       // slots of vf per head
+__device__ __forceinline__ int pos_k8(int k) { return 2 * (k & 3) + (k >> 2); }     // km8 chunk position of chunk k
 inline size_t alinha256(size_t n) { return (n + 255) & ~(size_t)255; }
 inline size_t bytes_fwd(long long BH, int T) {
     const size_t n = (size_t)BH * T;
-    return alinha256(n * 64) + alinha256(n * 2) + alinha256(n * 64 * 2) + alinha256((size_t)BH * 16);
+    return alinha256(n * 64) + alinha256(n * 2) + alinha256((size_t)BH * npv(T) * 4096) + alinha256((size_t)BH * 16);
 }
 inline Ws parte(void* base, long long BH, int T) {
     const size_t n = (size_t)BH * T;
@@ -36,7 +44,7 @@ inline Ws parte(void* base, long long BH, int T) {
     Ws w;
     w.km8 = (int8_t*)p; p += alinha256(n * 64);
     w.kl = (int8_t*)p; p += alinha256(n * 2);
-    w.vt = (_Float16*)p; p += alinha256(n * 64 * 2);
+    w.vf = (_Float16*)p; p += alinha256((size_t)BH * npv(T) * 4096);
     w.mx = (int*)p;
     return w;
 }
@@ -143,7 +151,11 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
-        grava_i8(w.km8 + tt * 64 + 16 * c4, m8);
+        int8_t lo[8], hi[8];                                          // chunks 2 c4 and 2 c4 + 1 of the key's row
+#pragma unroll
+        for (int k = 0; k < 8; k++) { lo[k] = m8[k]; hi[k] = m8[8 + k]; }
+        grava_i8(w.km8 + tt * 64 + 8 * atw::pos_k8(2 * c4), lo);
+        grava_i8(w.km8 + tt * 64 + 8 * atw::pos_k8(2 * c4 + 1), hi);
         if ((c4 & 1) == 0) w.kl[tt * 2 + half] = (int8_t)L;
         if constexpr (SALVA) {
             const Desl dk(emk - ekt);
@@ -175,7 +187,15 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         for (int k = 0; k < 16; k++) tqk[0][16 * c4 + k][tid >> 2] = (_Float16)dq(shl(v[k], GA));
     }
     __syncthreads();
-    grava_t64(tv, w.vt + (size_t)bh * 64 * T, T, part * 64);
+    {   // v fragments of the part's 4 key tiles: thread x writes dimension 16 dt + lr of tile 4 part + x / 64, the
+        // 8-key halves (lg % 2 = 0, 1) of its fragment block
+        const int i = tid >> 6, dt = (tid >> 4) & 3, lr = tid & 15, tk = 4 * part + i;
+        const int slot = 4 * (tk >> 3) + (tk & 3), meio = (tk >> 2) & 1;   // meio 1: the pair's second tile (lg >= 2)
+        _Float16* dst = w.vf + ((((size_t)bh * atw::npv(T) + slot) * 4 + dt) * 64 + 32 * meio + lr) * 8;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; h2++)
+            *reinterpret_cast<int4*>(dst + 16 * 8 * h2) = *reinterpret_cast<const int4*>(&tv[16 * dt + lr][16 * i + 8 * h2]);
+    }
     if constexpr (SALVA) {
         grava_t64(tqk[0], s.qt + (size_t)bh * 64 * T, T, part * 64);
         grava_t64(tqk[SALVA ? 1 : 0], s.kt + (size_t)bh * 64 * T, T, part * 64);
@@ -222,11 +242,13 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 #pragma unroll
     for (int m = 0; m < NPAR; m++) {
         if (2 * m >= nv) continue;
-        int tv = wv + 4 * (2 * m + (lg >> 1));
-        if (tv >= nqt) tv = wv;
-        const int j = 16 * tv + 8 * (lg & 1);
+        const int tv = wv + 4 * (2 * m + (lg >> 1));                 // the slot of pair m is 4 m + wv
+        const _Float16* src = w.vf + (((size_t)bh * atw::npv(T) + 4 * m + wv) * 4 * 64 + lane) * 8;
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) vb[m][dt] = *reinterpret_cast<const h8_t*>(w.vt + ((size_t)bh * 64 + 16 * dt + lr) * T + j);
+        for (int dt = 0; dt < 4; dt++) {
+            vb[m][dt] = h8_t{};
+            if (tv < nqt) vb[m][dt] = *reinterpret_cast<const h8_t*>(src + dt * 64 * 8);   // past the last tile: P = 0 and v = 0
+        }
     }
     // K fragments of this wave's key tiles, loaded at entry as well
     long kb[NTW][2];
@@ -235,8 +257,9 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
         const size_t j = hb + 16 * (wv + 4 * n) + lr;
-        kb[n][0] = *reinterpret_cast<const long*>(w.km8 + j * 64 + 8 * lg);
-        kb[n][1] = *reinterpret_cast<const long*>(w.km8 + j * 64 + 32 + 8 * lg);
+        const int4 k2 = *reinterpret_cast<const int4*>(w.km8 + j * 64 + 16 * lg);   // chunks lg and 4 + lg (atw::pos_k8)
+        kb[n][0] = (long)(unsigned)k2.x | ((long)k2.y << 32);
+        kb[n][1] = (long)(unsigned)k2.z | ((long)k2.w << 32);
         lk[n][0] = w.kl[j * 2];
         lk[n][1] = w.kl[j * 2 + 1];
     }
