@@ -49,8 +49,9 @@ inline Ws parte(void* base, long long BH, int T) {
     return w;
 }
 // The backward's conversions of q, k, v, written by the forward's conversion pass, which has those values loaded
-// (kept by the caller from the forward to the backward of the same qkv): vm8 int8 [BH][T][64]; vL int8 [BH][T][2];
-// kt, qt f16 [BH][64][T]; mx int [BH][4] (emq, emk, emv: the head maxima, before - GA)
+// (kept by the caller from the forward to the backward of the same qkv): vm8 int8 [BH][T][64] (chunks as km8's);
+// vL int8 [BH][T][2]; kt, qt f16 [BH][64][T] in fragment order (grava_ft64); mx int [BH][4] (emq, emk, emv: the
+// head maxima, before - GA)
 struct Salvo {
     int8_t *vm8, *vL;
     _Float16 *kt, *qt;
@@ -112,6 +113,33 @@ __device__ __forceinline__ void grava_t64(const TileT& tile, _Float16* __restric
         *reinterpret_cast<int4*>(cab + (size_t)row * T + t0 + 8 * ch) = *reinterpret_cast<const int4*>(&tile[row][8 * ch]);
     }
 }
+// The same 64 tokens x 64 dimensions (key tiles 4 p .. 4 p + 3 of a head, p = t0 / 64) in fragment order, the
+// head's [64][T] f16 array as [T / 16 tiles][4 dt][2 h][16 lr][8]: lane (lr, lg) of an f16 MFMA B fragment reading
+// dimension 16 dt + lr of keys 16 t + 8 h .. + 7 (h = lg % 2) finds them at block (t, dt, h), row lr, so the 32
+// lanes of one tile read 512 contiguous bytes, where [64][T] rows gave them 32-byte pieces of 16 rows.
+__device__ __forceinline__ size_t pos_ft(int t, int dt, int h, int lr) { return ((((size_t)t * 4 + dt) * 2 + h) * 16 + lr) * 8; }
+__device__ __forceinline__ void grava_ft64(const TileT& tile, _Float16* __restrict__ cab, int t0) {
+    const int x = threadIdx.x, i = x >> 6, dt = (x >> 4) & 3, lr = x & 15, t = t0 / 16 + i;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+        *reinterpret_cast<int4*>(cab + pos_ft(t, dt, h, lr)) = *reinterpret_cast<const int4*>(&tile[16 * dt + lr][16 * i + 8 * h]);
+}
+// 16 m8 values of a token's dimensions 16 c4 .. 16 c4 + 15 into its 64-byte row with the 8-byte chunks k at
+// 2 (k % 4) + k / 4 (atw::pos_k8), so an MFMA lane's two fragments (dimensions 8 g .. and 32 + 8 g ..) are one
+// 16-byte load
+__device__ __forceinline__ void grava_m8_fragmentos(int8_t* __restrict__ linha, int c4, const int8_t (&m8)[16]) {
+    int8_t lo[8], hi[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) { lo[k] = m8[k]; hi[k] = m8[8 + k]; }
+    grava_i8(linha + 8 * atw::pos_k8(2 * c4), lo);
+    grava_i8(linha + 8 * atw::pos_k8(2 * c4 + 1), hi);
+}
+// the two fragments (chunks g and 4 + g) of a row written that way
+__device__ __forceinline__ void le_m8_fragmentos(const int8_t* __restrict__ linha, int g, long& f0, long& f1) {
+    const int4 x = *reinterpret_cast<const int4*>(linha + 16 * g);
+    f0 = (long)(unsigned)x.x | ((long)x.y << 32);
+    f1 = (long)(unsigned)x.z | ((long)x.w << 32);
+}
 
 // SALVA: also the backward's conversions of q, k, v into s (the arithmetic of k_atb_prep's: v as m8 << L
 // fragments, q and k aligned as f16 [64][T], the head maxima), so the backward converts only dO.
@@ -151,11 +179,7 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
         int L = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
-        int8_t lo[8], hi[8];                                          // chunks 2 c4 and 2 c4 + 1 of the key's row
-#pragma unroll
-        for (int k = 0; k < 8; k++) { lo[k] = m8[k]; hi[k] = m8[8 + k]; }
-        grava_i8(w.km8 + tt * 64 + 8 * atw::pos_k8(2 * c4), lo);
-        grava_i8(w.km8 + tt * 64 + 8 * atw::pos_k8(2 * c4 + 1), hi);
+        grava_m8_fragmentos(w.km8 + tt * 64, c4, m8);
         if ((c4 & 1) == 0) w.kl[tt * 2 + half] = (int8_t)L;
         if constexpr (SALVA) {
             const Desl dk(emk - ekt);
@@ -175,7 +199,7 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
             int L = 0;
 #pragma unroll
             for (int k = 0; k < 16; k++) { int a; m8_L(v[k], sh, GA, a, L); m8[k] = (int8_t)a; }
-            grava_i8(s.vm8 + tt * 64 + 16 * c4, m8);
+            grava_m8_fragmentos(s.vm8 + tt * 64, c4, m8);
             if ((c4 & 1) == 0) s.vL[tt * 2 + half] = (int8_t)L;
         }
     }
@@ -197,8 +221,8 @@ __global__ void __launch_bounds__(256) k_atf_prep(const int8_t* __restrict__ qm,
             *reinterpret_cast<int4*>(dst + 16 * 8 * h2) = *reinterpret_cast<const int4*>(&tv[16 * dt + lr][16 * i + 8 * h2]);
     }
     if constexpr (SALVA) {
-        grava_t64(tqk[0], s.qt + (size_t)bh * 64 * T, T, part * 64);
-        grava_t64(tqk[SALVA ? 1 : 0], s.kt + (size_t)bh * 64 * T, T, part * 64);
+        grava_ft64(tqk[0], s.qt + (size_t)bh * 64 * T, part * 64);
+        grava_ft64(tqk[SALVA ? 1 : 0], s.kt + (size_t)bh * 64 * T, part * 64);
     }
 }
 
@@ -257,9 +281,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
         const size_t j = hb + 16 * (wv + 4 * n) + lr;
-        const int4 k2 = *reinterpret_cast<const int4*>(w.km8 + j * 64 + 16 * lg);   // chunks lg and 4 + lg (atw::pos_k8)
-        kb[n][0] = (long)(unsigned)k2.x | ((long)k2.y << 32);
-        kb[n][1] = (long)(unsigned)k2.z | ((long)k2.w << 32);
+        le_m8_fragmentos(w.km8 + j * 64, lg, kb[n][0], kb[n][1]);
         lk[n][0] = w.kl[j * 2];
         lk[n][1] = w.kl[j * 2 + 1];
     }
@@ -405,8 +427,8 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
 namespace atw {
 constexpr int SLOTS = 32;            // per head and kind: T / 16 <= 32 query tiles
 struct WsB {
-    int8_t *gm8, *gL, *vm8, *vL;     // dO, v: m8 [BH][T][64], L [BH][T][2]
-    _Float16 *kt, *qt, *gt;          // k, q, dO aligned: f16 [BH][64][T]
+    int8_t *gm8, *gL, *vm8, *vL;     // dO, v: m8 [BH][T][64] (chunks as km8's), L [BH][T][2]
+    _Float16 *kt, *qt, *gt;          // k, q, dO aligned: f16 [BH][64][T] in fragment order (grava_ft64)
     int* sl;                         // s_i [BH][T]
     int* mx;                         // [BH][4]: ego, eq, ek, ev (head maxima - GA)
     int* p1a;                        // [BH][SLOTS]: max |gP| per query tile, or max |dO| per 64 tokens (LIMITE)
@@ -681,7 +703,7 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
             amax = max(amax, abs(al));
             tg[16 * c4 + k][tid >> 2] = (_Float16)al;
         }
-        grava_i8(w.gm8 + tt * 64 + 16 * c4, m8);
+        grava_m8_fragmentos(w.gm8 + tt * 64, c4, m8);
         if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
     }
     {   // v: m8 << L fragments (and ||v||_1 for LIMITE)
@@ -696,7 +718,7 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
             if (LIMITE) v1 += abs(ds(shl(v[k], GA)));
         }
-        grava_i8(w.vm8 + tt * 64 + 16 * c4, m8);
+        grava_m8_fragmentos(w.vm8 + tt * 64, c4, m8);
         if ((c4 & 1) == 0) w.vL[tt * 2 + half] = (int8_t)L;
     }
 #pragma unroll
@@ -709,9 +731,9 @@ __global__ void __launch_bounds__(256) k_atb_prep(const int8_t* __restrict__ gom
         for (int k = 0; k < 16; k++) dst[16 * c4 + k][tid >> 2] = (_Float16)ds(shl(v[k], GA));
     }
     __syncthreads();
-    grava_t64(tg, w.gt + (size_t)bh * 64 * T, T, part * 64);
-    grava_t64(tq, w.qt + (size_t)bh * 64 * T, T, part * 64);
-    grava_t64(tk, w.kt + (size_t)bh * 64 * T, T, part * 64);
+    grava_ft64(tg, w.gt + (size_t)bh * 64 * T, part * 64);
+    grava_ft64(tq, w.qt + (size_t)bh * 64 * T, part * 64);
+    grava_ft64(tk, w.kt + (size_t)bh * 64 * T, part * 64);
     if (LIMITE) {
         v1 = quad_soma(v1);
         const int a = wg_max4(amax, red1), c = wg_max4(v1, red1);
@@ -756,11 +778,11 @@ __global__ void __launch_bounds__(256) k_atb_prep_s(const int8_t* __restrict__ g
             int a; m8_L(v[k], s, GA, a, L); m8[k] = (int8_t)a;
             tg[16 * c4 + k][tid >> 2] = (_Float16)ds(shl(v[k], GA));
         }
-        grava_i8(w.gm8 + tt * 64 + 16 * c4, m8);
+        grava_m8_fragmentos(w.gm8 + tt * 64, c4, m8);
         if ((c4 & 1) == 0) w.gL[tt * 2 + half] = (int8_t)L;
     }
     __syncthreads();
-    grava_t64(tg, w.gt + (size_t)bh * 64 * T, T, part * 64);
+    grava_ft64(tg, w.gt + (size_t)bh * 64 * T, part * 64);
 }
 
 // gP tile of query rows i0 .. i0 + 3 (this lane) x key j = 16 t + lr from the workspace fragments
@@ -771,16 +793,16 @@ struct FragQ {                                      // dO fragments of a query t
 __device__ __forceinline__ FragQ frag_q(const atw::WsB& w, size_t hb, int qt, int lr, int lg) {
     FragQ f;
     const size_t ia = hb + 16 * qt + lr, i0 = hb + 16 * qt + 4 * lg;
-    f.ga[0] = *reinterpret_cast<const long*>(w.gm8 + ia * 64 + 8 * lg);
-    f.ga[1] = *reinterpret_cast<const long*>(w.gm8 + ia * 64 + 32 + 8 * lg);
+    le_m8_fragmentos(w.gm8 + ia * 64, lg, f.ga[0], f.ga[1]);
 #pragma unroll
     for (int v = 0; v < 4; v++) { f.lx[v][0] = w.gL[(i0 + v) * 2]; f.lx[v][1] = w.gL[(i0 + v) * 2 + 1]; }
     return f;
 }
 __device__ __forceinline__ void gp_tile(const atw::WsB& w, size_t hb, const FragQ& f, int t, int lr, int lg, int (&o)[4]) {
     const size_t j = hb + 16 * t + lr;
-    tile_xyt(f.ga[0], f.ga[1], *reinterpret_cast<const long*>(w.vm8 + j * 64 + 8 * lg), *reinterpret_cast<const long*>(w.vm8 + j * 64 + 32 + 8 * lg),
-             f.lx, w.vL[j * 2], w.vL[j * 2 + 1], o);
+    long v0, v1;
+    le_m8_fragmentos(w.vm8 + j * 64, lg, v0, v1);
+    tile_xyt(f.ga[0], f.ga[1], v0, v1, f.lx, w.vL[j * 2], w.vL[j * 2 + 1], o);
 }
 // query tile of this workgroup, in decreasing work across all heads (tile qt pairs with qt + 1 key tiles)
 #define ATB_TILE_Q ATB_TILE_Q_(blockIdx.x, gridDim.x)
@@ -952,10 +974,9 @@ __device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __r
         pedacos_ds(*reinterpret_cast<const s8_t*>(&dw[wv][lr][32 * m + 8 * lg]), pa, pb, pc);
         int tk = wv + 4 * (2 * m + (lg >> 1));
         if (tk >= nqt) tk = wv;                                      // pad tile: dS = 0 there
-        const int j = 16 * tk + 8 * (lg & 1);
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            const h8_t kv = *reinterpret_cast<const h8_t*>(w.kt + ((size_t)bh * 64 + 16 * dt + lr) * T + j);
+            const h8_t kv = *reinterpret_cast<const h8_t*>(w.kt + (size_t)bh * 64 * T + pos_ft(tk, dt, lg & 1, lr));
             acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, kv, acc[dt][0], 0, 0, 0);
             acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, kv, acc[dt][1], 0, 0, 0);
             acc[dt][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc, kv, acc[dt][2], 0, 0, 0);
@@ -1052,10 +1073,9 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
         for (int k = 0; k < 8; k++) { ph[k] = (_Float16)(pp[k] >> 4); pl[k] = (_Float16)(pp[k] & 15); }
         int tq = kt + wv + 4 * (2 * m + (lg >> 1));
         if (tq >= nqt) tq = kt + wv;                                 // pad tile: dS = P = 0 there
-        const int i = 16 * tq + 8 * (lg & 1);
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            const size_t r = ((size_t)bh * 64 + 16 * dt + lr) * T + i;
+            const size_t r = (size_t)bh * 64 * T + pos_ft(tq, dt, lg & 1, lr);
             const h8_t qv = *reinterpret_cast<const h8_t*>(w.qt + r);
             const h8_t gv = *reinterpret_cast<const h8_t*>(w.gt + r);
             ak[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, qv, ak[dt][0], 0, 0, 0);
