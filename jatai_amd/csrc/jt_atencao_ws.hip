@@ -1037,26 +1037,43 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
     // dS before its shrink, as k_atb2 stored it (0 past the diagonal): row lr (query 16 t + lr) of tile (t, kt),
     // columns 4 lg .. 4 lg + 3 (this lane's keys), one 16-byte load; P of the same pairs
     int4 dr[NTW];
-    int pv[NTW][4];
 #pragma unroll
     for (int n = 0; n < NTW; n++) {                                  // loads of every n issued together: tiles past
-        const int t = min(kt + wv + 4 * n, nqt - 1), i = 16 * t + lr;   // this wave's last re-read tile nqt - 1, unused
+        const int t = min(kt + wv + 4 * n, nqt - 1);                 // this wave's last re-read tile nqt - 1, unused
         dr[n] = *reinterpret_cast<const int4*>(w.ds + atw::ds_pos(bh, nqt, t, kt) + 16 * lr + 4 * lg);
+    }
+    // P of the tile's 16 keys against query tiles kt .. nqt - 1: 16 rows of the [j][i] storage, one 16-byte piece
+    // (query tile kt + c, key 16 kt + r) per thread and column group, staged for the wave that owns query tile kt + c
+    constexpr int NC = NTW / 4;
+    const int r = tid >> 4;
+    int4 pq[NC];
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int p = Pb[(size_t)(jr + v) * T + i];
-            pv[n][v] = i >= jr + v ? p : 0;
-        }
+    for (int c = 0; c < NC; c++) {
+        const int t = kt + (tid & 15) + 16 * c;
+        if (t < nqt) pq[c] = *reinterpret_cast<const int4*>(Pb + (size_t)(16 * kt + r) * T + 16 * t);
     }
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
         const int d4[4] = {dr[n].x, dr[n].y, dr[n].z, dr[n].w};
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            dw[wv][4 * lg + v][16 * n + lr] = (short)dsh2(d4[v]);
-            pw[wv][4 * lg + v][16 * n + lr] = (uint8_t)pv[n][v];
+        for (int v = 0; v < 4; v++) dw[wv][4 * lg + v][16 * n + lr] = (short)dsh2(d4[v]);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int cc = (tid & 15) + 16 * c, t = kt + cc;
+        if (t >= nqt) continue;
+        int4 q = pq[c];
+        if (t == kt) {                                               // the diagonal tile: P = 0 for queries before key r
+            unsigned x[4] = {(unsigned)q.x, (unsigned)q.y, (unsigned)q.z, (unsigned)q.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int z = min(max(r - 4 * k, 0), 4);             // bytes of word k below the diagonal
+                x[k] &= z == 4 ? 0u : (~0u << (8 * z));
+            }
+            q = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
         }
+        *reinterpret_cast<int4*>(&pw[cc & 3][r][16 * (cc >> 2)]) = q;
     }
     if (nv & 1)
 #pragma unroll
