@@ -318,6 +318,7 @@ class Modelo:
                 for Z, Zt in zip(falta, ops.transpoe_lote(falta)):
                     prontas[id(Z[0])] = Zt
         adiados = [(n, T_(X), T_(Y)) for n, X, Y in adiados]
+        self._pt_validas = False                   # the weights change below; only jt_otimizador_t rewrites their transposes
         if adiados and self._otim_no_gemm():
             with reg.trecho("gradientes dos pesos + otimizador"):
                 ops.gemm_otim_lote([(A, B, self.mom[n], self.p[n], self.res[n]) for n, A, B in adiados], k_lr, self.error_feedback)
