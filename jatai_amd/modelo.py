@@ -109,7 +109,7 @@ class Modelo:
         # transposes as before). A caller that changes weights outside the optimizer calls invalida_transpostas().
         self.transposta_no_otimizador = hasattr(ops, "tabela_otimizador") and O.BLK == 32 and all(
             t[0].shape[0] % 32 == 0 and t[0].shape[1] % 128 == 0 for t in self.p.values())
-        self._pt, self._pt_validas, self._tabela_t = None, False, None
+        self._pt, self._pt_validas, self._tabela_t, self._pt_lidas = None, False, None, False
         # the grouped weight-gradient launch writes the exponents of the fused optimizer's gradient buffers as row
         # and column vectors (OpsHip)
         self.grad_compacto = hasattr(ops, "gemm_cru_lote") and hasattr(ops, "otimizador")
@@ -162,8 +162,17 @@ class Modelo:
         return self._gbuf
 
     def invalida_transpostas(self):
-        """The weights changed outside the optimizer: the next step transposes them again."""
+        """The weights changed outside the optimizer: the next eager step transposes them again, and a captured step
+        (PassoGravado) rewrites the transposes it reads from the current weights before its next replay."""
         self._pt_validas = False
+
+    def renova_transpostas(self):
+        """transpoe(W) of the current weights into the buffers the fused optimizer writes (one batched launch)."""
+        nomes = list(self._pt)
+        for n, (Ym, YE) in zip(nomes, self.ops.transpoe_lote([self.p[n] for n in nomes])):
+            self._pt[n][0].copy_(Ym)
+            self._pt[n][1].copy_(YE)
+        self._pt_validas = True
 
     def _st(self, nome, t, zeros_normais=False):
         if self.estatisticas:
@@ -180,6 +189,7 @@ class Modelo:
             return x8 if x8 is not None else ops.para8(x16)
         tok, alvo = tok.reshape(-1).to(torch.int32).contiguous(), alvo.reshape(-1).to(torch.int32).contiguous()
         prontas = {}                # id(mantissas) -> transpose already written by its producer (or a batched launch)
+        self._pt_lidas = False      # whether this step's backward reads the transposes the last fused update wrote
         with reg.trecho("forward"):
             with reg.trecho("embedding"):
                 x = ops.embed(p["emb"], tok)
@@ -239,6 +249,7 @@ class Modelo:
                     for n, Y in self._pt.items():          # written by the last fused update
                         prontas[id(p[n][0])] = Y
                     pesos = []
+                    self._pt_lidas = True
                 ativ = [t for c in caches for t in (c[8], c[5], c[4], c[0]) if id(t[0]) not in prontas] + [nf]   # a, n2, om, n1
                 for X, Y in zip(pesos + ativ, ops.transpoe_lote(pesos) + ops.transpoe_lote(ativ)):
                     prontas[id(X[0])] = Y
@@ -383,11 +394,21 @@ class PassoGravado:
             lib.jt_stream(None)
             modelo.estatisticas, self.reg.vigiar, modelo.perda_inteira = est, vig, pi
         self.lancamentos = list(self.reg.lancamentos)
+        # the captured backward reads the weights' transposes from the buffers the fused update writes (at capture
+        # they held the transposes of the current weights); weights changed since outside the graph's own update
+        # (invalida_transpostas) need them rewritten before the next replay
+        self.le_transpostas = modelo._pt_lidas
         self.reg.info(f"passo gravado num hipGraph: {len(self.lancamentos)} lancamentos", lancamentos=len(self.lancamentos))
+
+    def _transpostas_em_dia(self):
+        if self.le_transpostas and not self.m._pt_validas:
+            self.m.renova_transpostas()
+            self.reg.confere_device()    # a sentinel of those launches is read while the step's list still names them
 
     def __call__(self, tok, alvo):
         if self.corpus is not None:
             raise RuntimeError("this graph reads its tokens from its corpus: call de_corpus(gerador)")
+        self._transpostas_em_dia()
         self.tok.copy_(tok)
         self.alvo.copy_(alvo)
         self.reg.lancamentos = self.lancamentos
@@ -397,6 +418,7 @@ class PassoGravado:
     def de_corpus(self, gerador):
         """One step on the batch that jatai_amd.dados.lote(dados, gerador, Bt, T) would draw: the Bt starts go to
         the device (64 bytes at Bt = 8) and the graph's first node writes the windows into its token buffers."""
+        self._transpostas_em_dia()
         self.ini.copy_(self.corpus.inicios(gerador, self.Bt, self.T))
         self.reg.lancamentos = self.lancamentos
         self.grafo.replay()

@@ -2,7 +2,8 @@
 with 2 layers and 2 sequences: every op output of the HIP path equals the CPU oracle's (jatai_amd.modelo.Modelo
 on both backends, same init and tokens); the step with batched transposes and the fused optimizer leaves the
 same weights, momenta and residuals. A third step replayed
-from a captured hipGraph (fused model) equals the eager op-by-op step."""
+from a captured hipGraph (fused model) equals the eager op-by-op step, and so does a fourth after a weight changed
+outside the optimizer."""
 import pytest
 import torch
 
@@ -64,4 +65,21 @@ def test_passo_config4_vs_oraculo():
     b = float(mg.passo(tok, alvo, k_lr=4))
     assert abs(a - b) <= 1e-14 * abs(b)
     assert est(mf) == est(mg), "graph-replayed fused step differs from the eager op-by-op step"
+    # a fourth: a weight changed outside the optimizer (layer 1's out-projection copied into layer 0's) and
+    # invalida_transpostas(); the graph reads the transposes its update wrote, so the replay must rewrite them first
+    assert pgraf.le_transpostas
+    for m in (mf, mg):
+        m.p["Wo0"][0].copy_(m.p["Wo1"][0])
+        m.p["Wo0"][1].copy_(m.p["Wo1"][1])
+    mf.invalida_transpostas()
+    x = R.tokens(R.substream(31, "b4 3"), Bt * (T + 1), V).reshape(Bt, T + 1)
+    tok, alvo = torch.from_numpy(x[:, :-1].copy()).long().cuda(), torch.from_numpy(x[:, 1:].copy()).long().cuda()
+    reg.novo_passo(3)
+    a = float(pgraf(tok, alvo))
+    torch.cuda.synchronize()
+    reg.fim_passo()
+    assert mf._pt_validas
+    b = float(mg.passo(tok, alvo, k_lr=4))
+    assert abs(a - b) <= 1e-14 * abs(b)
+    assert est(mf) == est(mg), "graph step after an outside weight change differs from the eager step"
     O.BLK = 128
