@@ -55,7 +55,8 @@ def test_janelas_iguais_ao_lote(treino, caso):
 
 def test_janelas_nos_limites(treino):
     """Starts 0 and n - T - 1 (the last whole window; the reference's draw stops one short of it) are gathered;
-    a start of n - T raises E_ARG naming janelas and the sequence's first token, and zeroes that row only."""
+    a start of n - T, or a negative one, raises E_ARG naming janelas and the sequence's first token, and zeroes
+    that row only."""
     from jatai_amd import dados as DD
     from jatai_amd.registro import ErroJatai
     ops, reg = _ops()
@@ -65,11 +66,19 @@ def test_janelas_nos_limites(treino):
     assert np.array_equal(host(tok[1]), treino[n - T - 1:n - 1].numpy()) and np.array_equal(host(alvo[1]), treino[n - T:].numpy())
     assert np.array_equal(host(tok[0]), treino[:T].numpy()) and np.array_equal(host(alvo[2]), treino[12346:12346 + T].numpy())
     reg.novo_passo(0)
+    t2, a2 = tok[:2].contiguous(), alvo[:2].contiguous()
     with pytest.raises(ErroJatai) as e:
-        c.janelas(torch.tensor([7, n - T]), T, tok[:2].contiguous(), alvo[:2].contiguous())
+        c.janelas(torch.tensor([7, n - T]), T, t2, a2)
     msg = str(e.value)
     assert "janelas" in msg and f"valor    : {n - T}" in msg, msg
     assert reg.ultimo_evento.idx == 1 * T
+    assert np.array_equal(host(t2[0]), treino[7:7 + T].numpy()) and np.array_equal(host(a2[0]), treino[8:8 + T].numpy())
+    assert not host(t2[1]).any() and not host(a2[1]).any()
+    reg.novo_passo(1)                           # a negative start is refused the same way
+    with pytest.raises(ErroJatai) as e:
+        c.janelas(torch.tensor([5, 9, -1]), T)
+    assert "janelas" in str(e.value) and "valor    : -1" in str(e.value), str(e.value)
+    assert reg.ultimo_evento.idx == 2 * T
 
 
 def test_grafo_com_corpus_igual_ao_grafo_com_lotes(treino):
