@@ -402,6 +402,7 @@ class PassoGravado:
 
     def _transpostas_em_dia(self):
         if self.le_transpostas and not self.m._pt_validas:
+            self.reg.lancamentos = list(self.reg.lancamentos)    # never append to the graph's own list
             self.m.renova_transpostas()
             self.reg.confere_device()    # a sentinel of those launches is read while the step's list still names them
 
