@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     constexpr int HD = 64, LP = 16 * (NTW + 1);                     // LDS row length of a wave's P (one pad tile)
     __shared__ int sred[4][16];
     __shared__ __align__(16) _Float16 pw[4][16][LP];
-    __shared__ float so[4][16][64];
+    __shared__ float so[4][16][68];                                  // rows of 68: rows 4 apart fall in other banks
     __shared__ __align__(16) unsigned short texp[EXP_N];
     exp_tab_lds(texp);                                               // published by the first barrier below
     // workgroups in decreasing work across all heads (the query tile qt costs qt + 1 key tiles): the ones resident
