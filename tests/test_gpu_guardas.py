@@ -51,3 +51,62 @@ def test_atencao_recusa_ga_fora(GA, H):
     torch.cuda.synchronize()
     for nome, t in (("oacc", oacc), ("oe", oe), ("P", Pout), ("gacc", gacc), ("ge", ge), ("ws", wf), ("ws back", wb)):
         assert bool((t == 7).all()), nome
+
+
+def test_otimizador_t_e_janelas_recusam():
+    """jt_otimizador_t refuses BLK 128, a block count that is not a whole number of 32 x 128 tiles and a table of 0
+    or more than 256 entries (a count of 0 is a no-op); jt_janelas refuses a corpus shorter than one window and
+    misaligned start or token buffers. The table is a real one and every buffer is larger than the shape asks, so
+    a guard that failed would launch on valid memory; the outputs must keep their values."""
+    from jatai_amd import ops as O
+    from jatai_amd.registro import Registro
+    lib = O.carrega_lib()
+    for f in ("jt_otimizador_t", "jt_janelas", "jt_bloco"):
+        getattr(lib, f).restype = ctypes.c_int
+    blk0 = O.BLK
+    try:
+        O.BLK = 32
+        ops = O.OpsHip(Registro("/tmp/jt_guardas", "g", eco=False))
+        assert lib.jt_bloco(32) == 0
+        M, N = 32, 128
+        g = torch.Generator().manual_seed(3)
+        W = (torch.randint(-100, 100, (M, N), generator=g, dtype=torch.int8).cuda(), torch.zeros(M, N // 32, dtype=torch.int8, device="cuda"))
+        Mom = (torch.zeros(M, N, dtype=torch.int8, device="cuda"), torch.full((M, N // 32), O.E_ZERO, dtype=torch.int8, device="cuda"))
+        R = (torch.zeros(M, N, dtype=torch.int8, device="cuda"), torch.full((M, N // 32), O.E_ZERO, dtype=torch.int8, device="cuda"))
+        G = (torch.randint(-1000, 1000, (M, N), generator=g, dtype=torch.int32).cuda(), torch.full((M, N), -20, dtype=torch.int16, device="cuda"))
+        Wt = (torch.full((N, M), 7, dtype=torch.int8, device="cuda"), torch.full((N, M // 32), 7, dtype=torch.int8, device="cuda"))
+        tab, ntab, nb, vivos, tr = ops.tabela_otimizador([(G, Mom, W, R, Wt)])
+        assert ntab == 1 and nb == 128 and tr
+        w0 = W[0].clone()
+        p = ctypes.c_void_p(tab.data_ptr())
+        ll = ctypes.c_longlong
+        assert lib.jt_otimizador_t(p, 1, ll(0), 4, 1, 0) == 0                      # nothing to do
+        assert lib.jt_otimizador_t(p, 1, ll(129), 4, 1, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_otimizador_t(p, 0, ll(128), 4, 1, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_otimizador_t(p, 257, ll(128), 4, 1, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_bloco(128) == 0
+        assert lib.jt_otimizador_t(p, 1, ll(128), 4, 1, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_bloco(32) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(W[0], w0) and bool((Wt[0] == 7).all()) and bool((Wt[1] == 7).all())
+        # windows: a 4096-byte corpus buffer, told n = T (one byte short of a window)
+        T, Bt = 64, 2
+        corpus = torch.randint(0, 256, (4096,), generator=g, dtype=torch.uint8).cuda()
+        ini = torch.zeros(4, dtype=torch.int64, device="cuda")
+        tok = torch.full((4 * Bt * T,), 7, dtype=torch.int32, device="cuda")
+        alvo = torch.full_like(tok, 7)
+        c, i, t, a = (ctypes.c_void_p(x.data_ptr()) for x in (corpus, ini, tok, alvo))
+        desl = lambda x, b: ctypes.c_void_p(x.data_ptr() + b)
+        assert lib.jt_janelas(c, ll(T), i, t, a, Bt, T, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_janelas(c, ll(4096), desl(ini, 4), t, a, Bt, T, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_janelas(c, ll(4096), i, desl(tok, 2), a, Bt, T, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_janelas(c, ll(4096), i, t, desl(alvo, 2), Bt, T, 0) == HIP_ERROR_INVALID_VALUE
+        assert lib.jt_janelas(c, ll(4096), i, t, a, 0, T, 0) == HIP_ERROR_INVALID_VALUE
+        torch.cuda.synchronize()
+        assert bool((tok == 7).all()) and bool((alvo == 7).all())
+        assert lib.jt_janelas(c, ll(4096), i, t, a, Bt, T, 0) == 0                  # the same call, well formed
+        torch.cuda.synchronize()
+        assert torch.equal(tok[:T].cpu(), corpus[:T].cpu().int()) and torch.equal(alvo[:T].cpu(), corpus[1:T + 1].cpu().int())
+    finally:
+        O.BLK = blk0
+        lib.jt_bloco(blk0)
