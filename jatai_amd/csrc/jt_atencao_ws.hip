@@ -248,7 +248,9 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     __shared__ __align__(16) _Float16 pw[4][16][LP];
     __shared__ float so[4][16][68];                                  // rows of 68: rows 4 apart fall in other banks
     __shared__ __align__(16) unsigned short texp[EXP_N];
-    exp_tab_lds(texp);                                               // published by the first barrier below
+    static_assert(256 * 2 >= EXP_N / 8 && 256 <= EXP_N / 8, "exp table: one or two chunks per thread");
+    int4 tch[2];
+    exp_tab_le(tch);                                                 // into LDS once every other load is issued
     // workgroups in decreasing work across all heads (the query tile qt costs qt + 1 key tiles): the ones resident
     // together on a CU then mix long and short rows
     const int nqt = T / 16, BH = gridDim.x / nqt, bh = blockIdx.x % BH, qt = nqt - 1 - (int)(blockIdx.x / BH);
@@ -264,34 +266,44 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     constexpr int NPAR = (NTW + 1) / 2;
     h8_t vb[NPAR][4];
 #pragma unroll
-    for (int m = 0; m < NPAR; m++) {
-        if (2 * m >= nv) continue;
-        const int tv = wv + 4 * (2 * m + (lg >> 1));                 // the slot of pair m is 4 m + wv
-        const _Float16* src = w.vf + (((size_t)bh * atw::npv(T) + 4 * m + wv) * 4 * 64 + lane) * 8;
+    for (int m = 0; m < NPAR; m++) {                                 // every load unconditional (no branch between
+        const int mm = 2 * m < nv ? m : 0;                            // them): a pair the wave does not use re-reads
+        const int tv = wv + 4 * (2 * mm + (lg >> 1));                // pair 0's slot; the slot of pair m is 4 m + wv
+        const _Float16* src = w.vf + (((size_t)bh * atw::npv(T) + 4 * mm + wv) * 4 * 64 + lane) * 8;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            vb[m][dt] = h8_t{};
-            if (tv < nqt) vb[m][dt] = *reinterpret_cast<const h8_t*>(src + dt * 64 * 8);   // past the last tile: P = 0 and v = 0
+            const h8_t x = *reinterpret_cast<const h8_t*>(src + dt * 64 * 8);
+            vb[m][dt] = tv < nqt ? x : h8_t{};                        // past the last tile: P = 0 and v = 0
         }
     }
     // K fragments of this wave's key tiles, loaded at entry as well
     long kb[NTW][2];
-    int lk[NTW][2];
+    unsigned lkr[NTW];                                                // both L bytes of a key, split where used
 #pragma unroll
-    for (int n = 0; n < NTW; n++) {
-        if (n >= nv) continue;
-        const size_t j = hb + 16 * (wv + 4 * n) + lr;
+    for (int n = 0; n < NTW; n++) {                                   // unconditional: a tile the wave does not own
+        const size_t j = hb + 16 * (n < nv ? wv + 4 * n : wv) + lr;   // re-reads its first (wv < nqt)
         le_m8_fragmentos(w.km8 + j * 64, lg, kb[n][0], kb[n][1]);
-        lk[n][0] = w.kl[j * 2];
-        lk[n][1] = w.kl[j * 2 + 1];
+        lkr[n] = *reinterpret_cast<const unsigned short*>(w.kl + j * 2);
     }
     // q fragments of the tile's 16 rows, converted here: A row lr = query ia, dimensions 32 c + 8 lg .. + 7
     __shared__ int qL[16][2];
     long qa[2];
+    int qv[2][8], qe[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {                                     // both halves' loads before either conversion
+        const int col = h * HD + 32 * c + 8 * lg;                     // (m8L_frag's arithmetic)
+        le_i8(qm + (size_t)(b0 + ia) * (3 * D) + col, qv[c]);
+        qe[c] = qE[(size_t)(b0 + ia) * (3 * D / blk) + col / blk];
+    }
+    exp_tab_grava(texp, tch);                                        // waits for the table's load only
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-        int L;
-        qa[c] = m8L_frag(qm, qE, 3 * D, h * HD, blk, b0 + ia, eq + GA, GA, c, lg, L);
+        const int s = eq + GA - qe[c];
+        int L = 0;
+        long pk = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) { int a; m8_L(qv[c][k], s, GA, a, L); pk |= (long)(uint8_t)a << (8 * k); }
+        qa[c] = pk;
         if (lg == 0) qL[lr][c] = L;
     }
     __syncthreads();
@@ -305,7 +317,7 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;                                       // guarded, not break: uu stays in registers
         const int j = 16 * (wv + 4 * n) + lr;
-        const int lk0 = lk[n][0], lk1 = lk[n][1];
+        const int lk0 = (int)(int8_t)(lkr[n] & 0xff), lk1 = (int)(int8_t)(lkr[n] >> 8);
         const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[0], kb[n][0], v4i{0, 0, 0, 0}, 0, 0, 0);
         const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[1], kb[n][1], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll

@@ -119,6 +119,25 @@ __device__ __forceinline__ void exp_tab_lds(unsigned short* t) {
     for (int c = threadIdx.x; c < EXP_N / 8; c += blockDim.x)
         reinterpret_cast<int4*>(t)[c] = reinterpret_cast<const int4*>(TAB_EXP.v)[c];
 }
+// The same copy in two halves: exp_tab_le loads a thread's chunks into registers, exp_tab_grava stores them, so
+// the kernel's other loads can be issued in between (a store right after its load waits for it first). NCH chunks
+// per thread: blockDim.x * NCH >= EXP_N / 8.
+template <int NCH>
+__device__ __forceinline__ void exp_tab_le(int4 (&r)[NCH]) {
+#pragma unroll
+    for (int k = 0; k < NCH; k++) {                                  // unconditional: past the table a thread re-reads
+        const int c0 = threadIdx.x + k * blockDim.x;                  // its first chunk (blockDim.x <= EXP_N / 8)
+        r[k] = reinterpret_cast<const int4*>(TAB_EXP.v)[c0 < EXP_N / 8 ? c0 : threadIdx.x];
+    }
+}
+template <int NCH>
+__device__ __forceinline__ void exp_tab_grava(unsigned short* t, const int4 (&r)[NCH]) {
+#pragma unroll
+    for (int k = 0; k < NCH; k++) {                                  // unconditional, as the loads (a thread writes its
+        const int c0 = threadIdx.x + k * blockDim.x;                  // first chunk again: no other thread's)
+        reinterpret_cast<int4*>(t)[c0 < EXP_N / 8 ? c0 : threadIdx.x] = r[k];
+    }
+}
 // exp_dif(mx, u) >> 3 from the table for u <= mx: the difference, taken in unsigned arithmetic (no signed
 // overflow), is exact (below 2^32) however far apart mx and u are, and every difference from EXP_D0 on reads the final 0 (an index never leaves the table)
 __device__ __forceinline__ int exp_tab(const unsigned short* t, int mx, int u) { return t[min((unsigned)mx - (unsigned)u, (unsigned)EXP_D0)]; }
