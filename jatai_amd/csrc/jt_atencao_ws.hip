@@ -481,8 +481,8 @@ inline WsB parte_b(void* base, long long BH, int T) {
 // not a chain of n dependent ones), then a wave-wide maximum; call from uniform control flow
 __device__ __forceinline__ int max_slots(const int* s, int bh, int n) {
     const int lane = threadIdx.x & 63;
-    const int v = lane < n ? s[(size_t)bh * SLOTS + lane] : 0;
-    return g_max<64>(v);
+    const int x = s[(size_t)bh * SLOTS + min(lane, SLOTS - 1)];      // every lane loads (no branch): lanes past n
+    return g_max<64>(lane < n ? x : 0);                               // count 0
 }
 template <int LIMITE>
 __device__ __forceinline__ int sh_gp_ws(const WsB& w, int bh, int T) {
@@ -850,9 +850,9 @@ __global__ void __launch_bounds__(256) k_atb2(atw::WsB w, const uint8_t* __restr
     __shared__ int red[4];
     __shared__ int sred[4][16];
     ATB_TILE_Q
-    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T);
-    const Desl dsh(sh);                                              // gP's shrink, one shift per head
     const FragQ f = frag_q(w, hb, qt, lr, lg);
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T);                  // after frag_q's loads are issued
+    const Desl dsh(sh);                                              // gP's shrink, one shift per head
     const uint8_t* Pb = P + (size_t)bh * T * T;
     int x[NTW][4];
     unsigned pr[NTW];
@@ -954,10 +954,6 @@ __device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __r
     auto& parc = *reinterpret_cast<int (*)[4][16][64]>(lds);
     ATB_TILE_Q_(blk, nblk)
     (void)P;
-    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
-    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
-    const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
-    const int eds = ego + ev + sh - 9 + sh2;
     // dS before its shrink, as k_atb2 stored it (0 past the diagonal): rows 4 lg + v of tile (qt, t), column lr
     int dr[NTW][4];
 #pragma unroll
@@ -967,6 +963,11 @@ __device__ __forceinline__ void atbq_corpo(const atw::WsB& w, const uint8_t* __r
 #pragma unroll
         for (int v = 0; v < 4; v++) dr[n][v] = dt[16 * v];
     }
+    // the head maxima after the loads above are issued (their slot reads need a reduction before any use)
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
+    const int ego = w.mx[bh * 4], ek = w.mx[bh * 4 + 2], ev = w.mx[bh * 4 + 3];
+    const int eds = ego + ev + sh - 9 + sh2;
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
@@ -1040,10 +1041,6 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15, lg = lane >> 4;
     const size_t hb = (size_t)bh * T;
     const int nv = (nqt - kt - wv + 3) / 4;                          // this wave's query tiles kt + wv + 4 n, n < nv
-    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
-    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
-    const int ego = w.mx[bh * 4], eq = w.mx[bh * 4 + 1], ev = w.mx[bh * 4 + 3];
-    const int eds = ego + ev + sh - 9 + sh2;
     const int jr = 16 * kt + 4 * lg;                                 // this lane's 4 keys jr .. jr + 3
     const uint8_t* Pb = P + (size_t)bh * T * T;
     // dS before its shrink, as k_atb2 stored it (0 past the diagonal): row lr (query 16 t + lr) of tile (t, kt),
@@ -1060,10 +1057,15 @@ __device__ __forceinline__ void atbkv_corpo(const atw::WsB& w, const uint8_t* __
     const int r = tid >> 4;
     int4 pq[NC];
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-        const int t = kt + (tid & 15) + 16 * c;
-        if (t < nqt) pq[c] = *reinterpret_cast<const int4*>(Pb + (size_t)(16 * kt + r) * T + 16 * t);
+    for (int c = 0; c < NC; c++) {                                  // unconditional: past the last query tile it
+        const int t = min(kt + (tid & 15) + 16 * c, nqt - 1);         // re-reads that tile, unused
+        pq[c] = *reinterpret_cast<const int4*>(Pb + (size_t)(16 * kt + r) * T + 16 * t);
     }
+    // the head maxima after the loads above are issued
+    const int sh = atw::sh_gp_ws<LIMITE>(w, bh, T), sh2 = atw::sh_ds_ws<LIMITE>(w, bh, T, dsb);
+    const Desl dsh2(sh2);                                            // dS's shrink, one shift per head
+    const int ego = w.mx[bh * 4], eq = w.mx[bh * 4 + 1], ev = w.mx[bh * 4 + 3];
+    const int eds = ego + ev + sh - 9 + sh2;
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
         if (n >= nv) continue;
