@@ -19,7 +19,7 @@ extern "C" {
 #endif
 
 /* ---- device error record and stream (jatai_cuda.cu:1062-1073, 1088) */
-int jt_erro_le(long long* out);        /* jatai_cuda.cu:1062: out[6] = {n, code, kid, idx, value, aux}; returns n, or -hipError; synchronizes the device first */
+int jt_erro_le(long long* out);        /* jatai_cuda.cu:1062: out[6] = {n, code, kid, idx, value, aux}; returns n, or -hipError; synchronizes the device first (the first call on a device also allocates a 4-byte host-pinned event flag, kept to the process's end) */
 int jt_erro_limpa(void);               /* jatai_cuda.cu:1069: clears the record, ordered on the library's stream (no host wait) */
 int jt_sincroniza(void);               /* hipDeviceSynchronize */
 void jt_stream(void* stream);          /* every later launch goes to this hipStream_t (graph capture) */

@@ -20,6 +20,9 @@
 #include "jt_atencao_ws.hip"
 
 __device__ Erro g_erro;
+// A host-pinned flag beside the record (set up by the first jt_erro_le): 1 once an event is recorded, 0 after each
+// clear. A read of the record that finds it 0 needs no device-to-host copy: the record is then all zeros.
+__device__ int* g_erro_flag = nullptr;
 __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long long valor, long long aux) {
     if (atomicAdd(&g_erro.n, 1) == 0) {
         g_erro.codigo = codigo;
@@ -28,11 +31,14 @@ __device__ __noinline__ void reporta(int codigo, int kid, long long idx, long lo
         g_erro.valor = valor;
         g_erro.aux = aux;
         __threadfence();
+        if (int* f = g_erro_flag) { *f = 1; __threadfence_system(); }
     }
 }
 
 __global__ void k_erro_limpa() {
     if (threadIdx.x < sizeof(Erro) / sizeof(int)) reinterpret_cast<int*>(&g_erro)[threadIdx.x] = 0;
+    if (threadIdx.x == 0)
+        if (int* f = g_erro_flag) *f = 0;
 }
 
 static hipStream_t g_stream = 0;
@@ -110,12 +116,33 @@ extern "C" {
 
 // ---------------------------------------------------------------------------------------------- state
 // jatai_cuda.cu:1062: reads the record after every launch so far, on any stream, has finished.
+// The flag of each device (host-pinned, allocated at that device's first read and kept to the process's end).
+static volatile int* g_flag_h[64] = {};
 int jt_erro_le(long long* out) {
     hipError_t c = hipDeviceSynchronize();
+    int dev = 0;
+    if (c == hipSuccess) c = hipGetDevice(&dev);
+    if (c != hipSuccess) return -(int)c;
+    volatile int* f = dev >= 0 && dev < 64 ? g_flag_h[dev] : nullptr;
+    if (f != nullptr && *f == 0) {                  // no event since the last clear: the record is all zeros
+        for (int i = 0; i < 6; i++) out[i] = 0;
+        return 0;
+    }
     Erro e;
-    if (c == hipSuccess) c = hipMemcpyFromSymbol(&e, HIP_SYMBOL(g_erro), sizeof(Erro), 0, hipMemcpyDeviceToHost);
+    c = hipMemcpyFromSymbol(&e, HIP_SYMBOL(g_erro), sizeof(Erro), 0, hipMemcpyDeviceToHost);
     if (c != hipSuccess) return -(int)c;
     out[0] = e.n; out[1] = e.codigo; out[2] = e.kid; out[3] = e.idx; out[4] = e.valor; out[5] = e.aux;
+    if (f == nullptr && dev >= 0 && dev < 64) {     // first read on this device (idle: synchronized above)
+        void* h = nullptr;
+        int* hd = nullptr;
+        if (hipHostMalloc(&h, sizeof(int), hipHostMallocCoherent) == hipSuccess) {
+            *static_cast<volatile int*>(h) = e.n > 0 ? 1 : 0;
+            if (hipHostGetDevicePointer(reinterpret_cast<void**>(&hd), h, 0) == hipSuccess &&
+                hipMemcpyToSymbol(HIP_SYMBOL(g_erro_flag), &hd, sizeof(hd)) == hipSuccess)
+                g_flag_h[dev] = static_cast<volatile int*>(h);
+        }
+        (void)hipGetLastError();                    // a failed set-up leaves the copy path, and no error behind
+    }
     return e.n;
 }
 // jatai_cuda.cu:1069: clears the record. A kernel on the library's stream rather than a synchronous copy: the
