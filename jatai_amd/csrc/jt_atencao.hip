@@ -243,12 +243,29 @@ __device__ __forceinline__ void carrega_p(const uint8_t* __restrict__ Pg, uint8_
         *reinterpret_cast<int4*>(&ps[r][col]) = *reinterpret_cast<const int4*>(Pg + (size_t)r * T + col);
     }
 }
+// carrega_p with at most CH chunks per thread (CH blockDim.x >= T T / 16), unrolled: a loop's head would wait for
+// every load issued before it
+template <int CH>
+__device__ __forceinline__ void carrega_p_u(const uint8_t* __restrict__ Pg, uint8_t (*ps)[PLD], int T) {
+    const int porl = T / 16, n = T * porl;
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+        const int c = threadIdx.x + k * blockDim.x;
+        if (c < n) {
+            const int r = c / porl, col = (c - r * porl) * 16;
+            *reinterpret_cast<int4*>(&ps[r][col]) = *reinterpret_cast<const int4*>(Pg + (size_t)r * T + col);
+        }
+    }
+}
 // NS head slices of 4 columns aligned at once (the alignment of alinha4<1>): thread t < T loads token t's 4 bytes
-// and block exponent of every slice before anything waits, and one workgroup reduction gives all NS head maxima
+// and block exponent of every slice before anything waits, and one workgroup reduction gives all NS head maxima.
+// entre() runs between those loads and the reduction: a copy into LDS placed there has its loads in flight with
+// these (before them, its LDS store would wait for its own load before they are issued); the reduction's barrier
+// publishes it.
 struct Fatia4 { const int8_t *m, *E; int ld, col; };
-template <int NS, int NW>
+template <int NS, int NW, class Entre>
 __device__ __forceinline__ void alinha4n(const Fatia4 (&f)[NS], int blk, int b0, int T, int GA, int (&red)[NS][NW], int (*const (&al)[NS])[4],
-                                         int (&eo)[NS]) {
+                                         int (&eo)[NS], Entre&& entre) {
     const int t = threadIdx.x;
     int e[NS], w[NS], mx[NS];
 #pragma unroll
@@ -256,6 +273,7 @@ __device__ __forceinline__ void alinha4n(const Fatia4 (&f)[NS], int blk, int b0,
         e[s] = t < T ? (int)f[s].E[(size_t)(b0 + t) * (f[s].ld / blk) + f[s].col / blk] : SEM_TOPO;
         w[s] = t < T ? *reinterpret_cast<const int*>(f[s].m + (size_t)(b0 + t) * f[s].ld + f[s].col) : 0;
     }
+    entre();
 #pragma unroll
     for (int s = 0; s < NS; s++) mx[s] = g_max<64>(e[s]);
     if ((t & 63) == 0)
@@ -289,8 +307,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l(const int8_t* __restri
     {
         const Fatia4 f[3] = {{qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
         int (*const al[3])[4] = {qa, ka, va};
-        exp_tab_lds(texp);                                           // published by the barriers below
-        alinha4n<3, NW>(f, blk, b0, T, GA, red, al, eo);
+        alinha4n<3, NW>(f, blk, b0, T, GA, red, al, eo, [&] { exp_tab_lds(texp); });
     }
     const int eq = eo[0], ek = eo[1], ev = eo[2];
     __syncthreads();
@@ -388,8 +405,7 @@ __global__ void __launch_bounds__(TMAX * LPR) k_atencao4l_back(const int8_t* __r
     {
         const Fatia4 f[4] = {{gom, goE, D, h * 4}, {qm, qE, ld, h * 4}, {qm, qE, ld, D + h * 4}, {qm, qE, ld, 2 * D + h * 4}};
         int (*const al[4])[4] = {goa, qa, ka, va};
-        carrega_p(Pb, ps, T);
-        alinha4n<4, NW>(f, blk, b0, T, GA, red4, al, eo);
+        alinha4n<4, NW>(f, blk, b0, T, GA, red4, al, eo, [&] { carrega_p_u<(TMAX * TMAX / 16 + TMAX * LPR - 1) / (TMAX * LPR)>(Pb, ps, T); });
     }
     const int ego = eo[0], eq = eo[1], ek = eo[2], ev = eo[3];
     __syncthreads();
