@@ -265,25 +265,31 @@ __global__ void __launch_bounds__(256) k_atf(const int8_t* __restrict__ qm, cons
     // 16 (wv + 4 (2m + kk / 16)) + kk % 16; a pad tile (P = 0 there) reads the wave's first tile of V
     constexpr int NPAR = (NTW + 1) / 2;
     h8_t vb[NPAR][4];
+    // Buffer loads over the head's regions, every one issued (no branch between them): an offset past a region
+    // (0x80000000) returns 0 and touches no memory, for a pair or tile the wave does not use and for V past the
+    // last key tile (P = 0 and v = 0 there)
+    const auto rsV = __builtin_amdgcn_make_buffer_rsrc((void*)(w.vf + (size_t)bh * atw::npv(T) * 2048), (short)0, atw::npv(T) * 4096, 0x00020000);
+    const auto rsK = __builtin_amdgcn_make_buffer_rsrc((void*)(w.km8 + hb * 64), (short)0, T * 64, 0x00020000);
 #pragma unroll
-    for (int m = 0; m < NPAR; m++) {                                 // every load unconditional (no branch between
-        const int mm = 2 * m < nv ? m : 0;                            // them): a pair the wave does not use re-reads
-        const int tv = wv + 4 * (2 * mm + (lg >> 1));                // pair 0's slot; the slot of pair m is 4 m + wv
-        const _Float16* src = w.vf + (((size_t)bh * atw::npv(T) + 4 * mm + wv) * 4 * 64 + lane) * 8;
+    for (int m = 0; m < NPAR; m++) {                                 // the slot of pair m is 4 m + wv
+        const int tv = wv + 4 * (2 * m + (lg >> 1));
+        const int off = 2 * m < nv && tv < nqt ? ((4 * m + wv) * 4 * 64 + lane) * 16 : (int)0x80000000;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            const h8_t x = *reinterpret_cast<const h8_t*>(src + dt * 64 * 8);
-            vb[m][dt] = tv < nqt ? x : h8_t{};                        // past the last tile: P = 0 and v = 0
+            const v4i x = __builtin_amdgcn_raw_buffer_load_b128(rsV, off + dt * 64 * 16, 0, 0);
+            vb[m][dt] = __builtin_bit_cast(h8_t, x);
         }
     }
     // K fragments of this wave's key tiles, loaded at entry as well
     long kb[NTW][2];
     unsigned lkr[NTW];                                                // both L bytes of a key, split where used
 #pragma unroll
-    for (int n = 0; n < NTW; n++) {                                   // unconditional: a tile the wave does not own
-        const size_t j = hb + 16 * (n < nv ? wv + 4 * n : wv) + lr;   // re-reads its first (wv < nqt)
-        le_m8_fragmentos(w.km8 + j * 64, lg, kb[n][0], kb[n][1]);
-        lkr[n] = *reinterpret_cast<const unsigned short*>(w.kl + j * 2);
+    for (int n = 0; n < NTW; n++) {                                   // a tile the wave does not own: 0 (its L
+        const int jl = 16 * (n < nv ? wv + 4 * n : wv) + lr;          // bytes re-read from its first tile)
+        const v4i x = __builtin_amdgcn_raw_buffer_load_b128(rsK, n < nv ? jl * 64 + 16 * lg : (int)0x80000000, 0, 0);
+        kb[n][0] = (long)(unsigned)x[0] | ((long)x[1] << 32);        // le_m8_fragmentos' two fragments
+        kb[n][1] = (long)(unsigned)x[2] | ((long)x[3] << 32);
+        lkr[n] = *reinterpret_cast<const unsigned short*>(w.kl + (hb + jl) * 2);
     }
     // q fragments of the tile's 16 rows, converted here: A row lr = query ia, dimensions 32 c + 8 lg .. + 7
     __shared__ int qL[16][2];
